@@ -1,0 +1,274 @@
+#!/usr/bin/env python3
+"""Benchmark of the hot path: fp32 row log-sum-exp forward + fused backward at
+(B, N) = (512, 128256) on one MI355X (robust forward).
+
+One step = robust forward (lse = onepass_lse_float_robust(x)) followed by the
+fused backward (grad_x = onepass_lse_float_backward(g, x, lse)), through the
+same extension functions the drop-in uses.  Inputs are resident in HBM before
+the timed region; three input/output buffer sets (3 x 525 MB) rotate so the
+working set exceeds twice the 256 MB Infinity Cache and the numbers are HBM
+numbers.  Per-kernel durations come from HIP events recorded on the stream
+the kernels run on.
+
+Prints ONE JSON line on stdout; progress goes to stderr.
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+B, N = 512, 128256
+HBM_PEAK = 8.0e12  # MI355X published HBM3E bandwidth, B/s
+FWD_BYTES = 4 * B * N + 4 * B  # read x, write lse
+BWD_BYTES = 8 * B * N + 8 * B  # read x, g, lse; write grad_x
+METRIC = "fwd+bwd ms/call & HBM GB/s (% peak), fp32 LSE at (512,128256), 1 MI355X"
+ROOT = os.path.dirname(os.path.abspath(__file__))
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_lse_f32_c2.json")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_inputs(torch, dev, seed):
+    """x ~ N(0, 3^2) with 0.1% of entries set to +15, generated on the device."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    x = torch.randn(B, N, device=dev, generator=gen) * 3.0
+    nspk = int(round(0.001 * B * N))
+    idx = torch.randperm(B * N, device=dev, generator=gen)[:nspk]
+    x.view(-1)[idx] = 15.0
+    g = torch.randn(B, device=dev, generator=gen)
+    return x, g
+
+
+def cpu_baseline(max_rows=512):
+    """FuseLSE-CPU forward (sequential expf/log1pf pair chain per row, rows over
+    OpenMP) plus the backward formula, the repo's C port, on the host cores:
+    median of 5 timed calls after 2 warm-ups (the reference's CPU protocol,
+    benchmark.py:36-44).  Also times torch.logsumexp fwd+bwd on CPU and, when
+    it was built, the reference's own AVX2 IntLSE (single thread, 32 rows)."""
+    import numpy as np
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as O
+
+    rng = np.random.default_rng(0)
+    rows = min(B, max_rows)
+    x = (rng.standard_normal((rows, N), dtype=np.float32) * np.float32(3.0))
+    g = rng.standard_normal(rows).astype(np.float32)
+
+    def fb():
+        lse = O.fuselse_cpu_rows(x)
+        O.lse_backward_rows(g, x, lse)
+
+    def med(fn, warm=2, it=5):
+        for _ in range(warm):
+            fn()
+        ts = []
+        for _ in range(it):
+            t0 = time.perf_counter()
+            fn()
+            ts.append((time.perf_counter() - t0) * 1e3)
+        return statistics.median(ts)
+
+    cores = O.omp_threads()
+    port_ms = med(fb) * (B / rows)
+    extra = {}
+    try:
+        torch.set_num_threads(cores)
+        xt = torch.from_numpy(x).requires_grad_(True)
+        gt = torch.from_numpy(g)
+
+        def tfb():
+            xt.grad = None
+            torch.logsumexp(xt, -1).backward(gt)
+
+        extra["torch_cpu_fwd_bwd_ms"] = round(med(tfb, 1, 3) * (B / rows), 3)
+    except Exception as e:  # pragma: no cover - reported, not fatal
+        extra["torch_cpu_error"] = repr(e)
+    if O.ref_available():
+        xs = np.ascontiguousarray(x[:32])
+        extra["intlse_avx2_ref_fwd_ms_1thread_32rows"] = round(med(lambda: O.ref_intlse_cpu_rows(xs, True), 1, 3), 3)
+    cpu = ""
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                cpu = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(port_ms, 3),
+        "unit": "ms/call",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"FuseLSE-CPU fwd + backward formula, C port (oracle/lse_oracle.c), {rows}x{N} fp32 rows "
+                  f"(full workload), OpenMP {cores} threads, median of 5 after 2 warm-ups; cpu={cpu}",
+        **extra,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="also launch one plain 1 GiB device copy (counter calibration runs)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        log("bench.py: this build measures one GPU only (each GPU box has one MI355X); "
+            "run with --gpus 1. Sharding over GPUs is described in DESIGN.md.")
+        sys.exit(2)
+
+    import torch
+
+    sys.path.insert(0, ROOT)
+    import fuselse_amd
+    from fuselse_amd import _lib
+
+    ext = fuselse_amd.ext
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    _lib.load()
+    log(f"device: {torch.cuda.get_device_name(dev)}")
+
+    NBUF = 3
+    xs, gs, gxs, lses = [], [], [], []
+    for i in range(NBUF):
+        x, g = make_inputs(torch, dev, seed=1234 + i)
+        xs.append(x)
+        gs.append(g)
+    torch.cuda.synchronize()
+    log("inputs ready")
+
+    if args.copy_calib:
+        a = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+        b = torch.empty_like(a)
+        b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
+
+    # The backward of step i runs on the previous step's batch, so no kernel
+    # re-reads the buffer the kernel before it just streamed (x is 263 MB, about
+    # the Infinity Cache size); every launch reads HBM.  Work per step is one
+    # forward and one backward over a full (512, 128256) batch.
+    ring = [None] * NBUF  # keeps NBUF grad_x outputs alive so outputs rotate too
+
+    def step(i, lse_prev, evs=None):
+        x = xs[i % NBUF]
+        j = (i - 1) % NBUF
+        if evs is not None:
+            evs[0].record(stream)
+        lse = ext.onepass_lse_float_robust(x)
+        if evs is not None:
+            evs[1].record(stream)
+        gx = ext.onepass_lse_float_backward(gs[j], xs[j], lse_prev)
+        if evs is not None:
+            evs[2].record(stream)
+        ring[i % NBUF] = gx
+        return lse
+
+    stream = torch.cuda.current_stream(dev)
+    lse_prev = ext.onepass_lse_float_robust(xs[NBUF - 1])
+    for i in range(args.warmup):
+        lse_prev = step(i, lse_prev)
+    torch.cuda.synchronize()
+    log("warmup done")
+
+    K = args.steps
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(K):
+        lse_prev = step(i, lse_prev, evs[i])
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    total_ms = evs[0][0].elapsed_time(evs[-1][2])
+    fwd_ms = statistics.fmean(e[0].elapsed_time(e[1]) for e in evs)
+    bwd_ms = statistics.fmean(e[1].elapsed_time(e[2]) for e in evs)
+    ms_step = total_ms / K
+    log(f"timed {K} steps: {ms_step * 1e3:.1f} us/step (wall {wall_ms / K * 1e3:.1f} us), "
+        f"fwd {fwd_ms * 1e3:.1f} us, bwd {bwd_ms * 1e3:.1f} us")
+
+    # same-batch variant (backward right after its own forward), for the record
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev[0].record(stream)
+    for i in range(K):
+        x = xs[i % NBUF]
+        lse = ext.onepass_lse_float_robust(x)
+        ring[i % NBUF] = ext.onepass_lse_float_backward(gs[i % NBUF], x, lse)
+    ev[1].record(stream)
+    torch.cuda.synchronize()
+    same_batch_ms = ev[0].elapsed_time(ev[1]) / K
+
+    # plain (non-robust) forward on the same buffers, for the record
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev[0].record(stream)
+    for i in range(K):
+        ext.onepass_lse_float(xs[i % NBUF])
+    ev[1].record(stream)
+    torch.cuda.synchronize()
+    fwd_plain_ms = ev[0].elapsed_time(ev[1]) / K
+
+    gbps = (FWD_BYTES + BWD_BYTES) / (ms_step * 1e-3) / 1e9
+    fwd_gbps = FWD_BYTES / (fwd_ms * 1e-3) / 1e9
+    bwd_gbps = BWD_BYTES / (bwd_ms * 1e-3) / 1e9
+    traffic = None
+    try:
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("bwd_hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        pass
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        cpu = cpu_baseline()
+
+    out = {
+        "metric": METRIC,
+        "value": round(ms_step, 5),
+        "unit": "ms/call",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: x~N(0,3^2) fp32 with 0.1% entries +15, g~N(0,1), seeded on device; 3 rotating buffers",
+        "config": {"workload": "fp32 row LSE robust fwd + fused bwd, (B,N)=(512,128256)", "B": B, "N": N,
+                   "robust": True},
+        "hbm_gbps": round(gbps, 1),
+        "pct_hbm_peak": round(100 * gbps * 1e9 / HBM_PEAK, 2),
+        "same_batch_step_us": round(same_batch_ms * 1e3, 2),
+        "fwd": {"us": round(fwd_ms * 1e3, 2), "gbps": round(fwd_gbps, 1),
+                "pct_peak": round(100 * fwd_gbps * 1e9 / HBM_PEAK, 2), "bytes": FWD_BYTES,
+                "plain_us": round(fwd_plain_ms * 1e3, 2)},
+        "bwd": {"us": round(bwd_ms * 1e3, 2), "gbps": round(bwd_gbps, 1),
+                "pct_peak": round(100 * bwd_gbps * 1e9 / HBM_PEAK, 2), "bytes": BWD_BYTES},
+        "roofline": {"bound": "hbm", "kernel": "lse_bwd_row_chunks<4> (fused backward)",
+                     "achieved": round(bwd_gbps, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": round(bwd_gbps * 1e9 / HBM_PEAK, 4), "traffic": traffic},
+        "roofline_fwd": {"bound": "hbm", "kernel": "lse_fwd_block_rows<float,robust,1024,4>",
+                         "achieved": round(fwd_gbps, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                         "frac": round(fwd_gbps * 1e9 / HBM_PEAK, 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

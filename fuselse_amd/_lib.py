@@ -1,0 +1,77 @@
+"""ctypes binding of the gfx950 C-ABI library (``libfuselse_amd.so``).
+
+The library is loaded after ``import torch`` so it binds to the HIP runtime
+torch already loaded (same soname), which makes torch's streams and device
+pointers valid inside it.  A missing or unloadable library raises loudly:
+there is no CPU fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "libfuselse_amd.so")
+HEADER_PATH = os.path.join(os.path.dirname(PKG_DIR), "include", "fuselse_amd.h")
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+
+# name -> (restype, argtypes); must match include/fuselse_amd.h
+SIGNATURES = {
+    "fl_last_error": (ctypes.c_char_p, []),
+    "fl_abi_version": (_int, []),
+    "fl_lse_fwd_f32": (_int, [_vp, _vp, _i64, _i64, _int, _vp]),
+    "fl_lse_bwd_f32": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "fl_lse_fwd_f16": (_int, [_vp, _vp, _i64, _i64, _int, _vp]),
+    "fl_lse_fwd_bf16": (_int, [_vp, _vp, _i64, _i64, _int, _vp]),
+}
+
+_lib = None
+
+
+class NativeLibraryMissing(RuntimeError):
+    pass
+
+
+def header_symbols(path: str = HEADER_PATH):
+    """Function names declared in the C header."""
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fl_[a-z0-9_]+)\s*\(", text)))
+
+
+def load():
+    """Load and type the library once; raises NativeLibraryMissing if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    import torch  # noqa: F401  (binds the HIP runtime torch ships before ours)
+
+    if not os.path.exists(LIB_PATH):
+        raise NativeLibraryMissing(
+            f"fuselse_amd: native library {LIB_PATH} is not built; run "
+            "`python -c 'import __graft_entry__ as g; g.build()'` (no CPU fallback exists)")
+    try:
+        lib = ctypes.CDLL(LIB_PATH)
+    except OSError as e:
+        raise NativeLibraryMissing(f"fuselse_amd: cannot load {LIB_PATH}: {e}") from e
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def call(name: str, *args) -> None:
+    """Call entry point `name`; a nonzero status raises RuntimeError with the
+    library's message."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.fl_last_error().decode(errors="replace")
+        raise RuntimeError(msg or f"{name} failed with status {rc}")

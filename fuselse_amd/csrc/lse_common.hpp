@@ -1,0 +1,176 @@
+// Shared device helpers for the gfx950 log-sum-exp kernels: wave64 lane
+// exchanges, the online (max, scaled-sum) state used by the float paths, and
+// 16-byte vector loads.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fl {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kInf = __builtin_huge_valf();
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float flog2(float x) { return __builtin_amdgcn_logf(x); }
+
+// ---------------------------------------------------------------------------
+// Lane exchanges. exact_xor<K> returns the value held by lane (lane ^ K); for
+// K < 32 it stays inside each 32-lane half (ds_swizzle bit-mask mode), which
+// is the exchange pattern of a warp-32 xor butterfly.
+// ---------------------------------------------------------------------------
+template <int K>
+__device__ __forceinline__ int exact_xor(int v) {
+    static_assert(K == 1 || K == 2 || K == 4 || K == 8 || K == 16 || K == 32, "xor distance");
+    if constexpr (K == 32) {
+        return __shfl_xor(v, 32, 64);
+    } else {
+        return __builtin_amdgcn_ds_swizzle(v, 0x1F | (K << 10));
+    }
+}
+template <int K>
+__device__ __forceinline__ float exact_xor(float v) {
+    return __builtin_bit_cast(float, exact_xor<K>(__builtin_bit_cast(int, v)));
+}
+
+// Partner exchange for commutative reductions whose operands are already
+// uniform within aligned groups of K lanes: DPP moves for K <= 8 (quad
+// permutes, then half-row and row mirrors, which pair the same groups as an
+// xor once those groups are uniform), a swizzle for 16, a lane shuffle for 32.
+template <int K>
+__device__ __forceinline__ float reduce_partner(float v) {
+    int iv = __builtin_bit_cast(int, v);
+    int r;
+    if constexpr (K == 1) r = __builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xF, 0xF, false);       // quad_perm 1,0,3,2
+    else if constexpr (K == 2) r = __builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, false);  // quad_perm 2,3,0,1
+    else if constexpr (K == 4) r = __builtin_amdgcn_update_dpp(0, iv, 0x141, 0xF, 0xF, false); // row_half_mirror
+    else if constexpr (K == 8) r = __builtin_amdgcn_update_dpp(0, iv, 0x140, 0xF, 0xF, false); // row_mirror
+    else r = exact_xor<K>(iv);
+    return __builtin_bit_cast(float, r);
+}
+
+// ---------------------------------------------------------------------------
+// Online log-sum-exp state: m is the running maximum (natural units, NaN never
+// enters it because fmaxf drops NaN), s = sum exp(x - base(m)) where base(m)
+// is m when finite and 0 when m is +-inf.  With that base, a row of all -inf
+// ends at (m=-inf, s=0) -> -inf, any +inf drives s to +inf -> +inf, and a NaN
+// element makes s NaN -> NaN: torch.logsumexp's special values, which the
+// reference's robust pair reproduces (fused_fp32_kernel.cu:34-40).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float lse_base(float m) { return __builtin_isfinite(m) ? m : 0.0f; }
+
+// Rescale factor that moves a partial sum from base(mi) to base(m); an empty
+// partial (mi = -inf) contributes nothing (0 * NaN still propagates NaN).
+__device__ __forceinline__ float lse_rescale(float mi, float m) {
+    return mi == -kInf ? 0.0f : fexp2((lse_base(mi) - lse_base(m)) * kLog2e);
+}
+
+__device__ __forceinline__ void lse_merge(float& m, float& s, float m2, float s2) {
+    float mn = fmaxf(m, m2);
+    s = s * lse_rescale(m, mn) + s2 * lse_rescale(m2, mn);
+    m = mn;
+}
+
+// Fold K new values into (m, s) with one rescale. ROBUST keeps the base finite
+// so non-finite inputs follow the rules above; the plain variant assumes
+// finite inputs (as the reference's non-robust kernel does).
+template <bool ROBUST, int K>
+__device__ __forceinline__ void lse_fold(float& m, float& s, const float (&v)[K]) {
+    float cm = v[0];
+#pragma unroll
+    for (int k = 1; k < K; ++k) cm = fmaxf(cm, v[k]);
+    float mn = fmaxf(m, cm);
+    float nb;
+    if constexpr (ROBUST) {
+        s *= lse_rescale(m, mn);
+        nb = -lse_base(mn) * kLog2e;
+    } else {
+        s *= fexp2((m - mn) * kLog2e);
+        nb = -mn * kLog2e;
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < K; ++k) acc += fexp2(__builtin_fmaf(v[k], kLog2e, nb));
+    s += acc;
+    m = mn;
+}
+
+template <bool ROBUST>
+__device__ __forceinline__ float lse_finish(float m, float s) {
+    float b = ROBUST ? lse_base(m) : m;
+    return b + flog2(s) * kLn2;
+}
+
+// Merge (m, s) across aligned groups of W lanes; every lane of a group ends
+// with the group result.
+template <int W>
+__device__ __forceinline__ void group_merge(float& m, float& s) {
+    if constexpr (W >= 2) { lse_merge(m, s, reduce_partner<1>(m), reduce_partner<1>(s)); }
+    if constexpr (W >= 4) { lse_merge(m, s, reduce_partner<2>(m), reduce_partner<2>(s)); }
+    if constexpr (W >= 8) { lse_merge(m, s, reduce_partner<4>(m), reduce_partner<4>(s)); }
+    if constexpr (W >= 16) { lse_merge(m, s, reduce_partner<8>(m), reduce_partner<8>(s)); }
+    if constexpr (W >= 32) { lse_merge(m, s, reduce_partner<16>(m), reduce_partner<16>(s)); }
+    if constexpr (W >= 64) { lse_merge(m, s, reduce_partner<32>(m), reduce_partner<32>(s)); }
+}
+
+// ---------------------------------------------------------------------------
+// Element types: 16-byte vector loads widened to fp32.
+// ---------------------------------------------------------------------------
+struct bf16_t { uint16_t bits; };
+
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+    static constexpr int kVec = 4;
+    __device__ static __forceinline__ float scalar(const float* p) { return *p; }
+    __device__ static __forceinline__ void vec(const float* p, float (&o)[4]) {
+        f32x4 v = *reinterpret_cast<const f32x4*>(p);
+        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+    }
+};
+template <> struct Elem<_Float16> {
+    static constexpr int kVec = 8;
+    __device__ static __forceinline__ float scalar(const _Float16* p) { return (float)*p; }
+    __device__ static __forceinline__ void vec(const _Float16* p, float (&o)[8]) {
+        f16x8 v = *reinterpret_cast<const f16x8*>(p);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) o[k] = (float)v[k];
+    }
+};
+template <> struct Elem<bf16_t> {
+    static constexpr int kVec = 8;
+    __device__ static __forceinline__ float scalar(const bf16_t* p) {
+        return __builtin_bit_cast(float, (uint32_t)p->bits << 16);
+    }
+    __device__ static __forceinline__ void vec(const bf16_t* p, float (&o)[8]) {
+        u32x4 v = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            o[2 * k] = __builtin_bit_cast(float, v[k] << 16);
+            o[2 * k + 1] = __builtin_bit_cast(float, v[k] & 0xFFFF0000u);
+        }
+    }
+};
+
+// Split of a row into a scalar head (up to the first 16-byte boundary), a
+// body of 16-byte vectors and a scalar tail.
+struct RowSplit {
+    int64_t head, nvec, tail;
+};
+template <typename T>
+__device__ __forceinline__ RowSplit split_row(const T* row, int64_t n) {
+    constexpr int64_t E = (int64_t)sizeof(T);
+    uint32_t mis = (uint32_t)(reinterpret_cast<uintptr_t>(row) & 15u);
+    int64_t head = mis ? (int64_t)((16u - mis) / E) : 0;
+    if (head > n) head = n;
+    int64_t nvec = (n - head) / Elem<T>::kVec;
+    return {head, nvec, n - head - nvec * Elem<T>::kVec};
+}
+
+}  // namespace fl

@@ -1,0 +1,312 @@
+// Float log-sum-exp kernels for gfx950: fp32 / fp16 / bf16 forward (plain and
+// robust) and the fused fp32 backward.
+//
+// Forward: a single pass over HBM.  Each lane keeps an online (max, scaled
+// sum) pair and folds one 16-byte vector group at a time with a single
+// rescale, so the steady state costs one v_exp_f32 per element.  Lanes merge
+// through DPP / swizzle exchanges and waves through LDS.  Three geometries:
+//   * group rows  : LPR lanes per row (4..64), 64/LPR rows per wave, for rows
+//                   of up to a few thousand vectors;
+//   * block rows  : one 256..1024-thread block per row for long rows;
+// Backward: grad * exp2((x - lse) * log2 e), 16-byte loads and stores, with
+// grad[r] and lse[r] wave-uniform.
+#include <stdint.h>
+
+#include "../../include/fuselse_amd.h"
+#include "fl_status.hpp"
+#include "lse_common.hpp"
+
+namespace fl {
+
+template <typename T, bool ROBUST>
+__device__ __forceinline__ void fold_scalar(float& m, float& s, const T* p) {
+    float v[1] = {Elem<T>::scalar(p)};
+    lse_fold<ROBUST, 1>(m, s, v);
+}
+
+// Folds the vectors body[i], body[i + STRIDE], ... (i < nvec) into (m, s),
+// U vectors per rescale.
+template <typename T, bool ROBUST, int STRIDE, int U>
+__device__ __forceinline__ void fold_body(float& m, float& s, const T* body, int64_t i, int64_t nvec) {
+    constexpr int VE = Elem<T>::kVec;
+    for (; i + (int64_t)(U - 1) * STRIDE < nvec; i += (int64_t)U * STRIDE) {
+        float v[U * VE];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float t[VE];
+            Elem<T>::vec(body + (i + (int64_t)u * STRIDE) * VE, t);
+#pragma unroll
+            for (int k = 0; k < VE; ++k) v[u * VE + k] = t[k];
+        }
+        lse_fold<ROBUST, U * VE>(m, s, v);
+    }
+    for (; i < nvec; i += STRIDE) {
+        float v[VE];
+        Elem<T>::vec(body + i * VE, v);
+        lse_fold<ROBUST, VE>(m, s, v);
+    }
+}
+
+// One block per row (grid-stride over rows).
+template <typename T, bool ROBUST, int THREADS, int U>
+__global__ __launch_bounds__(THREADS) void lse_fwd_block_rows(const T* __restrict__ x, float* __restrict__ out,
+                                                              int64_t B, int64_t N) {
+    constexpr int VE = Elem<T>::kVec;
+    constexpr int WAVES = THREADS / 64;
+    __shared__ float sh_m[WAVES], sh_s[WAVES];
+    const int tid = threadIdx.x;
+    for (int64_t row = blockIdx.x; row < B; row += gridDim.x) {
+        const T* p = x + row * N;
+        const RowSplit sp = split_row(p, N);
+        float m = -kInf, s = 0.0f;
+        if (tid < sp.head) fold_scalar<T, ROBUST>(m, s, p + tid);
+        if (tid < sp.tail) fold_scalar<T, ROBUST>(m, s, p + sp.head + sp.nvec * VE + tid);
+        fold_body<T, ROBUST, THREADS, U>(m, s, p + sp.head, tid, sp.nvec);
+        group_merge<64>(m, s);
+        if ((tid & 63) == 0) {
+            sh_m[tid >> 6] = m;
+            sh_s[tid >> 6] = s;
+        }
+        __syncthreads();
+        if (tid < 64) {
+            m = tid < WAVES ? sh_m[tid] : -kInf;
+            s = tid < WAVES ? sh_s[tid] : 0.0f;
+            group_merge<WAVES>(m, s);
+            if (tid == 0) out[row] = lse_finish<ROBUST>(m, s);
+        }
+        __syncthreads();
+    }
+}
+
+// LPR lanes per row, 64/LPR rows per wave, WAVES waves per block
+// (grid-stride over row groups).
+template <typename T, bool ROBUST, int LPR, int U>
+__global__ __launch_bounds__(256) void lse_fwd_group_rows(const T* __restrict__ x, float* __restrict__ out,
+                                                          int64_t B, int64_t N) {
+    constexpr int VE = Elem<T>::kVec;
+    constexpr int RPW = 64 / LPR;
+    constexpr int WAVES = 4;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int g = lane / LPR;
+    const int j = lane % LPR;
+    const int64_t step = (int64_t)gridDim.x * WAVES * RPW;
+    for (int64_t base = ((int64_t)blockIdx.x * WAVES + wave) * RPW; base < B; base += step) {
+        const int64_t row = base + g;
+        float m = -kInf, s = 0.0f;
+        if (row < B) {
+            const T* p = x + row * N;
+            const RowSplit sp = split_row(p, N);
+            for (int64_t h = j; h < sp.head; h += LPR) fold_scalar<T, ROBUST>(m, s, p + h);
+            const T* tail = p + sp.head + sp.nvec * VE;
+            for (int64_t t = j; t < sp.tail; t += LPR) fold_scalar<T, ROBUST>(m, s, tail + t);
+            fold_body<T, ROBUST, LPR, U>(m, s, p + sp.head, j, sp.nvec);
+        }
+        group_merge<LPR>(m, s);
+        if (j == 0 && row < B) out[row] = lse_finish<ROBUST>(m, s);
+    }
+}
+
+static int64_t pow2_ceil(int64_t v) {
+    int64_t p = 1;
+    while (p < v) p <<= 1;
+    return p;
+}
+
+template <typename T, bool ROBUST>
+static void launch_fwd(const T* x, float* out, int64_t B, int64_t N, hipStream_t st) {
+    constexpr int VE = Elem<T>::kVec;
+    const int64_t vecs = (N + VE - 1) / VE;
+    if (vecs > 4096) {
+        const int64_t grid = B;
+        if (vecs > 16384)
+            lse_fwd_block_rows<T, ROBUST, 1024, 4><<<dim3((unsigned)grid), dim3(1024), 0, st>>>(x, out, B, N);
+        else
+            lse_fwd_block_rows<T, ROBUST, 512, 4><<<dim3((unsigned)grid), dim3(512), 0, st>>>(x, out, B, N);
+        return;
+    }
+    int64_t lpr = pow2_ceil((vecs + 3) / 4);
+    if (lpr < 4) lpr = 4;
+    if (lpr > 64) lpr = 64;
+    const int64_t rows_per_block = 4 * (64 / lpr);
+    int64_t grid = (B + rows_per_block - 1) / rows_per_block;
+    if (grid > (int64_t)1 << 30) grid = (int64_t)1 << 30;
+    const dim3 g((unsigned)grid), blk(256);
+    switch (lpr) {
+    case 4: lse_fwd_group_rows<T, ROBUST, 4, 2><<<g, blk, 0, st>>>(x, out, B, N); break;
+    case 8: lse_fwd_group_rows<T, ROBUST, 8, 2><<<g, blk, 0, st>>>(x, out, B, N); break;
+    case 16: lse_fwd_group_rows<T, ROBUST, 16, 2><<<g, blk, 0, st>>>(x, out, B, N); break;
+    case 32: lse_fwd_group_rows<T, ROBUST, 32, 2><<<g, blk, 0, st>>>(x, out, B, N); break;
+    default: lse_fwd_group_rows<T, ROBUST, 64, 4><<<g, blk, 0, st>>>(x, out, B, N); break;
+    }
+}
+
+template <typename T>
+static int fwd_entry(const char* name, const T* x, float* out, int64_t B, int64_t N, int robust, void* stream) {
+    FL_CHECK(B >= 0 && N >= 0, "%s: negative shape (B=%lld, N=%lld)", name, (long long)B, (long long)N);
+    if (B == 0) return ok();
+    FL_CHECK(out != nullptr, "%s: out is NULL", name);
+    FL_CHECK(x != nullptr || N == 0, "%s: x is NULL", name);
+    FL_CHECK((reinterpret_cast<uintptr_t>(x) % sizeof(T)) == 0, "%s: x is not element-aligned", name);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (robust)
+        launch_fwd<T, true>(x, out, B, N, st);
+    else
+        launch_fwd<T, false>(x, out, B, N, st);
+    return launch_status(name);
+}
+
+// ---------------------------------------------------------------------------
+// Backward
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bwd_elem(float gv, float lse, float xv) {
+    return gv * fexp2((xv - lse) * kLog2e);
+}
+
+// Long rows: grid = B * chunks_per_row blocks of 256 threads; a block covers
+// 256*U consecutive vectors of one row.  x and grad_x share their alignment.
+template <int U>
+__global__ __launch_bounds__(256) void lse_bwd_row_chunks(const float* __restrict__ g, const float* __restrict__ x,
+                                                          const float* __restrict__ lse, float* __restrict__ gx,
+                                                          int64_t N, int64_t chunks_per_row) {
+    const int64_t blk = blockIdx.x;
+    const int64_t row = blk / chunks_per_row;
+    const int64_t chunk = blk - row * chunks_per_row;
+    const int tid = threadIdx.x;
+    const float* xr = x + row * N;
+    float* gr = gx + row * N;
+    const RowSplit sp = split_row(xr, N);
+    const float gv = g[row];
+    const float lv = lse[row];
+    if (chunk == 0) {
+        if (tid < sp.head) gr[tid] = bwd_elem(gv, lv, xr[tid]);
+        const int64_t t0 = sp.head + sp.nvec * 4;
+        if (tid < sp.tail) gr[t0 + tid] = bwd_elem(gv, lv, xr[t0 + tid]);
+    }
+    const f32x4* xb = reinterpret_cast<const f32x4*>(xr + sp.head);
+    f32x4* gb = reinterpret_cast<f32x4*>(gr + sp.head);
+    const int64_t i0 = chunk * 256 * U + tid;
+    f32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int64_t i = i0 + (int64_t)u * 256;
+        if (i < sp.nvec) v[u] = xb[i];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int64_t i = i0 + (int64_t)u * 256;
+        if (i < sp.nvec) {
+            f32x4 r;
+            r.x = bwd_elem(gv, lv, v[u].x);
+            r.y = bwd_elem(gv, lv, v[u].y);
+            r.z = bwd_elem(gv, lv, v[u].z);
+            r.w = bwd_elem(gv, lv, v[u].w);
+            gb[i] = r;
+        }
+    }
+}
+
+// Short rows: LPR lanes per row, 256/LPR rows per block, grid-stride.
+template <int LPR>
+__global__ __launch_bounds__(256) void lse_bwd_group_rows(const float* __restrict__ g, const float* __restrict__ x,
+                                                          const float* __restrict__ lse, float* __restrict__ gx,
+                                                          int64_t B, int64_t N) {
+    constexpr int RPB = 256 / LPR;
+    const int gi = threadIdx.x / LPR;
+    const int j = threadIdx.x % LPR;
+    for (int64_t row = (int64_t)blockIdx.x * RPB + gi; row < B; row += (int64_t)gridDim.x * RPB) {
+        const float* xr = x + row * N;
+        float* gr = gx + row * N;
+        const RowSplit sp = split_row(xr, N);
+        const float gv = g[row];
+        const float lv = lse[row];
+        for (int64_t h = j; h < sp.head; h += LPR) gr[h] = bwd_elem(gv, lv, xr[h]);
+        const int64_t t0 = sp.head + sp.nvec * 4;
+        for (int64_t t = j; t < sp.tail; t += LPR) gr[t0 + t] = bwd_elem(gv, lv, xr[t0 + t]);
+        const f32x4* xb = reinterpret_cast<const f32x4*>(xr + sp.head);
+        f32x4* gb = reinterpret_cast<f32x4*>(gr + sp.head);
+        for (int64_t i = j; i < sp.nvec; i += LPR) {
+            f32x4 v = xb[i], r;
+            r.x = bwd_elem(gv, lv, v.x);
+            r.y = bwd_elem(gv, lv, v.y);
+            r.z = bwd_elem(gv, lv, v.z);
+            r.w = bwd_elem(gv, lv, v.w);
+            gb[i] = r;
+        }
+    }
+}
+
+// Fallback when x and grad_x differ in 16-byte alignment: scalar grid-stride.
+__global__ __launch_bounds__(256) void lse_bwd_scalar(const float* __restrict__ g, const float* __restrict__ x,
+                                                      const float* __restrict__ lse, float* __restrict__ gx,
+                                                      int64_t B, int64_t N) {
+    for (int64_t row = blockIdx.y; row < B; row += gridDim.y) {
+        const float gv = g[row];
+        const float lv = lse[row];
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < N; i += (int64_t)gridDim.x * 256)
+            gx[row * N + i] = bwd_elem(gv, lv, x[row * N + i]);
+    }
+}
+
+static void launch_bwd(const float* g, const float* x, const float* lse, float* gx, int64_t B, int64_t N,
+                       hipStream_t st) {
+    const bool same_align = ((reinterpret_cast<uintptr_t>(x) ^ reinterpret_cast<uintptr_t>(gx)) & 15u) == 0;
+    if (!same_align) {
+        int64_t gxdim = (N + 255) / 256;
+        if (gxdim > 1024) gxdim = 1024;
+        int64_t gydim = B < 65535 ? B : 65535;
+        lse_bwd_scalar<<<dim3((unsigned)gxdim, (unsigned)gydim), dim3(256), 0, st>>>(g, x, lse, gx, B, N);
+        return;
+    }
+    const int64_t vecs = N / 4 + 1;
+    if (vecs >= 1024) {
+        constexpr int U = 4;
+        const int64_t cpr = (vecs + 256 * U - 1) / (256 * U);
+        lse_bwd_row_chunks<U><<<dim3((unsigned)(B * cpr)), dim3(256), 0, st>>>(g, x, lse, gx, N, cpr);
+        return;
+    }
+    int64_t lpr = pow2_ceil((vecs + 3) / 4);
+    if (lpr < 4) lpr = 4;
+    const int64_t rpb = 256 / lpr;
+    int64_t grid = (B + rpb - 1) / rpb;
+    if (grid > (int64_t)1 << 30) grid = (int64_t)1 << 30;
+    const dim3 gd((unsigned)grid), blk(256);
+    switch (lpr) {
+    case 4: lse_bwd_group_rows<4><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N); break;
+    case 8: lse_bwd_group_rows<8><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N); break;
+    case 16: lse_bwd_group_rows<16><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N); break;
+    case 32: lse_bwd_group_rows<32><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N); break;
+    case 64: lse_bwd_group_rows<64><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N); break;
+    case 128: lse_bwd_group_rows<128><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N); break;
+    default: lse_bwd_group_rows<256><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N); break;
+    }
+}
+
+}  // namespace fl
+
+using namespace fl;
+
+extern "C" int fl_lse_fwd_f32(const float* x, float* out, int64_t B, int64_t N, int robust, void* stream) {
+    return fwd_entry<float>("fl_lse_fwd_f32", x, out, B, N, robust, stream);
+}
+
+extern "C" int fl_lse_fwd_f16(const void* x, float* out, int64_t B, int64_t N, int robust, void* stream) {
+    return fwd_entry<_Float16>("fl_lse_fwd_f16", static_cast<const _Float16*>(x), out, B, N, robust, stream);
+}
+
+extern "C" int fl_lse_fwd_bf16(const void* x, float* out, int64_t B, int64_t N, int robust, void* stream) {
+    return fwd_entry<bf16_t>("fl_lse_fwd_bf16", static_cast<const bf16_t*>(x), out, B, N, robust, stream);
+}
+
+extern "C" int fl_lse_bwd_f32(const float* grad, const float* x, const float* lse, float* grad_x, int64_t B,
+                              int64_t N, void* stream) {
+    const char* name = "fl_lse_bwd_f32";
+    FL_CHECK(B >= 0 && N >= 0, "%s: negative shape (B=%lld, N=%lld)", name, (long long)B, (long long)N);
+    if (B == 0 || N == 0) return ok();
+    FL_CHECK(grad && x && lse && grad_x, "%s: NULL pointer argument", name);
+    FL_CHECK((reinterpret_cast<uintptr_t>(x) & 3u) == 0 && (reinterpret_cast<uintptr_t>(grad_x) & 3u) == 0,
+             "%s: x / grad_x are not 4-byte aligned", name);
+    FL_CHECK(B * ((N / 4 + 1 + 1023) / 1024) < ((int64_t)1 << 32), "%s: B*N too large for the grid", name);
+    launch_bwd(grad, x, lse, grad_x, B, N, reinterpret_cast<hipStream_t>(stream));
+    return launch_status(name);
+}

@@ -1,0 +1,65 @@
+/*
+ * fuselse_amd C ABI: row-wise log-sum-exp kernels for AMD Instinct MI355X
+ * (gfx950).
+ *
+ * Conventions shared by every entry point:
+ *   - All pointers are device pointers the caller allocated (torch or
+ *     hipMalloc); the library allocates nothing.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *     Work is enqueued asynchronously on it on the current HIP device; the
+ *     caller keeps the buffers alive until the stream has run the work.
+ *   - Matrices are row-major and contiguous: element (r, i) of a (B, N)
+ *     matrix lives at base + r*N + i.  The reduction runs over the last axis.
+ *   - Return value: FL_OK (0) on success; FL_EINVAL (1) for a rejected
+ *     argument, FL_ELAUNCH (2) when the kernel launch failed, FL_ERANGE (3) for
+ *     a size beyond what the kernel indexes.  fl_last_error() then describes
+ *     the failure (per calling thread).
+ *   - B == 0 (or an empty edge list) returns FL_OK without launching.
+ */
+#ifndef FUSELSE_AMD_H
+#define FUSELSE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FL_ABI_VERSION 1
+
+/* Message for the last failing call on this thread ("" after a success). */
+const char* fl_last_error(void);
+/* FL_ABI_VERSION the library was built with. */
+int fl_abi_version(void);
+
+/* ---------------------------------------------------------------------------
+ * fp32 forward: out[r] = log(sum_i exp(x[r, i])), out is fp32 [B].
+ * robust != 0 gives torch.logsumexp's special values (all -inf -> -inf, any
+ * +inf -> +inf, any NaN -> NaN); robust == 0 assumes finite inputs.
+ * Replaces onepass_lse_float / onepass_lse_float_robust
+ * (fuselse/gpu/fused_fp32_kernel.cu:154-173, 175-194; kernel :50-133).
+ * ------------------------------------------------------------------------- */
+int fl_lse_fwd_f32(const float* x, float* out, int64_t B, int64_t N, int robust, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * fp32 backward: grad_x[r, i] = grad[r] * exp(x[r, i] - lse[r]).
+ * Replaces onepass_lse_float_backward (fused_fp32_kernel.cu:196-252; kernel
+ * :135-150).  grad and lse are fp32 [B], x and grad_x fp32 [B, N].
+ * ------------------------------------------------------------------------- */
+int fl_lse_bwd_f32(const float* grad, const float* x, const float* lse, float* grad_x, int64_t B,
+                   int64_t N, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Half-precision inputs with fp32 accumulation and fp32 output [B].
+ * fl_lse_fwd_f16 replaces batched_logsumexp_fp16 (fuselse/gpu/fused_fp16_kernel.cu:
+ * 112-132; kernel :25-110).  fl_lse_fwd_bf16 is the bf16 twin, which the
+ * reference does not have.  x points to IEEE binary16 / bfloat16 [B, N].
+ * ------------------------------------------------------------------------- */
+int fl_lse_fwd_f16(const void* x, float* out, int64_t B, int64_t N, int robust, void* stream);
+int fl_lse_fwd_bf16(const void* x, float* out, int64_t B, int64_t N, int robust, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FUSELSE_AMD_H */

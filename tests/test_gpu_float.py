@@ -1,0 +1,232 @@
+"""GPU parity of the float kernels (fp32 forward, robust forward, fused
+backward, fp16/bf16 forward) against the fp64 oracle and torch's fp32
+logsumexp, through the C ABI via fuselse_amd.ext.
+
+Tolerances (stated by the north star): fp32 within 1e-5 relative, fp16/bf16
+inputs within 1e-3 relative of the fp32 LSE of the same (rounded) inputs.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+RTOL32 = 1e-5
+RTOL16 = 1e-3
+
+
+def _ext():
+    import fuselse_amd
+
+    return fuselse_amd.ext
+
+
+def _offset_view(x_cpu: torch.Tensor, dev, elem_offset: int) -> torch.Tensor:
+    """Contiguous (B, N) device tensor whose data pointer sits elem_offset
+    elements past a 256-byte boundary (exercises the unaligned head path)."""
+    B, N = x_cpu.shape
+    buf = torch.empty(B * N + elem_offset + 8, dtype=x_cpu.dtype, device=dev)
+    v = buf[elem_offset:elem_offset + B * N].view(B, N)
+    v.copy_(x_cpu.to(dev))
+    assert v.is_contiguous()
+    return v
+
+
+def _close(got, want, rtol, atol=0.0):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    np.testing.assert_allclose(got, want, rtol=rtol, atol=atol, equal_nan=True)
+
+
+SHAPES = [(1, 2), (5, 3), (32, 256), (200, 1000), (7, 1023), (33, 4097), (16, 16384), (9, 16385),
+          (3, 50257), (4, 128256), (2, 300001)]
+
+
+@pytest.mark.parametrize("B,N", SHAPES)
+@pytest.mark.parametrize("robust", [False, True])
+def test_fwd_f32_matches_fp64(cuda, B, N, robust):
+    print(f"case fwd_f32 B={B} N={N} robust={robust}", flush=True)
+    rng = np.random.default_rng(B * 1000 + N)
+    x = (rng.standard_normal((B, N)) * 3).astype(np.float32)
+    ext = _ext()
+    fn = ext.onepass_lse_float_robust if robust else ext.onepass_lse_float
+    got = fn(torch.from_numpy(x).to(cuda)).cpu().numpy()
+    want = O.lse_fp64(x)
+    _close(got, want, RTOL32, atol=1e-6)
+    # torch fp32 on the same device agrees to the same tolerance
+    tor = torch.logsumexp(torch.from_numpy(x).to(cuda), dim=-1).cpu().numpy()
+    _close(got, tor, RTOL32, atol=2e-6)
+
+
+@pytest.mark.parametrize("elem_offset", [1, 2, 3])
+@pytest.mark.parametrize("B,N", [(6, 7), (5, 1001), (3, 20000)])
+def test_fwd_f32_unaligned_rows(cuda, B, N, elem_offset):
+    print(f"case fwd_f32_unaligned B={B} N={N} off={elem_offset}", flush=True)
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((B, N)) * 2).astype(np.float32)
+    v = _offset_view(torch.from_numpy(x), cuda, elem_offset)
+    got = _ext().onepass_lse_float_robust(v).cpu().numpy()
+    _close(got, O.lse_fp64(x), RTOL32, atol=1e-6)
+
+
+def test_fwd_f32_c2_full_size(cuda):
+    """BASELINE C2 forward at (512, 128256): N(0, 3^2) with 0.1% +15 spikes."""
+    print("case fwd_f32 C2 512x128256", flush=True)
+    x = O.make_c2_input(512, 128256, seed=0)
+    xd = torch.from_numpy(x).to(cuda)
+    got = _ext().onepass_lse_float_robust(xd).cpu().numpy()
+    _close(got, O.lse_fp64(x), RTOL32)
+    got2 = _ext().onepass_lse_float(xd).cpu().numpy()
+    _close(got2, O.lse_fp64(x), RTOL32)
+
+
+def test_fwd_f32_robust_special_values(cuda):
+    print("case fwd_f32 robust specials", flush=True)
+    for B, N in [(8, 5), (300, 1000), (64, 128256)]:
+        x = O.make_robust_rows(O.make_c2_input(B, N, seed=3), seed=B)
+        got = _ext().onepass_lse_float_robust(torch.from_numpy(x).to(cuda)).cpu().numpy()
+        want = O.lse_fp64(x)
+        assert np.isneginf(got[0]) and np.isposinf(got[1]) and np.isnan(got[2]) and np.isposinf(got[3])
+        _close(got, want, RTOL32, atol=1e-6)
+        tor = torch.logsumexp(torch.from_numpy(x).to(cuda), dim=-1).cpu().numpy()
+        _close(got, tor, RTOL32, atol=2e-6)
+
+
+def test_fwd_f32_robust_edge_rows(cuda):
+    """Rows made only of -inf, +inf, NaN, or mixes, at short and long N."""
+    print("case fwd_f32 robust edge rows", flush=True)
+    for N in (2, 9, 4096, 70000):
+        rows = [np.full(N, -np.inf), np.full(N, np.inf), np.full(N, np.nan)]
+        r = np.full(N, -np.inf); r[N // 2] = 1.5; rows.append(r)
+        r = np.full(N, -np.inf); r[-1] = np.nan; rows.append(r)
+        r = np.zeros(N); r[0] = np.inf; r[1] = np.nan; rows.append(r)
+        r = np.full(N, 80.0); rows.append(r)
+        r = np.full(N, -1e30); rows.append(r)
+        x = np.stack(rows).astype(np.float32)
+        got = _ext().onepass_lse_float_robust(torch.from_numpy(x).to(cuda)).cpu().numpy()
+        _close(got, O.lse_fp64(x), RTOL32, atol=1e-6)
+
+
+@pytest.mark.parametrize("B,N", [(1, 2), (32, 256), (200, 1000), (8, 1023), (16, 4099), (64, 128256), (3, 50257)])
+def test_bwd_f32_matches_fp64(cuda, B, N):
+    print(f"case bwd_f32 B={B} N={N}", flush=True)
+    rng = np.random.default_rng(N)
+    x = O.make_c2_input(B, N, seed=N)
+    g = rng.standard_normal(B).astype(np.float32)
+    xd = torch.from_numpy(x).to(cuda)
+    ext = _ext()
+    lse = ext.onepass_lse_float_robust(xd)
+    gx = ext.onepass_lse_float_backward(torch.from_numpy(g).to(cuda), xd, lse).cpu().numpy()
+    want = O.lse_bwd_fp64(g, x, O.lse_fp64(x))
+    np.testing.assert_allclose(gx, want, rtol=RTOL32, atol=1e-30)
+    # each row of softmax sums to 1: rows of grad sum to g
+    np.testing.assert_allclose(gx.astype(np.float64).sum(1), g, rtol=1e-4, atol=1e-6)
+
+
+def test_bwd_f32_unaligned_and_mismatched(cuda):
+    print("case bwd_f32 unaligned", flush=True)
+    rng = np.random.default_rng(11)
+    for B, N, off in [(5, 1001, 1), (4, 9000, 3), (3, 7, 2)]:
+        x = (rng.standard_normal((B, N)) * 2).astype(np.float32)
+        g = rng.standard_normal(B).astype(np.float32)
+        xd = _offset_view(torch.from_numpy(x), cuda, off)  # grad buffer is aligned: scalar path
+        lse = _ext().onepass_lse_float_robust(xd)
+        gx = _ext().onepass_lse_float_backward(torch.from_numpy(g).to(cuda), xd, lse).cpu().numpy()
+        np.testing.assert_allclose(gx, O.lse_bwd_fp64(g, x, O.lse_fp64(x)), rtol=RTOL32, atol=1e-30)
+
+
+def test_bwd_f32_special_rows(cuda):
+    """All -inf row -> NaN gradient (torch's grad*exp(x-result)); +inf row."""
+    print("case bwd_f32 special rows", flush=True)
+    x = O.make_robust_rows(O.make_c2_input(8, 300, seed=5), seed=8)
+    g = np.ones(8, np.float32)
+    xd = torch.from_numpy(x).to(cuda)
+    lse = _ext().onepass_lse_float_robust(xd)
+    gx = _ext().onepass_lse_float_backward(torch.from_numpy(g).to(cuda), xd, lse).cpu().numpy()
+    want = O.lse_bwd_fp64(g, x, O.lse_fp64(x))
+    np.testing.assert_allclose(gx, want, rtol=RTOL32, atol=1e-30, equal_nan=True)
+    xt = torch.from_numpy(x).to(cuda).requires_grad_(True)
+    torch.logsumexp(xt, -1).sum().backward()
+    np.testing.assert_allclose(gx, xt.grad.cpu().numpy(), rtol=RTOL32, atol=1e-30, equal_nan=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("B,N", [(4, 3), (65536, 256), (64, 32000), (16, 128256), (5, 50257), (100, 1000)])
+def test_fwd_half_matches_fp64(cuda, dtype, B, N):
+    print(f"case fwd_half {dtype} B={B} N={N}", flush=True)
+    rng = np.random.default_rng(N + B)
+    x = (rng.standard_normal((B, N)) * 2).astype(np.float32)
+    xh = torch.from_numpy(x).to(dtype)
+    xf = xh.float().numpy()  # the values the kernel sees
+    ext = _ext()
+    fn = ext.batched_logsumexp_fp16 if dtype == torch.float16 else ext.batched_logsumexp_bf16
+    got = fn(xh.to(cuda)).cpu().numpy()
+    assert got.dtype == np.float32
+    want = O.lse_fp64(xf)
+    _close(got, want, RTOL16)
+    # fp32 accumulation: in fact far inside 1e-3
+    _close(got, want, 2e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fwd_half_unaligned(cuda, dtype):
+    print(f"case fwd_half unaligned {dtype}", flush=True)
+    rng = np.random.default_rng(3)
+    for B, N, off in [(5, 9, 1), (4, 1001, 3), (3, 20001, 5)]:
+        x = torch.from_numpy((rng.standard_normal((B, N)) * 2).astype(np.float32)).to(dtype)
+        v = _offset_view(x, cuda, off)
+        ext = _ext()
+        fn = ext.batched_logsumexp_fp16 if dtype == torch.float16 else ext.batched_logsumexp_bf16
+        got = fn(v).cpu().numpy()
+        _close(got, O.lse_fp64(x.float().numpy()), 2e-5, atol=1e-5)
+
+
+def test_dropin_autograd_matches_torch(cuda):
+    """make_fuselse_logsumexp(ext) vs torch.logsumexp: forward, backward,
+    keepdim, N-D input, non-contiguous input and every fallback branch."""
+    print("case dropin autograd", flush=True)
+    import fuselse_amd
+
+    for robust in (True, False):
+        lse = fuselse_amd.make_fuselse_logsumexp(fuselse_amd.ext, robust=robust)
+        x = torch.randn(4, 6, 1000, device=cuda) * 2
+        a = x.clone().requires_grad_(True)
+        b = x.clone().requires_grad_(True)
+        ya = lse(a, dim=-1)
+        yb = torch.logsumexp(b, dim=-1)
+        assert ya.shape == yb.shape == (4, 6)
+        torch.testing.assert_close(ya, yb, rtol=RTOL32, atol=2e-6)
+        w = torch.randn_like(ya)
+        (ya * w).sum().backward()
+        (yb * w).sum().backward()
+        torch.testing.assert_close(a.grad, b.grad, rtol=RTOL32, atol=1e-7)
+        # keepdim, 2-D direct path, non-contiguous input
+        x2 = torch.randn(37, 515, device=cuda)
+        torch.testing.assert_close(lse(x2, dim=1, keepdim=True), torch.logsumexp(x2, 1, keepdim=True),
+                                   rtol=RTOL32, atol=2e-6)
+        xt = torch.randn(515, 37, device=cuda).t()
+        assert not xt.is_contiguous()
+        torch.testing.assert_close(lse(xt, -1), torch.logsumexp(xt, -1), rtol=RTOL32, atol=2e-6)
+        # fallbacks: other dim, dtype, N == 1
+        torch.testing.assert_close(lse(x2, dim=0), torch.logsumexp(x2, 0))
+        xd = x2.double()
+        assert lse(xd, -1).dtype == torch.float64
+        x1 = torch.randn(5, 1, device=cuda)
+        torch.testing.assert_close(lse(x1, -1), torch.logsumexp(x1, -1))
+        # empty batch
+        assert lse(torch.empty(0, 8, device=cuda), -1).shape == (0,)
+
+
+def test_dropin_is_native(cuda):
+    """The GPU drop-in path runs the native library (it is loaded in-process)."""
+    import fuselse_amd
+    from fuselse_amd import _lib
+
+    x = torch.randn(8, 64, device=cuda)
+    fuselse_amd.logsumexp(x)
+    assert _lib._lib is not None
+    maps = open("/proc/self/maps").read()
+    assert "libfuselse_amd.so" in maps
