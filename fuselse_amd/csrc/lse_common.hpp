@@ -87,17 +87,20 @@ __device__ __forceinline__ void lse_fold(float& m, float& s, const float (&v)[K]
 #pragma unroll
     for (int k = 1; k < K; ++k) cm = fmaxf(cm, v[k]);
     float mn = fmaxf(m, cm);
-    float nb;
+    float b;
     if constexpr (ROBUST) {
         s *= lse_rescale(m, mn);
-        nb = -lse_base(mn) * kLog2e;
+        b = lse_base(mn);
     } else {
         s *= fexp2((m - mn) * kLog2e);
-        nb = -mn * kLog2e;
+        b = mn;
     }
+    // exp(v - b) as exp2((v - b) * log2 e): the difference is exact for v near
+    // b at any magnitude (a fused v*log2e - b*log2e would carry the rounding
+    // of b*log2e, about 1e23 when |b| ~ 1e30).
     float acc = 0.0f;
 #pragma unroll
-    for (int k = 0; k < K; ++k) acc += fexp2(__builtin_fmaf(v[k], kLog2e, nb));
+    for (int k = 0; k < K; ++k) acc += fexp2((v[k] - b) * kLog2e);
     s += acc;
     m = mn;
 }

@@ -1,0 +1,414 @@
+"""Pins for the CPU oracle (oracle/lse_oracle.c, oracle/oracle.py) before it is
+trusted as the parity checker.
+
+Each pin is chosen so that a plausible slip in the restatement (a dropped LUT
+term, a wrong index or shift, a mis-ordered tree level, a wrong identity or
+alignment prefix) fails at least one check:
+
+* the compiled reference (oracle/_ref, built from intlse/cpu/lse_kernel_simd.c)
+  and the fixtures it wrote (tests/golden/) pin the Q16.16 pair op, the CPU
+  quantisers and the whole AVX2 block tree bit for bit;
+* closed forms and exhaustive error bounds pin the pair ops and tables;
+* hand-computable special rows pin the GPU reduction tree shape;
+* the reference's published accuracy envelopes (mean |err| vs fp64 per N,
+  experiment_microbenchmark/*/outputs/*.json) pin the GPU trees statistically.
+"""
+
+import math
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+NEG = O.GPU_NEG_INF
+
+
+# ---------------------------------------------------------------------------
+# compiled reference + golden fixtures
+# ---------------------------------------------------------------------------
+def _fixture_rows():
+    d = np.load(os.path.join(GOLD, "intlse_cpu_ref.npz"))
+    off = 0
+    for (B, N) in d["shapes"]:
+        n = int(B * N)
+        yield d["x"][off:off + n].reshape(B, N), int(B)
+        off += n
+
+
+def test_intlse_cpu_restatement_matches_fixtures():
+    d = np.load(os.path.join(GOLD, "intlse_cpu_ref.npz"))
+    got, got_ni = [], []
+    for x, _ in _fixture_rows():
+        got.append(O.intlse_cpu_rows(x, False))
+        got_ni.append(O.intlse_cpu_rows(x, True))
+    np.testing.assert_array_equal(np.concatenate(got).view(np.int32), d["out"].view(np.int32))
+    np.testing.assert_array_equal(np.concatenate(got_ni).view(np.int32), d["out_neg_inf"].view(np.int32))
+
+
+def test_q16_pair_sweep_matches_fixture():
+    """N=2 rows: scalar quantiser and one scalar pair over a dense gap sweep."""
+    d = np.load(os.path.join(GOLD, "q16_pair_ref.npz"))
+    np.testing.assert_array_equal(O.intlse_cpu_rows(d["x"]).view(np.int32), d["out"].view(np.int32))
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built (reference tree absent)")
+@pytest.mark.parametrize("N", [2, 5, 63, 64, 65, 128, 191, 192, 640, 1000, 4096, 50257])
+@pytest.mark.parametrize("rng_kind", ["u1", "u100", "u500", "wide"])
+def test_intlse_cpu_restatement_matches_compiled_reference(N, rng_kind):
+    rng = np.random.default_rng(N)
+    lo, hi = {"u1": (-1, 0), "u100": (-100, 0), "u500": (-500, 0), "wide": (-2e4, 2e4)}[rng_kind]
+    x = (rng.random((6, N)) * (hi - lo) + lo).astype(np.float32)
+    x[1, ::5] = -np.inf
+    if N > 3:
+        x[2, 3] = np.float32(4e9)
+        x[3, 0] = np.float32(-4e9)
+    for ni in (False, True):
+        np.testing.assert_array_equal(O.intlse_cpu_rows(x, ni).view(np.int32),
+                                      O.ref_intlse_cpu_rows(x, ni).view(np.int32))
+
+
+# ---------------------------------------------------------------------------
+# Q16.16 pair op
+# ---------------------------------------------------------------------------
+def test_q16_pair_closed_forms():
+    x = np.array([0, 12345, -987654, 2 ** 24], np.int32)
+    # pair(x, x) = x + 1.0 (log2 2 = 1): M = 65536, LUT[(65536>>10)&63] = LUT[0] = 0
+    np.testing.assert_array_equal(O.q16_pair(x, x), x + 65536)
+    # one unit apart: M = 32768 -> LUT[32] = 5399
+    np.testing.assert_array_equal(O.q16_pair(x, x - 65536), x + 32768 + 5399)
+    # beyond 16 units the smaller operand vanishes exactly
+    for d in (17 * 65536, 100 * 65536, 2 ** 30):
+        np.testing.assert_array_equal(O.q16_pair(x, x - d), x)
+    # symmetric
+    rng = np.random.default_rng(0)
+    a = rng.integers(-2 ** 31, 2 ** 31, 10000, dtype=np.int64).astype(np.int32)
+    b = rng.integers(-2 ** 31, 2 ** 31, 10000, dtype=np.int64).astype(np.int32)
+    np.testing.assert_array_equal(O.q16_pair(a, b), O.q16_pair(b, a))
+    # the identity of the GPU kernels vanishes against ordinary values
+    v = (rng.standard_normal(1000) * 2 ** 22).astype(np.int32)
+    np.testing.assert_array_equal(O.q16_pair(v, np.full_like(v, NEG)), v)
+    assert O.q16_pair(np.array([NEG], np.int32), np.array([NEG], np.int32))[0] == NEG + 65536
+
+
+def test_q16_pair_error_bound_exhaustive():
+    """Every gap d in [0, 17*65536]: |pair(0, -d) - 65536*log2(1 + 2^(-d/65536))|
+    stays within the Mitchell+LUT bound, and without the LUT the error is the
+    plain Mitchell error (up to 0.086 log2 units)."""
+    d = np.arange(0, 17 * 65536 + 1, dtype=np.int64)
+    zero = np.zeros(d.size, np.int32)
+    exact = 65536.0 * np.log2(1.0 + np.exp2(-d / 65536.0))
+    err = O.q16_pair(zero, (-d).astype(np.int32)) - exact
+    assert np.max(np.abs(err)) < 0.011 * 65536, np.max(np.abs(err)) / 65536
+    err_nolut = O.q16_pair(zero, (-d).astype(np.int32), mode="nolut") - exact
+    assert 0.08 * 65536 < np.max(np.abs(err_nolut)) < 0.09 * 65536
+    # the x86 scalar helper equals the GPU form wherever the difference does not wrap
+    np.testing.assert_array_equal(O.q16_pair(zero, (-d).astype(np.int32), mode="x86"),
+                                  O.q16_pair(zero, (-d).astype(np.int32)))
+
+
+def test_q16_pair_wrapped_difference():
+    """Operands more than 2^31 apart make the difference wrap to a positive
+    value.  For a wrapped difference of 2^20 + 1 the count -(sub >> 16) is -16:
+    the GPU/SIMD form reads it unsigned (>= 32 -> M = 0, the max survives), the
+    x86 scalar helper shifts by -16 mod 32 = 16 (M = 1).  For a wrapped
+    difference below 2^16 the count is 0 and both add 65536 + sub."""
+    a = np.array([2 ** 31 - 1], np.int32)
+    b = np.array([-2 ** 31 + 2 ** 20], np.int32)
+    assert O.q16_pair(a, b)[0] == 2 ** 31 - 1
+    assert O.q16_pair(a, b, mode="x86")[0] == -2 ** 31  # (2^31 - 1) + 1 wraps
+    b2 = np.array([-2 ** 31 + 5], np.int32)  # wrapped difference 6
+    want = np.int64(2 ** 31 - 1) + 65536 + 6 - 2 ** 32
+    assert O.q16_pair(a, b2)[0] == want
+    assert O.q16_pair(a, b2, mode="x86")[0] == want
+
+
+def test_q16_luts():
+    """The Q10.6 table is the Q16.16 table rounded to 6 fractional bits
+    (lse_kernel_q10_6.cu:23-26)."""
+    q16 = O.lut_q16()
+    q10 = O.lut_q10_6()
+    assert q16[0] == 0 and q16[32] == 5399 and q16[63] == 2
+    np.testing.assert_array_equal(q10, np.floor(q16 / 1024.0 + 0.5).astype(np.int64))
+
+
+# ---------------------------------------------------------------------------
+# Q10.6 pair op
+# ---------------------------------------------------------------------------
+def test_q10_6_pair_closed_forms_and_bound():
+    x = np.array([0, 100, -5000, 30000], np.int32)
+    np.testing.assert_array_equal(O.q10_6_pair(x, x), x + 64)
+    # d = 32 (half a unit): M = 48 -> LUT[48] = 1
+    np.testing.assert_array_equal(O.q10_6_pair(x, x - 32), x + 49)
+    for d in (17 * 64, 400, 10 ** 6):
+        np.testing.assert_array_equal(O.q10_6_pair(x, x - d), x)
+    d = np.arange(0, 2000, dtype=np.int64)
+    zero = np.zeros(d.size, np.int32)
+    exact = 64.0 * np.log2(1.0 + np.exp2(-d / 64.0))
+    err = O.q10_6_pair(zero, (-d).astype(np.int32)) - exact
+    assert np.max(np.abs(err)) <= 1.6, np.max(np.abs(err))  # Mitchell alone: ~5.5
+    # the whole pair op depends only on the gap and is the identity past 384
+    assert np.all(O.q10_6_pair(zero, (-d).astype(np.int32))[385:] == 0)
+    rng = np.random.default_rng(1)
+    a = rng.integers(-30000, 30000, 5000).astype(np.int32)
+    b = rng.integers(-30000, 30000, 5000).astype(np.int32)
+    np.testing.assert_array_equal(O.q10_6_pair(a, b), O.q10_6_pair(b, a))
+    np.testing.assert_array_equal(O.q10_6_pair(a, b) - np.maximum(a, b),
+                                  O.q10_6_pair(np.zeros_like(a), -np.abs(a - b)))
+
+
+# ---------------------------------------------------------------------------
+# quantisers
+# ---------------------------------------------------------------------------
+def test_q16_quantisers():
+    assert float(O.Q16_CONV) == 94548.4609375
+    specials = np.array([np.nan, np.inf, -np.inf, 3e5, -3e5, 0.0, -0.0], np.float32)
+    np.testing.assert_array_equal(O.q16_quant(specials, "gpu"),
+                                  [0, 2 ** 31 - 1, -2 ** 31, 2 ** 31 - 1, -2 ** 31, 0, 0])
+    np.testing.assert_array_equal(O.q16_quant(specials, "cpu_simd")[1:],
+                                  [2147483520, -2147483520, 2147483520, -2147483520, 0, 0])
+    # sparse quantiser clamps logits at -20000 first; NaN -> -20000
+    np.testing.assert_array_equal(O.q16_quant(np.array([np.nan, -1e9], np.float32), "sparse"),
+                                  [int(np.float32(-20000.0) * O.Q16_CONV)] * 2)  # fp32 product: -1890969216
+    # ties: round half to even on the GPU and in SIMD, half away from zero in the scalar CPU path
+    v = np.array([2.5, 3.5, -2.5], np.float32) / O.Q16_CONV
+    prod = v * O.Q16_CONV
+    exact_ties = prod == np.array([2.5, 3.5, -2.5], np.float32)
+    if exact_ties.all():
+        np.testing.assert_array_equal(O.q16_quant(v, "gpu"), [2, 4, -2])
+        np.testing.assert_array_equal(O.q16_quant(v, "cpu_scalar"), [3, 4, -3])
+    # in range, GPU and CPU SIMD quantisers agree (SIMD one pinned by the reference build)
+    x = (np.random.default_rng(2).standard_normal(100000) * 1000).astype(np.float32)
+    np.testing.assert_array_equal(O.q16_quant(x, "gpu"), O.q16_quant(x, "cpu_simd"))
+
+
+def test_to_q10_6():
+    x = np.array([0.0, 1.0, -1.0, 1000.0, -1000.0, 0.5 / 92.33248], np.float32)
+    q = O.to_q10_6(x)
+    conv = np.float32(math.log2(math.e) * 64.0)
+    assert q[1] == int(np.rint(np.float32(1.0) * conv)) == 92
+    assert q[3] == 32767 and q[4] == -32768
+    assert q.dtype == np.int16
+
+
+# ---------------------------------------------------------------------------
+# GPU reduction trees
+# ---------------------------------------------------------------------------
+def _chain(vals, pair):
+    acc = np.array([vals[0]], np.int32)
+    for v in vals[1:]:
+        acc = pair(acc, np.array([v], np.int32))
+    return int(acc[0])
+
+
+def test_gpu_tree_single_chain_row():
+    """N=4, aligned: only virtual thread 0 has elements; every other lane holds
+    the identity, which vanishes, so the row equals the sequential chain."""
+    q = np.array([[1000000, -300000, 2500000, 2400000]], np.int32)
+    out, raw = O.q16_gpu_rows(q, raw=True)
+    assert raw[0] == _chain(list(q[0]), O.q16_pair)
+    assert out[0] == np.float32(np.float32(raw[0]) * O.Q16_OUT)
+
+
+def test_gpu_tree_equal_rows_closed_form():
+    """N = 256*4*k equal values v: each of the 256 chains folds 4k copies
+    (chain value c), then 8 doubling levels (5 in the warp, 3 in the final
+    stage where the identity padding drops out): result c + 8*65536."""
+    for k in (1, 2, 3):
+        v = 123456
+        q = np.full((1, 1024 * k), v, np.int32)
+        raw = O.q16_gpu_rows(q, raw=True)[1][0]
+        c = _chain([v] * (4 * k), O.q16_pair)
+        assert raw == c + 8 * 65536
+    # the same for Q10.6 with +64 per level
+    q = np.full((1, 2048), 300, np.int16)
+    raw = O.q10_6_rows(q, raw=True)[1][0]
+    assert raw == _chain([300] * 8, O.q10_6_pair) + 8 * 64
+
+
+def test_gpu_tree_prefix_and_suffix():
+    """A misaligned row start gives threads 0..p-1 one prefix element; the
+    remaining elements form vector chunks and a suffix.  With N = 7 and a row
+    starting 4 bytes past a 16-byte boundary: prefix 3 (threads 0,1,2), one
+    chunk (thread 0) and no suffix: thread 0 = chain(e0, e3..e6), threads 1, 2
+    hold e1, e2; the warp butterfly then pairs lanes (0,2) at distance 2 and
+    (0,1) at distance 1."""
+    q = np.array([[40000, -70000, 90000, 10000, 20000, 30000, 40000]], np.int32)
+    raw = O.q16_gpu_rows(q, base_mod=4, raw=True)[1][0]
+    p = O.q16_pair
+    t0 = _chain([q[0, 0], q[0, 3], q[0, 4], q[0, 5], q[0, 6]], p)
+    one = lambda a, b: int(p(np.array([a], np.int32), np.array([b], np.int32))[0])  # noqa: E731
+    # off=16,8,4: lanes 0..2 pair with identity lanes (exact); lane 0 then
+    # pairs with lane 2 (off=2) and the result with lane 1's (lane1 paired with lane3 = identity)
+    want = one(one(t0, int(q[0, 2])), int(q[0, 1]))
+    assert raw == want
+    # aligned start: the same 7 values take one chunk (thread 0: e0..e3) and a suffix (threads 0..2)
+    raw_al = O.q16_gpu_rows(q, base_mod=0, raw=True)[1][0]
+    t0 = _chain([q[0, 0], q[0, 1], q[0, 2], q[0, 3], q[0, 4]], p)
+    want_al = one(one(t0, int(q[0, 6])), int(q[0, 5]))
+    assert raw_al == want_al
+
+
+# Published envelopes: intlse_gpu / intlse_nolut / intlse_cpu mean |err| vs fp64
+# at B=512, 20 seeds, inputs U(lo, 0) (experiment_microbenchmark/microbench/
+# outputs/benchmark_results.json, ranges U(-1,0), U(-100,0), U(-500,0)).
+ENVELOPE = {
+    # (lo, N): (intlse_gpu, intlse_nolut, intlse_cpu)
+    (-1, 1024): (8.86e-05, 0.0905, 0.00015),
+    (-1, 8192): (0.00196, 0.262, 5.57e-05),
+    (-1, 32000): (0.114, 0.305, 5.2e-05),
+    (-1, 128256): (0.269, 0.321, 6.4e-05),
+    (-100, 4096): (0.0012, 0.168, 0.00118),
+    (-100, 128256): (0.0109, 0.234, 0.00111),
+    (-500, 16384): (0.00123, 0.167, 0.0012),
+    (-500, 128256): (0.00232, 0.178, 0.00114),
+}
+
+
+@pytest.mark.parametrize("lo,N", sorted(ENVELOPE))
+def test_gpu_tree_matches_published_envelope(lo, N):
+    rng = np.random.default_rng(N + int(-lo))
+    B = 256 if N > 20000 else 512
+    x = (rng.random((B, N), dtype=np.float32) * np.float32(-lo) + np.float32(lo)).astype(np.float32)
+    ref = O.fp64_lse_ref(x)
+    gpu, nolut, cpu = ENVELOPE[(lo, N)]
+    e_gpu = np.abs(O.q16_gpu_rows(x) - ref).mean()
+    e_nolut = np.abs(O.q16_gpu_rows(x, use_lut=False) - ref).mean()
+    assert abs(e_gpu / gpu - 1) < 0.2, (e_gpu, gpu)
+    assert abs(e_nolut / nolut - 1) < 0.2, (e_nolut, nolut)
+    if N <= 8192:
+        e_cpu = np.abs(O.intlse_cpu_rows(x, True) - ref).mean()
+        assert abs(e_cpu / cpu - 1) < 0.25, (e_cpu, cpu)
+
+
+# Reduced-bit envelope: Q10.6 mean |err| vs fp64 at B=512, U(-100, 0)
+# (experiment_microbenchmark/reduced_bit/outputs/bench_results.json).
+Q106_ENVELOPE = {64: 0.01135, 1024: 0.02728, 16384: 0.04471, 128256: 0.09466}
+
+
+@pytest.mark.parametrize("N", sorted(Q106_ENVELOPE))
+def test_q10_6_tree_matches_published_envelope(N):
+    rng = np.random.default_rng(N)
+    B = 128 if N > 20000 else 512
+    x = (rng.random((B, N), dtype=np.float32) * np.float32(100.0) - np.float32(100.0)).astype(np.float32)
+    out = O.q10_6_rows(O.to_q10_6(x))
+    e = np.abs(out - O.fp64_lse_ref(x)).mean()
+    assert abs(e / Q106_ENVELOPE[N] - 1) < 0.2, (e, Q106_ENVELOPE[N])
+
+
+# ---------------------------------------------------------------------------
+# sparse Q16 tree
+# ---------------------------------------------------------------------------
+def test_edge_thread_rule():
+    assert [O.edge_threads(k) for k in (1, 8, 9, 16, 17, 32, 33, 256)] == [1, 1, 2, 2, 4, 4, 8, 8]
+
+
+def test_sparse_q16_closed_forms():
+    """One edge: the identity seed vanishes -> q itself.  Two equal edges
+    (ET=1): pair(q, q) = q + 65536.  Nine equal edges (ET=2): chains of 5 and 4
+    then one butterfly level."""
+    child = np.array([[1.25, -3.0], [0.5, 0.75]], np.float32)  # 2 children x batch 2
+    for k in (1, 2, 9):
+        off = np.array([0, k], np.int64)
+        cids = np.zeros(k, np.int32)
+        lp = np.full(k, -0.5, np.float32)
+        out = O.sparse_q16_csr(child, off, cids, lp)
+        for b in range(2):
+            q = int(O.q16_quant(np.array([np.float32(-0.5) + child[0, b]], np.float32), "sparse")[0])
+            if k == 1:
+                r = q
+            elif k == 2:
+                r = q + 65536
+            else:
+                c5 = _chain([q] * 5, O.q16_pair)
+                c4 = _chain([q] * 4, O.q16_pair)
+                r = int(O.q16_pair(np.array([c5], np.int32), np.array([c4], np.int32))[0])
+            assert out[0, b] == np.float32(np.float32(r) * O.Q16_OUT)
+    # an empty node gives -inf
+    out = O.sparse_q16_csr(child, np.array([0, 0], np.int64), np.zeros(0, np.int32), np.zeros(0, np.float32))
+    assert np.all(np.isneginf(out))
+
+
+def test_sparse_q16_tracks_float_oracle():
+    rng = np.random.default_rng(5)
+    nodes, nch, batch = 300, 200, 16
+    k = O.powerlaw_fanin(nodes, seed=1)
+    off = np.concatenate([[0], np.cumsum(k)]).astype(np.int64)
+    cids = rng.integers(0, nch, off[-1]).astype(np.int32)
+    lp = np.log(rng.random(off[-1])).astype(np.float32)
+    child = np.log(rng.random((nch, batch))).astype(np.float32)
+    want = O.sparse_csr_fp64(child, off, cids, lp)
+    got = O.sparse_q16_csr(child, off, cids, lp)
+    err = np.abs(got - want)
+    assert err.mean() < 5e-3 and err.max() < 0.05, (err.mean(), err.max())
+
+
+def test_sparse_blocked_q16_equals_csr_on_expanded_layout():
+    """The pyjuice block layout is the CSR layout after block expansion
+    (run_pyjuice.py:103-113): node nids[j]+p owns edges cids[j, :] with
+    weights params[pids[j, e] + p]."""
+    rng = np.random.default_rng(6)
+    nb, ne, bs, batch, nelem = 3, 5, 4, 8, 20
+    nids = np.array([0, 4, 8], np.int64)
+    cids = rng.integers(0, nelem, (nb, ne)).astype(np.int64)
+    pids = rng.integers(0, 40, (nb, ne)).astype(np.int64)
+    params = rng.random(64).astype(np.float32)
+    em = np.log(rng.random((nelem, batch))).astype(np.float32)
+    logw = np.empty((nb, bs, ne), np.float32)
+    for j in range(nb):
+        for p in range(bs):
+            logw[j, p] = np.log(np.maximum(params[pids[j] + p], np.float32(1e-45)))
+    nm = O.sparse_q16_blocked(np.zeros((12, batch), np.float32), em, logw, nids, cids, bs)
+    off = np.arange(0, nb * bs * ne + 1, ne, dtype=np.int64)
+    ccs = np.repeat(cids, bs, axis=0).reshape(-1).astype(np.int32)
+    out = O.sparse_q16_csr(em, off, ccs, logw.reshape(-1))
+    np.testing.assert_array_equal(nm, out)
+
+
+# ---------------------------------------------------------------------------
+# float oracles
+# ---------------------------------------------------------------------------
+def test_lse_fp64_against_scipy_and_invariants():
+    from scipy.special import logsumexp
+
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((50, 333)) * 5).astype(np.float32)
+    np.testing.assert_allclose(O.lse_fp64(x), logsumexp(x.astype(np.float64), axis=-1), rtol=1e-13)
+    np.testing.assert_allclose(O.lse_fp64(x.astype(np.float64) + 7.0), O.lse_fp64(x) + 7.0, rtol=1e-12)
+    np.testing.assert_allclose(O.lse_fp64(np.full((2, 1000), 2.0)), 2.0 + np.log(1000.0), rtol=1e-14)
+    np.testing.assert_allclose(O.lse_fp64(x[:, rng.permutation(333)]), O.lse_fp64(x), rtol=1e-13)
+    # N = 2: textbook max + log1p(exp(-|a - b|))
+    a, b = 3.0, -1.5
+    assert math.isclose(O.lse_fp64(np.array([[a, b]]))[0], a + math.log1p(math.exp(-(a - b))), rel_tol=1e-15)
+
+
+def test_lse_fp64_special_values_follow_torch():
+    import torch
+
+    x = O.make_robust_rows(O.make_c2_input(12, 50, seed=2), seed=3)
+    want = torch.logsumexp(torch.from_numpy(x).double(), -1).numpy()
+    np.testing.assert_allclose(O.lse_fp64(x), want, rtol=1e-12, equal_nan=True)
+
+
+def test_lse_bwd_fp64_is_scaled_softmax():
+    from scipy.special import softmax
+
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((7, 40))
+    g = rng.standard_normal(7)
+    np.testing.assert_allclose(O.lse_bwd_fp64(g, x, O.lse_fp64(x)), g[:, None] * softmax(x, axis=-1), rtol=1e-12)
+
+
+def test_fuselse_cpu_port_envelope_and_pair():
+    """Sequential float pair chain (fused_fp32_cpu.cpp): N=2 is the textbook
+    pair in fp32, and at N=128256 on U(-100,0) the chain's mean |err| lands on
+    the published 1.06e-4 (benchmark_results.json fuselse_cpu)."""
+    x = np.array([[3.0, -1.5]], np.float32)
+    want = np.float32(3.0) + np.log1p(np.exp(np.float32(-4.5)))
+    assert abs(O.fuselse_cpu_rows(x)[0] - want) <= 2e-7
+    rng = np.random.default_rng(8)
+    x = (rng.random((64, 128256), dtype=np.float32) * np.float32(100.0) - np.float32(100.0))
+    e = np.abs(O.fuselse_cpu_rows(x) - O.fp64_lse_ref(x)).mean()
+    assert abs(e / 1.06e-4 - 1) < 0.25, e
