@@ -118,11 +118,10 @@ static void launch_fwd(const T* x, float* out, int64_t B, int64_t N, hipStream_t
     constexpr int VE = Elem<T>::kVec;
     const int64_t vecs = (N + VE - 1) / VE;
     if (vecs > 4096) {
-        const int64_t grid = B;
-        if (vecs > 16384)
-            lse_fwd_block_rows<T, ROBUST, 1024, 4><<<dim3((unsigned)grid), dim3(1024), 0, st>>>(x, out, B, N);
-        else
-            lse_fwd_block_rows<T, ROBUST, 512, 4><<<dim3((unsigned)grid), dim3(512), 0, st>>>(x, out, B, N);
+        // one 512-thread block per row, two 16-byte loads per lane per fold:
+        // measured best at (512, 128256) among 256..1024 threads x 1..8 loads
+        int64_t grid = B < ((int64_t)1 << 30) ? B : ((int64_t)1 << 30);
+        lse_fwd_block_rows<T, ROBUST, 512, 2><<<dim3((unsigned)grid), dim3(512), 0, st>>>(x, out, B, N);
         return;
     }
     int64_t lpr = pow2_ceil((vecs + 3) / 4);
@@ -163,6 +162,26 @@ __device__ __forceinline__ float bwd_elem(float gv, float lse, float xv) {
     return gv * fexp2((xv - lse) * kLog2e);
 }
 
+// grad * exp(x - lse) for four elements.  For |lse| < 64 the exponent is one
+// FMA, x*log2e - lse*log2e, whose shared rounding of lse*log2e costs at most
+// 64*log2e*2^-24 (4e-6 relative); larger |lse| use the exact difference.
+__device__ __forceinline__ f32x4 bwd_vec(float gv, float lv, bool fma_ok, f32x4 v) {
+    f32x4 r;
+    if (fma_ok) {
+        const float nb = -lv * kLog2e;
+        r.x = gv * fexp2(__builtin_fmaf(v.x, kLog2e, nb));
+        r.y = gv * fexp2(__builtin_fmaf(v.y, kLog2e, nb));
+        r.z = gv * fexp2(__builtin_fmaf(v.z, kLog2e, nb));
+        r.w = gv * fexp2(__builtin_fmaf(v.w, kLog2e, nb));
+    } else {
+        r.x = bwd_elem(gv, lv, v.x);
+        r.y = bwd_elem(gv, lv, v.y);
+        r.z = bwd_elem(gv, lv, v.z);
+        r.w = bwd_elem(gv, lv, v.w);
+    }
+    return r;
+}
+
 // Long rows: grid = B * chunks_per_row blocks of 256 threads; a block covers
 // 256*U consecutive vectors of one row.  x and grad_x share their alignment.
 template <int U>
@@ -185,24 +204,18 @@ __global__ __launch_bounds__(256) void lse_bwd_row_chunks(const float* __restric
     }
     const f32x4* xb = reinterpret_cast<const f32x4*>(xr + sp.head);
     f32x4* gb = reinterpret_cast<f32x4*>(gr + sp.head);
+    const bool fma_ok = __builtin_fabsf(lv) < 64.0f;
     const int64_t i0 = chunk * 256 * U + tid;
     f32x4 v[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int64_t i = i0 + (int64_t)u * 256;
-        if (i < sp.nvec) v[u] = xb[i];
+        if (i < sp.nvec) v[u] = load_stream<f32x4>(xb + i);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int64_t i = i0 + (int64_t)u * 256;
-        if (i < sp.nvec) {
-            f32x4 r;
-            r.x = bwd_elem(gv, lv, v[u].x);
-            r.y = bwd_elem(gv, lv, v[u].y);
-            r.z = bwd_elem(gv, lv, v[u].z);
-            r.w = bwd_elem(gv, lv, v[u].w);
-            gb[i] = r;
-        }
+        if (i < sp.nvec) store_stream<f32x4>(bwd_vec(gv, lv, fma_ok, v[u]), gb + i);
     }
 }
 
@@ -225,14 +238,9 @@ __global__ __launch_bounds__(256) void lse_bwd_group_rows(const float* __restric
         for (int64_t t = j; t < sp.tail; t += LPR) gr[t0 + t] = bwd_elem(gv, lv, xr[t0 + t]);
         const f32x4* xb = reinterpret_cast<const f32x4*>(xr + sp.head);
         f32x4* gb = reinterpret_cast<f32x4*>(gr + sp.head);
-        for (int64_t i = j; i < sp.nvec; i += LPR) {
-            f32x4 v = xb[i], r;
-            r.x = bwd_elem(gv, lv, v.x);
-            r.y = bwd_elem(gv, lv, v.y);
-            r.z = bwd_elem(gv, lv, v.z);
-            r.w = bwd_elem(gv, lv, v.w);
-            gb[i] = r;
-        }
+        const bool fma_ok = __builtin_fabsf(lv) < 64.0f;
+        for (int64_t i = j; i < sp.nvec; i += LPR)
+            store_stream<f32x4>(bwd_vec(gv, lv, fma_ok, load_stream<f32x4>(xb + i)), gb + i);
     }
 }
 
@@ -260,7 +268,8 @@ static void launch_bwd(const float* g, const float* x, const float* lse, float* 
     }
     const int64_t vecs = N / 4 + 1;
     if (vecs >= 1024) {
-        constexpr int U = 4;
+        // one 16-byte vector per lane: measured best (with 128x2 and 1024x1)
+        constexpr int U = 1;
         const int64_t cpr = (vecs + 256 * U - 1) / (256 * U);
         lse_bwd_row_chunks<U><<<dim3((unsigned)(B * cpr)), dim3(256), 0, st>>>(g, x, lse, gx, N, cpr);
         return;
@@ -306,7 +315,7 @@ extern "C" int fl_lse_bwd_f32(const float* grad, const float* x, const float* ls
     FL_CHECK(grad && x && lse && grad_x, "%s: NULL pointer argument", name);
     FL_CHECK((reinterpret_cast<uintptr_t>(x) & 3u) == 0 && (reinterpret_cast<uintptr_t>(grad_x) & 3u) == 0,
              "%s: x / grad_x are not 4-byte aligned", name);
-    FL_CHECK(B * ((N / 4 + 1 + 1023) / 1024) < ((int64_t)1 << 32), "%s: B*N too large for the grid", name);
+    FL_CHECK(B * ((N / 4 + 1 + 255) / 256) < ((int64_t)1 << 32), "%s: B*N too large for the grid", name);
     launch_bwd(grad, x, lse, grad_x, B, N, reinterpret_cast<hipStream_t>(stream));
     return launch_status(name);
 }
