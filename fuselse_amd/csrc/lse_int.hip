@@ -1,0 +1,348 @@
+// IntLSE fixed-point kernels for gfx950: Q16.16 (fp32 input quantised in the
+// kernel, or pre-quantised int32 input) and Q10.6 (int16 input).
+//
+// The reduction tree is part of the result (the pair op is commutative but not
+// associative), so it follows the reference kernels exactly
+// (intlse/gpu/lse_kernel.cu:67-159, lse_kernel_q10_6.cu:55-139):
+//   * 256 virtual threads per row; virtual thread t folds, in order, its
+//     alignment-prefix element (t < prefix), the 4-element vector chunks
+//     t, t+256, t+512, ... (elements x, y, z, w), and its suffix element
+//     (t < tail); the first element seeds the chain, an empty chain holds the
+//     identity -0x3fffffff;
+//   * a 32-lane xor butterfly (distances 16, 8, 4, 2, 1) inside each virtual
+//     warp of 32;
+//   * the 8 warp partials plus 24 identity lanes go through one more 32-lane
+//     xor butterfly.
+// On wave64 the 256 virtual threads are 4 waves of one 256-thread block; each
+// wave's two 32-lane halves are two virtual warps and the xor exchanges are
+// ds_swizzle bit-mask moves, which stay inside each half.
+//
+// Shift semantics: the reference computes M = (1 + frac) >> shift with a
+// count that can exceed 31 (or be negative when the difference wraps); NVIDIA
+// clamps counts >= 32 (read unsigned) to a zero result.  Here the count is
+// clamped unsigned to 31, which gives the same zero for every count >= 17
+// because the shifted value is below 2^17.
+//
+// The 64-entry correction tables live in LDS; the Q10.6 pair op, which depends
+// only on the operand gap d and is the identity for d > 384, is read from a
+// 386-entry LDS table of (M + LUT) built per block from the same formula.
+#include <stdint.h>
+
+#include "../../include/fuselse_amd.h"
+#include "fl_status.hpp"
+#include "lse_common.hpp"
+
+namespace fl {
+
+constexpr int kQNegInf = -0x3fffffff;
+// chunks per lane kept in flight ahead of the pair chain
+constexpr int kPrefetch = 8;
+// cache-policy bits of the raw buffer loads: nontemporal (streamed once)
+constexpr int kBufNT = 2;
+
+// lse_kernel.cu:35-44 (Mitchell-error correction per 1/64 bin, Q16.16)
+__constant__ int kLutQ16[64] = {
+       0,  571,  907, 1282, 1634, 1745, 2054, 2592,
+    2900, 2859, 2895, 3015, 3222, 3522, 3922, 4426,
+    4617, 4441, 4294, 4178, 4093, 4039, 4018, 4030,
+    4076, 4157, 4272, 4424, 4613, 4838, 5102, 5404,
+    5399, 5068, 4746, 4435, 4134, 3843, 3562, 3291,
+    3031, 2781, 2541, 2312, 2094, 1886, 1689, 1502,
+    1327, 1162, 1008,  865,  732,  611,  500,  401,
+     312,  235,  168,  113,   69,   35,   13,    2,
+};
+
+// lse_kernel_q10_6.cu:27-32 (the same table at 6 fractional bits)
+__constant__ int kLutQ10[64] = {
+    0, 1, 1, 1, 2, 2, 2, 3, 3, 3, 3, 3, 3, 3, 4, 4,
+    5, 4, 4, 4, 4, 4, 4, 4, 4, 4, 4, 4, 5, 5, 5, 5,
+    5, 5, 5, 4, 4, 4, 3, 3, 3, 3, 2, 2, 2, 2, 2, 1,
+    1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0,
+};
+
+// fl32(fl32(1.44269504089f) * 65536) = 94548.4609375 and
+// fl32(0.69314718056f) / 65536, / 64 (lse_kernel.cu:28-30,156).
+constexpr float kQ16Conv = 1.44269504089f * 65536.0f;
+constexpr float kQ16Out = 0.69314718056f / 65536.0f;
+constexpr float kQ10Out = 0.69314718056f / 64.0f;
+
+// Q16.16 pair: max + M + LUT[(M >> 10) & 63], M = (2^16 + (sub & 0xFFFF)) >> -(sub >> 16).
+template <bool USE_LUT>
+__device__ __forceinline__ int q16_pair(int a, int b, const int* __restrict__ lut) {
+    const int hi = a > b ? a : b;
+    const int lo = a > b ? b : a;
+    const int sub = (int)((uint32_t)lo - (uint32_t)hi);
+    const uint32_t sh = (uint32_t)(-(sub >> 16));
+    const uint32_t shc = sh < 31u ? sh : 31u;
+    const uint32_t fr = 0x10000u | ((uint32_t)sub & 0xFFFFu);
+    const int m = (int)(fr >> shc);
+    const uint32_t r = (uint32_t)hi + (uint32_t)m;
+    if constexpr (USE_LUT) {
+        // LUT index (m >> 10) & 63 as a byte offset, (m >> 8) & 0xFC, taken as
+        // ((fr >> 8) >> shc) & 0xFC so it does not wait for m.
+        const uint32_t off = ((fr >> 8) >> shc) & 0xFCu;
+        return (int)(r + (uint32_t)*reinterpret_cast<const int*>(reinterpret_cast<const char*>(lut) + off));
+    } else {
+        return (int)r;
+    }
+}
+
+// Q10.6 pair through the gap table: g[min(hi - lo, 385)], g[385] = 0.
+__device__ __forceinline__ int q10_pair(int a, int b, const int* __restrict__ g) {
+    const int hi = a > b ? a : b;
+    const int lo = a > b ? b : a;
+    uint32_t d = (uint32_t)hi - (uint32_t)lo;
+    d = d < 385u ? d : 385u;
+    return (int)((uint32_t)hi + (uint32_t)g[d]);
+}
+
+// __float2int_rn semantics: round half to even, saturate, NaN -> 0
+// (v_rndne_f32, then v_cvt_i32_f32, which clamps and maps NaN to 0).
+__device__ __forceinline__ int q16_quant(float v) {
+    const float r = __builtin_rintf(v * kQ16Conv);
+    int q;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(q) : "v"(r));
+    return q;
+}
+
+// Element sources for the trees: fp32 quantised in the kernel, int32, int16.
+// bload() fetches one 4-element chunk by raw buffer load, unpack() turns it
+// into Q values, one() reads a single (prefix or suffix) element.
+struct SrcF32 {
+    using T = float;
+    using Raw = f32x4;
+    __device__ static __forceinline__ int one(const float* p) { return q16_quant(*p); }
+    __device__ static __forceinline__ Raw bload(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+        return __builtin_bit_cast(Raw, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kBufNT));
+    }
+    __device__ static __forceinline__ void unpack(Raw v, int (&q)[4]) {
+        q[0] = q16_quant(v.x); q[1] = q16_quant(v.y); q[2] = q16_quant(v.z); q[3] = q16_quant(v.w);
+    }
+};
+struct SrcI32 {
+    using T = int32_t;
+    using Raw = u32x4;
+    __device__ static __forceinline__ int one(const int32_t* p) { return *p; }
+    __device__ static __forceinline__ Raw bload(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+        return __builtin_bit_cast(Raw, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kBufNT));
+    }
+    __device__ static __forceinline__ void unpack(Raw v, int (&q)[4]) {
+        q[0] = (int)v.x; q[1] = (int)v.y; q[2] = (int)v.z; q[3] = (int)v.w;
+    }
+};
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+struct SrcI16 {
+    using T = int16_t;
+    using Raw = u32x2;
+    __device__ static __forceinline__ int one(const int16_t* p) { return (int)*p; }
+    __device__ static __forceinline__ Raw bload(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+        return __builtin_bit_cast(Raw, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, kBufNT));
+    }
+    __device__ static __forceinline__ void unpack(Raw v, int (&q)[4]) {
+        q[0] = (int)(int16_t)(v.x & 0xFFFFu); q[1] = (int)(int16_t)(v.x >> 16);
+        q[2] = (int)(int16_t)(v.y & 0xFFFFu); q[3] = (int)(int16_t)(v.y >> 16);
+    }
+};
+
+// The reference tree over one row per block (grid-stride over rows).
+// ALIGN is the vector alignment the reference uses for the chunks (16 bytes
+// for 4-byte elements, 8 for int16); PAIR folds two accumulators.
+template <typename SRC, int ALIGN, int D, typename PAIR>
+__device__ __forceinline__ int tree_row(const typename SRC::T* row, int64_t n, const int* __restrict__ tab, PAIR pair,
+                                        int* __restrict__ sh_warp) {
+    using T = typename SRC::T;
+    const int t = threadIdx.x;
+    const uint32_t mis = (uint32_t)(reinterpret_cast<uintptr_t>(row) & (ALIGN - 1));
+    int64_t prefix = mis ? (int64_t)((ALIGN - mis) / sizeof(T)) : 0;
+    if (prefix > n) prefix = n;
+    const int64_t n4 = (n - prefix) / 4;
+    const int64_t tail = n - prefix - 4 * n4;
+    const T* body = row + prefix;
+
+    int acc = kQNegInf;
+    bool has = false;
+    if (t < prefix) {
+        acc = SRC::one(row + t);
+        has = true;
+    }
+    // Vector chunks of virtual thread t are c = t + 256*k.  Every thread owns
+    // k = 0 .. kmain-1 with kmain = n4 / 256 (a block-uniform count), and
+    // threads t < n4 % 256 own one more, k = kmain.  The uniform part runs
+    // with wave-uniform control flow; loads are raw buffer loads addressed by
+    // a per-lane constant (t * chunk bytes) plus a scalar k * 256 * chunk
+    // bytes, with the hardware range check returning zero past the body.
+    constexpr int64_t CB = 4 * (int64_t)sizeof(T);  // chunk bytes
+    const int64_t kmain = n4 / 256;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<T*>(body), 0, (int)(n4 * CB), 0x00020000);
+    const int vofs = (int)(t * CB);
+    auto chunk = [&](int64_t k) { return SRC::bload(rsrc, vofs, (int)(k * 256 * CB)); };
+    auto fold = [&](const typename SRC::Raw& raw) {
+        int qq[4];
+        SRC::unpack(raw, qq);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc = pair(acc, qq[i], tab);
+    };
+    if (kmain > 0) {
+        {
+            int qq[4];
+            SRC::unpack(chunk(0), qq);
+            acc = has ? pair(acc, qq[0], tab) : qq[0];
+            has = true;
+            acc = pair(acc, qq[1], tab);
+            acc = pair(acc, qq[2], tab);
+            acc = pair(acc, qq[3], tab);
+        }
+        // Two register buffers of D chunks alternate: while one is folded
+        // the other's loads are in flight.
+        typename SRC::Raw bufa[D], bufb[D];
+        int64_t k = 1;
+        if (k < kmain) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) bufa[d] = chunk(k + d);
+            for (;;) {
+#pragma unroll
+                for (int d = 0; d < D; ++d) bufb[d] = chunk(k + D + d);
+#pragma unroll
+                for (int d = 0; d < D; ++d)
+                    if (k + d < kmain) fold(bufa[d]);
+                k += D;
+                if (k >= kmain) break;
+#pragma unroll
+                for (int d = 0; d < D; ++d) bufa[d] = chunk(k + D + d);
+#pragma unroll
+                for (int d = 0; d < D; ++d)
+                    if (k + d < kmain) fold(bufb[d]);
+                k += D;
+                if (k >= kmain) break;
+            }
+        }
+    }
+    if (t < n4 - kmain * 256) {
+        int qq[4];
+        SRC::unpack(chunk(kmain), qq);
+        acc = has ? pair(acc, qq[0], tab) : qq[0];
+        has = true;
+        acc = pair(acc, qq[1], tab);
+        acc = pair(acc, qq[2], tab);
+        acc = pair(acc, qq[3], tab);
+    }
+    if (t < tail) {
+        const int q = SRC::one(body + 4 * n4 + t);
+        acc = has ? pair(acc, q, tab) : q;
+    }
+    // virtual-warp butterfly (xor 16, 8, 4, 2, 1 inside each 32-lane half)
+    acc = pair(acc, exact_xor<16>(acc), tab);
+    acc = pair(acc, exact_xor<8>(acc), tab);
+    acc = pair(acc, exact_xor<4>(acc), tab);
+    acc = pair(acc, exact_xor<2>(acc), tab);
+    acc = pair(acc, exact_xor<1>(acc), tab);
+    if ((t & 31) == 0) sh_warp[t >> 5] = acc;
+    __syncthreads();
+    int v = kQNegInf;
+    if (t < 64) {
+        v = (t & 31) < 8 ? sh_warp[t & 31] : kQNegInf;
+        v = pair(v, exact_xor<16>(v), tab);
+        v = pair(v, exact_xor<8>(v), tab);
+        v = pair(v, exact_xor<4>(v), tab);
+        v = pair(v, exact_xor<2>(v), tab);
+        v = pair(v, exact_xor<1>(v), tab);
+    }
+    __syncthreads();  // sh_warp is reused by the next row
+    return v;
+}
+
+template <typename SRC, bool USE_LUT>
+__global__ __launch_bounds__(256) void intlse_q16_rows(const typename SRC::T* __restrict__ x, float* __restrict__ out,
+                                                       int32_t* __restrict__ acc_out, int64_t B, int64_t N) {
+    __shared__ int lut[64];
+    __shared__ int sh_warp[8];
+    if (threadIdx.x < 64) lut[threadIdx.x] = kLutQ16[threadIdx.x];
+    __syncthreads();
+    auto pair = [](int a, int b, const int* t) { return q16_pair<USE_LUT>(a, b, t); };
+    for (int64_t row = blockIdx.x; row < B; row += gridDim.x) {
+        const int v = tree_row<SRC, 16, kPrefetch>(x + row * N, N, lut, pair, sh_warp);
+        if (threadIdx.x == 0) {
+            out[row] = (float)v * kQ16Out;
+            if (acc_out) acc_out[row] = v;
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void intlse_q10_6_rows(const int16_t* __restrict__ x, float* __restrict__ out,
+                                                         int32_t* __restrict__ acc_out, int64_t B, int64_t N) {
+    __shared__ int gap[386];
+    __shared__ int sh_warp[8];
+    // gap[d] = M + LUT[M & 63], M = (64 + ((-d) & 63)) >> ceil(d / 64), for d <= 384
+    for (int d = threadIdx.x; d < 386; d += 256) {
+        int g = 0;
+        if (d <= 384) {
+            const int sub = -d;
+            const uint32_t sh = (uint32_t)(-(sub >> 6));
+            const int m = (int)((64u | ((uint32_t)sub & 63u)) >> (sh < 31u ? sh : 31u));
+            g = m + kLutQ10[m & 63];
+        }
+        gap[d] = g;
+    }
+    __syncthreads();
+    for (int64_t row = blockIdx.x; row < B; row += gridDim.x) {
+        const int v = tree_row<SrcI16, 8, kPrefetch>(x + row * N, N, gap, q10_pair, sh_warp);
+        if (threadIdx.x == 0) {
+            out[row] = (float)v * kQ10Out;
+            if (acc_out) acc_out[row] = v;
+        }
+    }
+}
+
+static unsigned row_grid(int64_t B) { return (unsigned)(B < ((int64_t)1 << 30) ? B : ((int64_t)1 << 30)); }
+
+template <typename T>
+static int int_entry_check(const char* name, const T* x, float* out, int64_t B, int64_t N) {
+    FL_CHECK(B >= 0 && N >= 0, "%s: negative shape (B=%lld, N=%lld)", name, (long long)B, (long long)N);
+    if (B == 0) return ok();
+    FL_CHECK(out != nullptr, "%s: out is NULL", name);
+    FL_CHECK(x != nullptr || N == 0, "%s: x is NULL", name);
+    FL_CHECK((reinterpret_cast<uintptr_t>(x) % sizeof(T)) == 0, "%s: x is not element-aligned", name);
+    if (N * (int64_t)sizeof(T) >= ((int64_t)1 << 31))
+        return set_error(FL_ERANGE, "%s: rows of %lld elements exceed the 2 GiB buffer range", name, (long long)N);
+    return ok();
+}
+
+}  // namespace fl
+
+using namespace fl;
+
+extern "C" int fl_intlse_q16_f32(const float* x, float* out, int32_t* acc_out, int64_t B, int64_t N, int use_lut,
+                                 void* stream) {
+    const char* name = "fl_intlse_q16_f32";
+    if (int rc = int_entry_check(name, x, out, B, N)) return rc;
+    if (B == 0) return ok();
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (use_lut)
+        intlse_q16_rows<SrcF32, true><<<dim3(row_grid(B)), dim3(256), 0, st>>>(x, out, acc_out, B, N);
+    else
+        intlse_q16_rows<SrcF32, false><<<dim3(row_grid(B)), dim3(256), 0, st>>>(x, out, acc_out, B, N);
+    return launch_status(name);
+}
+
+extern "C" int fl_intlse_q16_i32(const int32_t* q, float* out, int32_t* acc_out, int64_t B, int64_t N, int use_lut,
+                                 void* stream) {
+    const char* name = "fl_intlse_q16_i32";
+    if (int rc = int_entry_check(name, q, out, B, N)) return rc;
+    if (B == 0) return ok();
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (use_lut)
+        intlse_q16_rows<SrcI32, true><<<dim3(row_grid(B)), dim3(256), 0, st>>>(q, out, acc_out, B, N);
+    else
+        intlse_q16_rows<SrcI32, false><<<dim3(row_grid(B)), dim3(256), 0, st>>>(q, out, acc_out, B, N);
+    return launch_status(name);
+}
+
+extern "C" int fl_intlse_q10_6(const int16_t* q, float* out, int32_t* acc_out, int64_t B, int64_t N, void* stream) {
+    const char* name = "fl_intlse_q10_6";
+    if (int rc = int_entry_check(name, q, out, B, N)) return rc;
+    if (B == 0) return ok();
+    intlse_q10_6_rows<<<dim3(row_grid(B)), dim3(256), 0, reinterpret_cast<hipStream_t>(stream)>>>(q, out, acc_out, B,
+                                                                                                  N);
+    return launch_status(name);
+}

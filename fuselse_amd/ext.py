@@ -116,3 +116,74 @@ def batched_logsumexp_bf16(x: torch.Tensor, robust: bool = False) -> torch.Tenso
     """bf16 (B, N) -> fp32 (B,) LSE with fp32 accumulation (no reference
     counterpart; the fp16 entry's contract with bf16 storage)."""
     return _fwd_half(x, torch.bfloat16, "fl_lse_fwd_bf16", "Input must be CUDA bf16", robust)
+
+
+# ---------------------------------------------------------------------------
+# IntLSE (fixed point)
+# ---------------------------------------------------------------------------
+def _acc_ptr(acc_out) -> int:
+    if acc_out is None:
+        return 0
+    _check(acc_out.is_cuda and acc_out.dtype == torch.int32 and acc_out.is_contiguous(),
+           "acc_out must be a contiguous CUDA int32 tensor")
+    return acc_out.data_ptr()
+
+
+def _intlse_q16_f32(input: torch.Tensor, use_lut: bool, acc_out=None) -> torch.Tensor:
+    # lse_kernel.cu:187-189 (the dtype/device check carries no message there)
+    _check(input.dim() == 2, "Expected 2-D tensor (B, N)")
+    _check(input.is_cuda and input.dtype == torch.float32,
+           "Expected input.is_cuda() && input.dtype() == torch::kFloat32 to be true, but got false.")
+    _check(input.is_contiguous(), "Input must be contiguous")
+    B, N = input.shape
+    out = torch.empty((B,), dtype=torch.float32, device=input.device)
+    if B == 0:
+        return out
+    with _on_device(input):
+        _lib.call("fl_intlse_q16_f32", input.data_ptr(), out.data_ptr(), _acc_ptr(acc_out), B, N, int(use_lut),
+                  _stream(input))
+    return out
+
+
+def batched_logsumexp(input: torch.Tensor, acc_out=None) -> torch.Tensor:
+    """Q16.16 IntLSE of fp32 (B, N) base-e logits -> fp32 (B,) base-e
+    (intlse/gpu/lse_kernel.cu:186-193); bit-exact reference tree."""
+    return _intlse_q16_f32(input, True, acc_out)
+
+
+def batched_logsumexp_nolut(input: torch.Tensor, acc_out=None) -> torch.Tensor:
+    """The same without the correction table (lse_kernel.cu:195-202)."""
+    return _intlse_q16_f32(input, False, acc_out)
+
+
+def batched_logsumexp_q16_i32(input: torch.Tensor, use_lut: bool = True, acc_out=None) -> torch.Tensor:
+    """Q16.16 IntLSE of pre-quantised int32 (B, N) base-2 values -> fp32 (B,)
+    base-e, with the reference's tree (no reference entry point)."""
+    _check(input.dim() == 2, "Expected 2-D tensor (B, N)")
+    _check(input.is_cuda, "Input must be CUDA")
+    _check(input.dtype == torch.int32, "Input must be int32 (Q16.16 base-2 fixed-point)")
+    _check(input.is_contiguous(), "Input must be contiguous")
+    B, N = input.shape
+    out = torch.empty((B,), dtype=torch.float32, device=input.device)
+    if B == 0:
+        return out
+    with _on_device(input):
+        _lib.call("fl_intlse_q16_i32", input.data_ptr(), out.data_ptr(), _acc_ptr(acc_out), B, N, int(use_lut),
+                  _stream(input))
+    return out
+
+
+def batched_logsumexp_q10_6(input: torch.Tensor, acc_out=None) -> torch.Tensor:
+    """Q10.6 IntLSE of int16 (B, N) base-2 values -> fp32 (B,) base-e
+    (intlse/gpu/lse_kernel_q10_6.cu:144-165, same checks and messages)."""
+    _check(input.dim() == 2, "Expected 2-D tensor (B, N)")
+    _check(input.is_cuda, "Input must be CUDA")
+    _check(input.dtype == torch.int16, "Input must be int16 (Q10.6 base-2 fixed-point)")
+    _check(input.is_contiguous(), "Input must be contiguous")
+    B, N = input.shape
+    out = torch.empty((B,), dtype=torch.float32, device=input.device)
+    if B == 0:
+        return out
+    with _on_device(input):
+        _lib.call("fl_intlse_q10_6", input.data_ptr(), out.data_ptr(), _acc_ptr(acc_out), B, N, _stream(input))
+    return out

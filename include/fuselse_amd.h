@@ -58,6 +58,26 @@ int fl_lse_bwd_f32(const float* grad, const float* x, const float* lse, float* g
 int fl_lse_fwd_f16(const void* x, float* out, int64_t B, int64_t N, int robust, void* stream);
 int fl_lse_fwd_bf16(const void* x, float* out, int64_t B, int64_t N, int robust, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * IntLSE fixed-point row LSE, bit-exact to the reference's GPU reduction tree
+ * (256 virtual threads, warp-32 butterflies).  out is fp32 base-e [B];
+ * acc_out (may be NULL) receives the final base-2 fixed-point accumulators.
+ *
+ * fl_intlse_q16_f32: fp32 input, quantised in the kernel as
+ *   rne_sat(fl32(x * 94548.4609375)); use_lut == 0 drops the correction table
+ *   (the reference's ablation).  Replaces batched_logsumexp /
+ *   batched_logsumexp_nolut (intlse/gpu/lse_kernel.cu:164-202; kernel :67-159).
+ * fl_intlse_q16_i32: the same tree over pre-quantised Q16.16 int32 input (the
+ *   reference has no int32-input entry; its kernel quantises inside the tree).
+ * fl_intlse_q10_6: Q10.6 int16 input.  Replaces batched_logsumexp_q10_6
+ *   (intlse/gpu/lse_kernel_q10_6.cu:144-165; kernel :55-139).
+ * ------------------------------------------------------------------------- */
+int fl_intlse_q16_f32(const float* x, float* out, int32_t* acc_out, int64_t B, int64_t N, int use_lut,
+                      void* stream);
+int fl_intlse_q16_i32(const int32_t* q, float* out, int32_t* acc_out, int64_t B, int64_t N, int use_lut,
+                      void* stream);
+int fl_intlse_q10_6(const int16_t* q, float* out, int32_t* acc_out, int64_t B, int64_t N, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
