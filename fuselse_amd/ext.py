@@ -187,3 +187,76 @@ def batched_logsumexp_q10_6(input: torch.Tensor, acc_out=None) -> torch.Tensor:
     with _on_device(input):
         _lib.call("fl_intlse_q10_6", input.data_ptr(), out.data_ptr(), _acc_ptr(acc_out), B, N, _stream(input))
     return out
+
+
+# ---------------------------------------------------------------------------
+# Sparse probabilistic-circuit sum layers
+# ---------------------------------------------------------------------------
+def _sparse_blocked(node_mars, element_mars, params, nids, cids, pids, block_size, q16, params_are_log):
+    # sparse_float_kernel.cu:119-121 / sparse_q16_kernel.cu:320-322
+    _check(node_mars.is_cuda, "node_mars must be CUDA")
+    _check(element_mars.is_cuda, "element_mars must be CUDA")
+    _check(params.is_cuda, "params must be CUDA")
+    # layout checks the reference leaves to the caller (a mismatch would read
+    # out of bounds on the device)
+    _check(node_mars.dtype == torch.float32 and element_mars.dtype == torch.float32 and params.dtype == torch.float32,
+           "node_mars, element_mars and params must be float32")
+    _check(node_mars.dim() == 2 and element_mars.dim() == 2 and node_mars.size(1) == element_mars.size(1),
+           "node_mars and element_mars must be 2-D [nodes, batch] with the same batch")
+    _check(node_mars.is_contiguous() and element_mars.is_contiguous() and params.is_contiguous(),
+           "node_mars, element_mars and params must be contiguous")
+    for name, t in (("nids", nids), ("cids", cids), ("pids", pids)):
+        _check(t.is_cuda and t.dtype == torch.int64 and t.is_contiguous(), f"{name} must be a contiguous CUDA int64 tensor")
+    _check(cids.dim() == 2 and pids.shape == cids.shape and nids.dim() == 1 and nids.size(0) == cids.size(0),
+           "nids [nblocks], cids and pids [nblocks, num_edges] shapes disagree")
+    batch = node_mars.size(1)
+    num_nblocks = nids.size(0)
+    num_edges = cids.size(1)
+    if batch == 0 or num_nblocks == 0 or block_size == 0:
+        return None
+    with _on_device(node_mars):
+        _lib.call("fl_sparse_blocked_fwd", node_mars.data_ptr(), element_mars.data_ptr(), params.data_ptr(),
+                  nids.data_ptr(), cids.data_ptr(), pids.data_ptr(), num_nblocks, num_edges, int(block_size), batch,
+                  int(q16), int(params_are_log), _stream(node_mars))
+    return None
+
+
+def sparse_forward_float(node_mars, element_mars, params, nids, cids, pids, block_size, params_are_log=False):
+    """pyjuice sum-layer forward in fp32, in place on node_mars
+    (experiment_pyjuice/sparse_float_kernel.cu:110-167):
+    node_mars[nids[j] + p, b] = LSE_e(log max(params[pids[j, e] + p], 1e-45)
+    + element_mars[cids[j, e], b]).  Returns None."""
+    return _sparse_blocked(node_mars, element_mars, params, nids, cids, pids, block_size, False, params_are_log)
+
+
+def sparse_forward_q16(node_mars, element_mars, params, nids, cids, pids, block_size, params_are_log=False):
+    """The same in IntLSE Q16.16 with the reference's edge-thread tree
+    (experiment_pyjuice/sparse_q16_kernel.cu:139-202).  Returns None."""
+    return _sparse_blocked(node_mars, element_mars, params, nids, cids, pids, block_size, True, params_are_log)
+
+
+def sparse_csr_forward(child, offsets, child_ids, logparams, q16=False, out=None):
+    """CSR sum layer: out[n, b] = LSE_{e in [offsets[n], offsets[n+1])}
+    (logparams[e] + child[child_ids[e], b]); -inf for a node without edges.
+    child: fp32 [num_children, batch]; offsets int64 [num_nodes + 1];
+    child_ids int32 [nnz]; logparams fp32 [nnz].  Returns out [num_nodes, batch]."""
+    _check(child.is_cuda and child.dtype == torch.float32 and child.dim() == 2 and child.is_contiguous(),
+           "child must be a contiguous CUDA float32 [num_children, batch] tensor")
+    _check(offsets.is_cuda and offsets.dtype == torch.int64 and offsets.dim() == 1 and offsets.is_contiguous(),
+           "offsets must be a contiguous CUDA int64 [num_nodes + 1] tensor")
+    _check(child_ids.is_cuda and child_ids.dtype == torch.int32 and child_ids.is_contiguous(),
+           "child_ids must be a contiguous CUDA int32 tensor")
+    _check(logparams.is_cuda and logparams.dtype == torch.float32 and logparams.is_contiguous()
+           and logparams.numel() == child_ids.numel(), "logparams must be contiguous CUDA float32, one per edge")
+    num_nodes = offsets.numel() - 1
+    batch = child.size(1)
+    if out is None:
+        out = torch.empty((max(num_nodes, 0), batch), dtype=torch.float32, device=child.device)
+    _check(out.is_cuda and out.dtype == torch.float32 and out.is_contiguous() and tuple(out.shape) == (num_nodes, batch),
+           "out must be a contiguous CUDA float32 [num_nodes, batch] tensor")
+    if num_nodes <= 0 or batch == 0:
+        return out
+    with _on_device(child):
+        _lib.call("fl_sparse_csr_fwd", child.data_ptr(), offsets.data_ptr(), child_ids.data_ptr(), logparams.data_ptr(),
+                  out.data_ptr(), num_nodes, batch, int(q16), _stream(child))
+    return out

@@ -78,6 +78,30 @@ int fl_intlse_q16_i32(const int32_t* q, float* out, int32_t* acc_out, int64_t B,
                       void* stream);
 int fl_intlse_q10_6(const int16_t* q, float* out, int32_t* acc_out, int64_t B, int64_t N, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Sparse probabilistic-circuit sum layer: out[n, b] = log sum_e exp(logw_e +
+ * child[c_e, b]) over node n's edges.  Node values are row-major [node][batch]
+ * fp32.  q16 != 0 runs the IntLSE Q16.16 arithmetic with the reference's
+ * edge-thread tree (bit-exact); q16 == 0 runs fp32.  A node without edges
+ * gives -inf.
+ *
+ * fl_sparse_csr_fwd: CSR edges; offsets int64 [num_nodes + 1], child_ids
+ *   int32 [nnz] (rows of child [num_children][batch]), logparams fp32 [nnz].
+ *   Writes out [num_nodes][batch].  (The reference has no CSR entry point.)
+ * fl_sparse_blocked_fwd: the pyjuice block layout, in place on node_mars:
+ *   node block j (nids int64 [num_nblocks]) of block_size parents p writes
+ *   node_mars[nids[j] + p, :] from children cids int64 [num_nblocks, num_edges]
+ *   with weights params[pids[j, e] + p] (linear weights, log taken with a
+ *   1e-45 floor, or log-weights when params_are_log != 0).  Replaces
+ *   sparse_forward_float / sparse_forward_q16 (experiment_pyjuice/
+ *   sparse_float_kernel.cu:110-167, sparse_q16_kernel.cu:139-202).
+ * ------------------------------------------------------------------------- */
+int fl_sparse_csr_fwd(const float* child, const int64_t* offsets, const int32_t* child_ids, const float* logparams,
+                      float* out, int64_t num_nodes, int64_t batch, int q16, void* stream);
+int fl_sparse_blocked_fwd(float* node_mars, const float* element_mars, const float* params, const int64_t* nids,
+                          const int64_t* cids, const int64_t* pids, int64_t num_nblocks, int64_t num_edges,
+                          int64_t block_size, int64_t batch, int q16, int params_are_log, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
