@@ -119,12 +119,102 @@ def cpu_baseline(max_rows=512):
     }
 
 
+def _time_calls(torch, stream, fn, nbuf, iters):
+    """Average per-call duration (ms) of fn(i), buffers rotating i % nbuf,
+    HIP events on the kernels' stream."""
+    for i in range(max(3, nbuf)):
+        fn(i)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for i in range(iters):
+        fn(i)
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / iters
+
+
+def measure_configs(torch, ext, dev, stream, iters=50):
+    """The other BASELINE configs: fp16/bf16 forward (C3), IntLSE Q16.16 fp32 /
+    int32 and Q10.6 int16 (C4), sparse PC at 1M nodes (C5).  Each input set
+    rotates over enough buffers to exceed twice the 256 MB Infinity Cache."""
+    import numpy as np
+
+    res = {}
+
+    def rec(name, ms, nbytes, **extra):
+        gbps = nbytes / (ms * 1e-3) / 1e9
+        res[name] = {"us": round(ms * 1e3, 2), "gbps": round(gbps, 1), "pct_peak": round(100 * gbps * 1e9 / HBM_PEAK, 2),
+                     "bytes": int(nbytes), **extra}
+        log(f"{name}: {ms * 1e3:.2f} us, {gbps:.1f} GB/s")
+
+    def nbuf_for(nbytes):
+        return max(2, int(np.ceil(2 * 256e6 / nbytes)) + 1)
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    # C3: half-precision inputs, x ~ N(0, 2^2)
+    for (b, n) in [(4096, 32000), (2048, 128256), (65536, 256)]:
+        for dt, fn, tag in [(torch.float16, ext.batched_logsumexp_fp16, "fp16"),
+                            (torch.bfloat16, ext.batched_logsumexp_bf16, "bf16")]:
+            nb = nbuf_for(2 * b * n)
+            bufs = [(torch.randn(b, n, device=dev, generator=gen) * 2).to(dt) for _ in range(nb)]
+            ms = _time_calls(torch, stream, lambda i: fn(bufs[i % nb]), nb, iters)
+            rec(f"C3_{tag}_fwd_{b}x{n}", ms, 2 * b * n + 4 * b)
+            del bufs
+    # C4: IntLSE fixed point
+    b, n = 512, 128256
+    nb = 3
+    xs = [torch.randn(b, n, device=dev, generator=gen) * 2 for _ in range(nb)]
+    ms = _time_calls(torch, stream, lambda i: ext.batched_logsumexp(xs[i % nb]), nb, iters)
+    rec("C4_q16_f32in_512x128256", ms, 4 * b * n + 4 * b)
+    ms = _time_calls(torch, stream, lambda i: ext.batched_logsumexp_nolut(xs[i % nb]), nb, iters)
+    rec("C4_q16_f32in_nolut_512x128256", ms, 4 * b * n + 4 * b)
+    qs = [torch.clamp(torch.round(x * 94548.4609375), -2 ** 31, 2 ** 31 - 1).to(torch.int32) for x in xs]
+    del xs
+    ms = _time_calls(torch, stream, lambda i: ext.batched_logsumexp_q16_i32(qs[i % nb]), nb, iters)
+    rec("C4_q16_i32in_512x128256", ms, 4 * b * n + 4 * b)
+    del qs
+    b, n = 1024, 32000
+    nb = nbuf_for(2 * b * n)
+    q6 = [torch.clamp(torch.round(torch.randn(b, n, device=dev, generator=gen) * 2 * 92.33248),
+                      -32768, 32767).to(torch.int16) for _ in range(nb)]
+    ms = _time_calls(torch, stream, lambda i: ext.batched_logsumexp_q10_6(q6[i % nb]), nb, iters)
+    rec("C4_q10_6_i16in_1024x32000", ms, 2 * b * n + 4 * b)
+    del q6
+    # C5: sparse PC, 1M sum nodes, power-law fan-in (alpha = 2) on [2, 256], batch 512
+    sys.path.insert(0, ROOT)
+    nodes, batch = 1_000_000, 512
+    rng = np.random.default_rng(11)
+    ks = np.arange(2, 257)
+    pk = ks.astype(np.float64) ** -2.0
+    fan = rng.choice(ks, size=nodes, p=pk / pk.sum())
+    off = np.concatenate([[0], np.cumsum(fan)]).astype(np.int64)
+    nnz = int(off[-1])
+    lp = rng.standard_normal(nnz)
+    seg = np.maximum.reduceat(lp, off[:-1])
+    lp = lp - np.repeat(seg + np.log(np.add.reduceat(np.exp(lp - np.repeat(seg, fan)), off[:-1])), fan)
+    child = torch.log(torch.rand(nodes, batch, device=dev, generator=gen).clamp_min_(1e-30))
+    d_off = torch.from_numpy(off).to(dev)
+    d_cid = torch.randint(0, nodes, (nnz,), device=dev, generator=gen, dtype=torch.int32)
+    d_lp = torch.from_numpy(lp.astype(np.float32)).to(dev)
+    out = torch.empty(nodes, batch, device=dev)
+    sbytes = nnz * batch * 4 + nnz * 8 + (nodes + 1) * 8 + nodes * batch * 4
+    for q16, tag in [(False, "fp32"), (True, "q16")]:
+        ms = _time_calls(torch, stream, lambda i: ext.sparse_csr_forward(child, d_off, d_cid, d_lp, q16=q16, out=out),
+                         1, max(5, iters // 5))
+        rec(f"C5_sparse_csr_{tag}_1M_nodes_b512", ms, sbytes, nnz=nnz, alpha=2.0)
+    del child, out
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-configs", action="store_true", help="skip the other BASELINE configs")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also launch one plain 1 GiB device copy (counter calibration runs)")
     args = ap.parse_args()
@@ -236,6 +326,10 @@ def main():
     except (OSError, ValueError):
         pass
 
+    configs = None
+    if not args.no_configs:
+        configs = measure_configs(torch, ext, dev, stream)
+
     cpu = None
     if not args.no_cpu:
         log("cpu baseline ...")
@@ -271,6 +365,7 @@ def main():
                          "achieved": round(fwd_gbps, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                          "frac": round(fwd_gbps * 1e9 / HBM_PEAK, 4)},
         "cpu_baseline": cpu,
+        "other_configs": configs,
     }
     print(json.dumps(out), flush=True)
 

@@ -1,0 +1,134 @@
+"""CPU tests of the drop-in's dispatch (fuselse/gpu/autograd.py:6-61) with a
+fake extension and a tensor subclass that reports is_cuda=True.
+
+They pin which function runs for which input (kernel vs torch fallback), the
+shapes handed to the kernel (2-D contiguous rows), keepdim, the autograd path
+(forward saves (rows, lse); backward flattens grad_output) and the factory's
+robust switch, without a GPU."""
+
+import pytest
+import torch
+
+from fuselse_amd.autograd import make_fuselse_logsumexp
+
+
+class FakeCuda(torch.Tensor):
+    @property
+    def is_cuda(self):
+        return True
+
+
+def fake(t):
+    return t.as_subclass(FakeCuda)
+
+
+class FakeExt:
+    def __init__(self):
+        self.calls = []
+
+    def _rec(self, name, *args):
+        self.calls.append((name, [tuple(a.shape) for a in args], [a.is_contiguous() for a in args]))
+
+    def onepass_lse_float(self, x):
+        self._rec("fwd", x)
+        assert x.dim() == 2 and x.is_contiguous()
+        return torch.logsumexp(x.as_subclass(torch.Tensor), -1).as_subclass(FakeCuda)
+
+    def onepass_lse_float_robust(self, x):
+        self._rec("fwd_robust", x)
+        assert x.dim() == 2 and x.is_contiguous()
+        return torch.logsumexp(x.as_subclass(torch.Tensor), -1).as_subclass(FakeCuda)
+
+    def onepass_lse_float_backward(self, g, x, lse):
+        self._rec("bwd", g, x, lse)
+        assert g.dim() == 1 and x.dim() == 2 and lse.dim() == 1
+        gt, xt, lt = (t.as_subclass(torch.Tensor) for t in (g, x, lse))
+        return (gt[:, None] * torch.exp(xt - lt[:, None])).as_subclass(FakeCuda)
+
+
+def test_robust_flag_selects_forward():
+    ext = FakeExt()
+    make_fuselse_logsumexp(ext, robust=True)(fake(torch.randn(3, 5)))
+    make_fuselse_logsumexp(ext, robust=False)(fake(torch.randn(3, 5)))
+    assert [c[0] for c in ext.calls] == ["fwd_robust", "fwd"]
+
+
+def test_2d_contiguous_goes_straight_to_the_kernel():
+    ext = FakeExt()
+    lse = make_fuselse_logsumexp(ext)
+    x = torch.randn(4, 9)
+    y = lse(fake(x))
+    assert ext.calls == [("fwd_robust", [(4, 9)], [True])]
+    torch.testing.assert_close(y.as_subclass(torch.Tensor), torch.logsumexp(x, -1))
+
+
+def test_nd_and_noncontiguous_inputs_are_flattened():
+    ext = FakeExt()
+    lse = make_fuselse_logsumexp(ext)
+    x = torch.randn(2, 3, 7)
+    y = lse(fake(x), dim=2)
+    assert ext.calls[-1][1] == [(6, 7)] and y.shape == (2, 3)
+    xt = torch.randn(7, 5).t()
+    y = lse(fake(xt), -1)
+    assert ext.calls[-1][1] == [(5, 7)] and ext.calls[-1][2] == [True]
+    torch.testing.assert_close(y.as_subclass(torch.Tensor), torch.logsumexp(xt, -1))
+
+
+def test_keepdim():
+    ext = FakeExt()
+    lse = make_fuselse_logsumexp(ext)
+    assert lse(fake(torch.randn(4, 6)), -1, keepdim=True).shape == (4, 1)
+    assert lse(fake(torch.randn(2, 4, 6)), dim=-1, keepdim=True).shape == (2, 4, 1)
+
+
+@pytest.mark.parametrize("case", ["cpu", "fp64", "fp16", "dim0", "n1", "middle_dim"])
+def test_fallbacks_do_not_touch_the_extension(case):
+    ext = FakeExt()
+    lse = make_fuselse_logsumexp(ext)
+    x = {
+        "cpu": torch.randn(3, 4),
+        "fp64": fake(torch.randn(3, 4, dtype=torch.float64)),
+        "fp16": fake(torch.randn(3, 4).half()),
+        "dim0": fake(torch.randn(3, 4)),
+        "n1": fake(torch.randn(3, 1)),
+        "middle_dim": fake(torch.randn(2, 3, 4)),
+    }[case]
+    dim = {"dim0": 0, "middle_dim": 1}.get(case, -1)
+    y = lse(x, dim=dim)
+    assert ext.calls == []
+    want = torch.logsumexp(x.as_subclass(torch.Tensor).float(), dim=dim)
+    torch.testing.assert_close(y.as_subclass(torch.Tensor).float(), want, rtol=1e-3, atol=1e-3)
+
+
+def test_factory_captures_torch_logsumexp_so_patching_does_not_recurse(monkeypatch):
+    ext = FakeExt()
+    lse = make_fuselse_logsumexp(ext)
+    monkeypatch.setattr(torch, "logsumexp", lse)
+    x = torch.randn(3, 4)  # CPU -> fallback to the captured original
+    torch.testing.assert_close(lse(x, -1), torch.log(torch.exp(x).sum(-1)))
+
+
+def test_autograd_path_saves_rows_and_flattens_grad():
+    ext = FakeExt()
+    lse = make_fuselse_logsumexp(ext)
+    x = torch.randn(2, 3, 6, requires_grad=True)
+    xf = fake(x)
+    y = lse(xf, -1)
+    assert y.shape == (2, 3)
+    assert ext.calls[0][1] == [(6, 6)]
+    w = torch.randn(2, 3)
+    (y.as_subclass(torch.Tensor) * w).sum().backward()
+    name, shapes, _ = ext.calls[-1]
+    assert name == "bwd" and shapes == [(6,), (6, 6), (6,)]
+    x2 = x.detach().clone().requires_grad_(True)
+    (torch.logsumexp(x2, -1) * w).sum().backward()
+    torch.testing.assert_close(x.grad, x2.grad)
+
+
+def test_no_grad_uses_direct_path():
+    ext = FakeExt()
+    lse = make_fuselse_logsumexp(ext)
+    x = torch.randn(3, 4, requires_grad=True)
+    with torch.no_grad():
+        lse(fake(x))
+    assert [c[0] for c in ext.calls] == ["fwd_robust"]
