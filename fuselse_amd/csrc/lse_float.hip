@@ -132,10 +132,10 @@ static void launch_fwd(const T* x, float* out, int64_t B, int64_t N, hipStream_t
     if (grid > (int64_t)1 << 30) grid = (int64_t)1 << 30;
     const dim3 g((unsigned)grid), blk(256);
     switch (lpr) {
-    case 4: lse_fwd_group_rows<T, ROBUST, 4, 2><<<g, blk, 0, st>>>(x, out, B, N); break;
-    case 8: lse_fwd_group_rows<T, ROBUST, 8, 2><<<g, blk, 0, st>>>(x, out, B, N); break;
-    case 16: lse_fwd_group_rows<T, ROBUST, 16, 2><<<g, blk, 0, st>>>(x, out, B, N); break;
-    case 32: lse_fwd_group_rows<T, ROBUST, 32, 2><<<g, blk, 0, st>>>(x, out, B, N); break;
+    case 4: lse_fwd_group_rows<T, ROBUST, 4, 4><<<g, blk, 0, st>>>(x, out, B, N); break;
+    case 8: lse_fwd_group_rows<T, ROBUST, 8, 4><<<g, blk, 0, st>>>(x, out, B, N); break;
+    case 16: lse_fwd_group_rows<T, ROBUST, 16, 4><<<g, blk, 0, st>>>(x, out, B, N); break;
+    case 32: lse_fwd_group_rows<T, ROBUST, 32, 4><<<g, blk, 0, st>>>(x, out, B, N); break;
     default: lse_fwd_group_rows<T, ROBUST, 64, 4><<<g, blk, 0, st>>>(x, out, B, N); break;
     }
 }

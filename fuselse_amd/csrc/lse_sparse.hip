@@ -10,16 +10,16 @@
 //     j of block_size parents p shares the child ids cids[j, :]; parent p takes
 //     weight params[pids[j, e] + p]; it writes node_mars[nids[j] + p, :].
 // Node values are [node][batch] rows, so each edge gathers one contiguous
-// child row of `batch` floats.
+// child row.
 //
-// Mapping: one wave per (node, batch tile of 64*VB columns); lane l owns
-// columns 4*(l + 64 v) .. +3 (16-byte vectors) when the batch is a multiple of
-// 4 and the rows are 16-byte aligned, else columns l + 64 v (scalars).  Edge
-// metadata is loaded once per 64 edges into lanes and broadcast per edge with
-// readlane, so the edge loop issues only the child-row loads, G edges at a
-// time.
+// Mapping: one wave per (node, 256-column tile); lane l owns 4 columns (one
+// 16-byte vector when the batch is a multiple of 4 and rows are 16-byte
+// aligned, else 4 strided scalars).  Edge metadata is held one 64-edge window
+// at a time across the lanes and broadcast per edge with readlane; child rows
+// are loaded G = 4 edges at a time into two alternating register buffers, so
+// the next group's loads are in flight while a group folds.
 //
-// fp32: an online (max, scaled sum) per column with one rescale per G edges.
+// fp32: an online (max, scaled sum) per column with one rescale per group.
 // Q16.16: bit-exact with the reference's reduction: ET = 1, 2, 4, 8 chains
 // for fan-in <= 8, 16, 32, above (sparse_q16_kernel.cu:161-165), chain et folds
 // edges e = et, et + ET, ... in order starting from the identity -0x3fffffff,
@@ -39,7 +39,9 @@ namespace sparse {
 constexpr int kNegInfQ = -0x3fffffff;
 constexpr float kConv = 1.44269504089f * 65536.0f;
 constexpr float kOutScale = 0.69314718056f / 65536.0f;
-constexpr int G = 4;  // edges folded per group
+constexpr int G = 4;      // edges per load group
+constexpr int P = 4;      // columns per lane
+constexpr int kTile = 256;  // columns per wave
 
 __constant__ int kLut[64] = {
        0,  571,  907, 1282, 1634, 1745, 2054, 2592,
@@ -71,64 +73,57 @@ __device__ __forceinline__ int quant(float logit) {
     return q;
 }
 
-// Column ownership of one lane inside a batch tile.
-template <bool VEC, int VB>
+// The 4 columns of lane l in the tile starting at b0.
+template <bool VEC>
 struct Cols {
-    static constexpr int kPer = VEC ? 4 * VB : VB;  // columns per lane
-    static constexpr int kTile = 64 * kPer;          // columns per wave tile
-    // column index of slot i (i < kPer) for lane l in tile starting at b0
-    __device__ static __forceinline__ int64_t col(int64_t b0, int l, int i) {
-        return VEC ? b0 + 4 * (l + 64 * (i / 4)) + (i % 4) : b0 + l + 64 * i;
-    }
     __device__ static __forceinline__ void load(const float* __restrict__ row, int64_t b0, int l, int64_t batch,
-                                                float (&v)[kPer]) {
+                                                float (&v)[P]) {
         if constexpr (VEC) {
-#pragma unroll
-            for (int u = 0; u < VB; ++u) {
-                const int64_t c = b0 + 4 * (l + 64 * u);
-                if (c < batch) {
-                    f32x4 t = load_stream<f32x4>(row + c);
-                    v[4 * u] = t.x; v[4 * u + 1] = t.y; v[4 * u + 2] = t.z; v[4 * u + 3] = t.w;
-                } else {
-                    v[4 * u] = v[4 * u + 1] = v[4 * u + 2] = v[4 * u + 3] = 0.0f;
-                }
+            const int64_t c = b0 + 4 * l;
+            if (c < batch) {
+                const f32x4 t = load_stream<f32x4>(row + c);
+                v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+            } else {
+                v[0] = v[1] = v[2] = v[3] = 0.0f;
             }
         } else {
 #pragma unroll
-            for (int u = 0; u < VB; ++u) {
-                const int64_t c = b0 + l + 64 * u;
-                v[u] = c < batch ? row[c] : 0.0f;
+            for (int i = 0; i < P; ++i) {
+                const int64_t c = b0 + l + 64 * i;
+                v[i] = c < batch ? row[c] : 0.0f;
             }
         }
     }
     __device__ static __forceinline__ void store(float* __restrict__ row, int64_t b0, int l, int64_t batch,
-                                                 const float (&v)[kPer]) {
+                                                 const float (&v)[P]) {
         if constexpr (VEC) {
-#pragma unroll
-            for (int u = 0; u < VB; ++u) {
-                const int64_t c = b0 + 4 * (l + 64 * u);
-                if (c < batch) {
-                    f32x4 t;
-                    t.x = v[4 * u]; t.y = v[4 * u + 1]; t.z = v[4 * u + 2]; t.w = v[4 * u + 3];
-                    store_stream<f32x4>(t, row + c);
-                }
+            const int64_t c = b0 + 4 * l;
+            if (c < batch) {
+                f32x4 t;
+                t.x = v[0]; t.y = v[1]; t.z = v[2]; t.w = v[3];
+                store_stream<f32x4>(t, row + c);
             }
         } else {
 #pragma unroll
-            for (int u = 0; u < VB; ++u) {
-                const int64_t c = b0 + l + 64 * u;
-                if (c < batch) row[c] = v[u];
+            for (int i = 0; i < P; ++i) {
+                const int64_t c = b0 + l + 64 * i;
+                if (c < batch) row[c] = v[i];
             }
         }
     }
 };
 
-// Edge metadata of one node held across the wave: lane l keeps edge
-// (base + l) of the current 64-edge window; edge(e) broadcasts it.
-struct EdgeWindow {
-    int64_t cid;   // lane-held child id
-    float logw;    // lane-held log-weight
+// Lane-held metadata of edge (window start + lane).
+struct EdgeMeta {
+    int64_t cid;
+    float logw;
 };
+
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+    const int lo = __builtin_amdgcn_readfirstlane((int)(uint32_t)(uint64_t)v);
+    const int hi = __builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)v >> 32));
+    return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
 
 __device__ __forceinline__ int64_t bcast64(int64_t v, int lane) {
     const int lo = __builtin_amdgcn_readlane((int)(uint32_t)(uint64_t)v, lane);
@@ -139,43 +134,149 @@ __device__ __forceinline__ float bcastf(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
-// Q16.16 reduction of one node with ET chains: edges are taken in groups of
-// GS = max(4, ET) so that edge g of a group always belongs to chain g % ET;
-// every group start is a multiple of ET (windows are 64 edges).
-template <int ET, bool VEC, int VB, typename META>
-__device__ __forceinline__ void q16_chains(int64_t k, META meta, const float* __restrict__ child, int64_t batch,
-                                           int64_t b0, const int* __restrict__ lut, float (&res)[Cols<VEC, VB>::kPer]) {
-    using C = Cols<VEC, VB>;
-    constexpr int P = C::kPer;
+// ---------------------------------------------------------------------------
+// Layouts: node(n) returns a wave-uniform descriptor (edge count, output row);
+// meta(d, e) the metadata of edge e of that node (called per lane).
+// ---------------------------------------------------------------------------
+struct CsrDesc {
+    int64_t e0, k, n;
+};
+struct CsrLayout {
+    const int64_t* offsets;
+    const int32_t* cids;
+    const float* logp;
+    float* out;
+    int64_t batch;
+    __device__ __forceinline__ CsrDesc node(int64_t n) const {
+        const int64_t e0 = uniform64(offsets[n]);
+        return {e0, uniform64(offsets[n + 1]) - e0, n};
+    }
+    __device__ __forceinline__ EdgeMeta meta(const CsrDesc& d, int64_t e) const {
+        return {(int64_t)cids[d.e0 + e], logp[d.e0 + e]};
+    }
+    __device__ __forceinline__ float* out_row(const CsrDesc& d) const { return out + d.n * batch; }
+};
+
+struct BlockDesc {
+    int64_t base, k, p, row;
+};
+template <bool LOGP>
+struct BlockLayout {
+    float* node_mars;
+    const float* params;
+    const int64_t* nids;
+    const int64_t* cids;
+    const int64_t* pids;
+    int64_t num_edges, block_size, batch;
+    __device__ __forceinline__ BlockDesc node(int64_t jp) const {
+        const int64_t j = jp / block_size;
+        const int64_t p = jp - j * block_size;
+        return {j * num_edges, num_edges, p, uniform64(nids[j]) + p};
+    }
+    __device__ __forceinline__ EdgeMeta meta(const BlockDesc& d, int64_t e) const {
+        const float w = params[pids[d.base + e] + d.p];
+        // log of the linear weight with the reference's 1e-45 floor
+        // (sparse_float_kernel.cu:76), accurate libm log once per edge
+        return {cids[d.base + e], LOGP ? w : logf(fmaxf(w, 1e-45f))};
+    }
+    __device__ __forceinline__ float* out_row(const BlockDesc& d) const { return node_mars + d.row * batch; }
+};
+
+// ---------------------------------------------------------------------------
+// Per-node reductions over one 256-column tile.
+// ---------------------------------------------------------------------------
+template <int GS, bool VEC>
+__device__ __forceinline__ void load_group(float (&v)[GS][P], const EdgeMeta& ew, int j, int wn,
+                                           const float* __restrict__ child, int64_t batch, int64_t b0, int l) {
+#pragma unroll
+    for (int g = 0; g < GS; ++g)
+        if (j + g < wn) Cols<VEC>::load(child + bcast64(ew.cid, j + g) * batch, b0, l, batch, v[g]);
+}
+
+__device__ __forceinline__ void fold_group_f32(const float (&v)[G][P], const EdgeMeta& ew, int j, int wn,
+                                               float (&m)[P], float (&s)[P]) {
+    float lw[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) lw[g] = j + g < wn ? bcastf(ew.logw, j + g) : -kInf;
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+        float col[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) col[g] = j + g < wn ? v[g][i] + lw[g] : -kInf;
+        lse_fold<true, G>(m[i], s[i], col);
+    }
+}
+
+template <int ET, int GS>
+__device__ __forceinline__ void fold_group_q16(const float (&v)[GS][P], const EdgeMeta& ew, int j, int wn,
+                                               int (&acc)[ET][P], const int* __restrict__ lut) {
+#pragma unroll
+    for (int g = 0; g < GS; ++g) {
+        if (j + g < wn) {
+            const float lw = bcastf(ew.logw, j + g);
+#pragma unroll
+            for (int i = 0; i < P; ++i) acc[g % ET][i] = pair(acc[g % ET][i], quant(lw + v[g][i]), lut);
+        }
+    }
+}
+
+// Walks the node's edges in 64-edge windows; groups of GS edges alternate
+// between two register buffers (loads of group g+1 in flight while group g
+// folds).  FOLD(buf, j, wn, ew) folds group starting at window edge j.
+template <int GS, bool VEC, typename LAYOUT, typename DESC, typename FOLD>
+__device__ __forceinline__ void walk_edges(const LAYOUT& L, const DESC& d, const EdgeMeta& first,
+                                           const float* __restrict__ child, int64_t batch, int64_t b0, int l,
+                                           FOLD fold) {
+    for (int64_t w0 = 0; w0 < d.k; w0 += 64) {
+        const EdgeMeta ew = w0 == 0 ? first : (w0 + l < d.k ? L.meta(d, w0 + l) : EdgeMeta{0, 0.0f});
+        const int wn = (int)(d.k - w0 < 64 ? d.k - w0 : 64);
+        const int ng = (wn + GS - 1) / GS;
+        float va[GS][P], vb[GS][P];
+        load_group<GS, VEC>(va, ew, 0, wn, child, batch, b0, l);
+        for (int gi = 0; gi < ng; gi += 2) {
+            if (gi + 1 < ng) load_group<GS, VEC>(vb, ew, (gi + 1) * GS, wn, child, batch, b0, l);
+            fold(va, gi * GS, wn, ew);
+            if (gi + 1 >= ng) break;
+            if (gi + 2 < ng) load_group<GS, VEC>(va, ew, (gi + 2) * GS, wn, child, batch, b0, l);
+            fold(vb, (gi + 1) * GS, wn, ew);
+        }
+    }
+}
+
+template <bool VEC, typename LAYOUT, typename DESC>
+__device__ __forceinline__ void reduce_f32(const LAYOUT& L, const DESC& d, const EdgeMeta& first,
+                                           const float* __restrict__ child, int64_t batch, int64_t b0, int l) {
+    float m[P], s[P];
+#pragma unroll
+    for (int i = 0; i < P; ++i) { m[i] = -kInf; s[i] = 0.0f; }
+    walk_edges<G, VEC>(L, d, first, child, batch, b0, l,
+                       [&](const float (&v)[G][P], int j, int wn, const EdgeMeta& ew) { fold_group_f32(v, ew, j, wn, m, s); });
+    float res[P];
+#pragma unroll
+    for (int i = 0; i < P; ++i) res[i] = lse_finish<true>(m[i], s[i]);
+    Cols<VEC>::store(L.out_row(d), b0, l, batch, res);
+}
+
+template <int ET, bool VEC, typename LAYOUT, typename DESC>
+__device__ __forceinline__ void reduce_q16_et(const LAYOUT& L, const DESC& d, const EdgeMeta& first,
+                                              const float* __restrict__ child, int64_t batch, int64_t b0, int l,
+                                              const int* __restrict__ lut) {
+    // group start edges are multiples of GS (and of 64 across windows), so
+    // edge g of a group belongs to chain g % ET
     constexpr int GS = ET > G ? ET : G;
-    const int l = lane_id();
     int acc[ET][P];
 #pragma unroll
     for (int c = 0; c < ET; ++c)
 #pragma unroll
         for (int i = 0; i < P; ++i) acc[c][i] = kNegInfQ;
-    for (int64_t w0 = 0; w0 < k; w0 += 64) {
-        const EdgeWindow ew = w0 + l < k ? meta(w0, l) : EdgeWindow{0, 0.0f};
-        const int wn = (int)(k - w0 < 64 ? k - w0 : 64);
-        for (int j = 0; j < wn; j += GS) {
-            const int gn = wn - j < GS ? wn - j : GS;
-            float v[GS][P];
-#pragma unroll
-            for (int g = 0; g < GS; ++g)
-                if (g < gn) C::load(child + bcast64(ew.cid, j + g) * batch, b0, l, batch, v[g]);
-#pragma unroll
-            for (int g = 0; g < GS; ++g) {
-                if (g < gn) {
-                    const float lw = bcastf(ew.logw, j + g);
-#pragma unroll
-                    for (int i = 0; i < P; ++i) acc[g % ET][i] = pair(acc[g % ET][i], quant(lw + v[g][i]), lut);
-                }
-            }
-        }
-    }
-    // xor butterfly over the chains (distances ET/2 .. 1); chain 0 ends with the result
+    walk_edges<GS, VEC>(L, d, first, child, batch, b0, l,
+                        [&](const float (&v)[GS][P], int j, int wn, const EdgeMeta& ew) {
+                            fold_group_q16<ET, GS>(v, ew, j, wn, acc, lut);
+                        });
+    float res[P];
 #pragma unroll
     for (int i = 0; i < P; ++i) {
+        // xor butterfly over the chains, distances ET/2 .. 1; chain 0 ends with the result
         if constexpr (ET >= 8) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) acc[c][i] = pair(acc[c][i], acc[c + 4][i], lut);
@@ -187,163 +288,57 @@ __device__ __forceinline__ void q16_chains(int64_t k, META meta, const float* __
         if constexpr (ET >= 2) acc[0][i] = pair(acc[0][i], acc[1][i], lut);
         res[i] = acc[0][i] > kNegInfQ ? (float)acc[0][i] * kOutScale : -kInf;
     }
+    Cols<VEC>::store(L.out_row(d), b0, l, batch, res);
 }
 
-// Reduce one node over a batch tile.  META(e0, lane) returns the EdgeWindow
-// entry for edge e0 + lane (valid for e0 + lane < k).
-template <bool Q16, bool VEC, int VB, typename META>
-__device__ __forceinline__ void reduce_node(int64_t k, META meta, const float* __restrict__ child, int64_t batch,
-                                            int64_t b0, float* __restrict__ out_row, const int* __restrict__ lut) {
-    using C = Cols<VEC, VB>;
-    constexpr int P = C::kPer;
+template <bool VEC, typename LAYOUT, typename DESC>
+__device__ __forceinline__ void reduce_q16(const LAYOUT& L, const DESC& d, const EdgeMeta& first,
+                                           const float* __restrict__ child, int64_t batch, int64_t b0, int l,
+                                           const int* __restrict__ lut) {
+    if (d.k <= 8)
+        reduce_q16_et<1, VEC>(L, d, first, child, batch, b0, l, lut);
+    else if (d.k <= 16)
+        reduce_q16_et<2, VEC>(L, d, first, child, batch, b0, l, lut);
+    else if (d.k <= 32)
+        reduce_q16_et<4, VEC>(L, d, first, child, batch, b0, l, lut);
+    else
+        reduce_q16_et<8, VEC>(L, d, first, child, batch, b0, l, lut);
+}
+
+// One wave per (node, 256-column tile): blockIdx.y is the tile, the four
+// waves of a block take four consecutive nodes.  Many small blocks let the
+// hardware balance the power-law fan-in.
+template <bool Q16, bool VEC, typename LAYOUT>
+__global__ __launch_bounds__(256) void sparse_kernel(LAYOUT L, const float* __restrict__ child, int64_t batch,
+                                                     int64_t items) {
+    __shared__ int lut[64];
+    if constexpr (Q16) {
+        if (threadIdx.x < 64) lut[threadIdx.x] = kLut[threadIdx.x];
+        __syncthreads();
+    }
     const int l = lane_id();
-    float res[P];
-    if constexpr (!Q16) {
-        float m[P], s[P];
-#pragma unroll
-        for (int i = 0; i < P; ++i) { m[i] = -kInf; s[i] = 0.0f; }
-        for (int64_t w0 = 0; w0 < k; w0 += 64) {
-            const EdgeWindow ew = w0 + l < k ? meta(w0, l) : EdgeWindow{0, 0.0f};
-            const int wn = (int)(k - w0 < 64 ? k - w0 : 64);
-            int e = 0;
-            for (; e + G <= wn; e += G) {
-                float v[G][P];
-#pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    const int64_t c = bcast64(ew.cid, e + g);
-                    C::load(child + c * batch, b0, l, batch, v[g]);
-                }
-#pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    const float lw = bcastf(ew.logw, e + g);
-#pragma unroll
-                    for (int i = 0; i < P; ++i) v[g][i] += lw;
-                }
-#pragma unroll
-                for (int i = 0; i < P; ++i) {
-                    float col[G];
-#pragma unroll
-                    for (int g = 0; g < G; ++g) col[g] = v[g][i];
-                    lse_fold<true, G>(m[i], s[i], col);
-                }
-            }
-            for (; e < wn; ++e) {
-                float v[P];
-                C::load(child + bcast64(ew.cid, e) * batch, b0, l, batch, v);
-                const float lw = bcastf(ew.logw, e);
-#pragma unroll
-                for (int i = 0; i < P; ++i) {
-                    float col[1] = {v[i] + lw};
-                    lse_fold<true, 1>(m[i], s[i], col);
-                }
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < P; ++i) res[i] = lse_finish<true>(m[i], s[i]);
-    } else {
-        const int et_n = k <= 8 ? 1 : k <= 16 ? 2 : k <= 32 ? 4 : 8;
-        switch (et_n) {
-        case 1: q16_chains<1, VEC, VB>(k, meta, child, batch, b0, lut, res); break;
-        case 2: q16_chains<2, VEC, VB>(k, meta, child, batch, b0, lut, res); break;
-        case 4: q16_chains<4, VEC, VB>(k, meta, child, batch, b0, lut, res); break;
-        default: q16_chains<8, VEC, VB>(k, meta, child, batch, b0, lut, res); break;
-        }
-    }
-    C::store(out_row, b0, l, batch, res);
+    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= items) return;
+    const auto desc = L.node(item);
+    const EdgeMeta first = l < desc.k ? L.meta(desc, l) : EdgeMeta{0, 0.0f};
+    const int64_t b0 = (int64_t)blockIdx.y * kTile;
+    if constexpr (Q16)
+        reduce_q16<VEC>(L, desc, first, child, batch, b0, l, lut);
+    else
+        reduce_f32<VEC>(L, desc, first, child, batch, b0, l);
 }
 
-template <bool Q16, bool VEC, int VB>
-__global__ __launch_bounds__(256) void csr_kernel(const float* __restrict__ child, const int64_t* __restrict__ offsets,
-                                                  const int32_t* __restrict__ cids, const float* __restrict__ logp,
-                                                  float* __restrict__ out, int64_t num_nodes, int64_t batch,
-                                                  int64_t tiles) {
-    __shared__ int lut[64];
-    if constexpr (Q16) {
-        if (threadIdx.x < 64) lut[threadIdx.x] = kLut[threadIdx.x];
-        __syncthreads();
-    }
-    const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int64_t nwaves = (int64_t)gridDim.x * 4;
-    for (int64_t w = wave; w < num_nodes * tiles; w += nwaves) {
-        const int64_t n = w / tiles;
-        const int64_t b0 = (w - n * tiles) * Cols<VEC, VB>::kTile;
-        const int64_t e0 = offsets[n];
-        const int64_t k = offsets[n + 1] - e0;
-        auto meta = [&](int64_t w0, int l) { return EdgeWindow{(int64_t)cids[e0 + w0 + l], logp[e0 + w0 + l]}; };
-        reduce_node<Q16, VEC, VB>(k, meta, child, batch, b0, out + n * batch, lut);
-    }
-}
-
-// pyjuice block layout.  LOGP: params already hold log-weights.
-template <bool Q16, bool VEC, int VB, bool LOGP>
-__global__ __launch_bounds__(256) void blocked_kernel(float* __restrict__ node_mars, const float* __restrict__ element_mars,
-                                                      const float* __restrict__ params, const int64_t* __restrict__ nids,
-                                                      const int64_t* __restrict__ cids, const int64_t* __restrict__ pids,
-                                                      int64_t num_nblocks, int64_t num_edges, int64_t block_size,
-                                                      int64_t batch, int64_t tiles) {
-    __shared__ int lut[64];
-    if constexpr (Q16) {
-        if (threadIdx.x < 64) lut[threadIdx.x] = kLut[threadIdx.x];
-        __syncthreads();
-    }
-    const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int64_t nwaves = (int64_t)gridDim.x * 4;
-    const int64_t total = num_nblocks * block_size * tiles;
-    for (int64_t w = wave; w < total; w += nwaves) {
-        const int64_t jp = w / tiles;
-        const int64_t b0 = (w - jp * tiles) * Cols<VEC, VB>::kTile;
-        const int64_t j = jp / block_size;
-        const int64_t p = jp - j * block_size;
-        auto meta = [&](int64_t w0, int l) {
-            const int64_t ge = j * num_edges + w0 + l;
-            const float wv = params[pids[ge] + p];
-            // log of the linear weight, clamped at the smallest fp32 denormal
-            // (sparse_float_kernel.cu:76); accurate libm log, once per edge
-            const float lw = LOGP ? wv : logf(fmaxf(wv, 1e-45f));
-            return EdgeWindow{cids[ge], lw};
-        };
-        reduce_node<Q16, VEC, VB>(num_edges, meta, element_mars, batch, b0, node_mars + (nids[j] + p) * batch, lut);
-    }
-}
-
-static int64_t grid_for(int64_t waves) {
-    int64_t blocks = (waves + 3) / 4;
-    const int64_t cap = (int64_t)1 << 20;  // grid-stride beyond ~1M blocks
-    return blocks < 1 ? 1 : (blocks > cap ? cap : blocks);
-}
-
-template <bool Q16>
-static void launch_csr(const float* child, const int64_t* off, const int32_t* cid, const float* lp, float* out,
-                       int64_t nodes, int64_t batch, hipStream_t st) {
-    const bool vec = (batch % 4 == 0) && ((reinterpret_cast<uintptr_t>(child) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
-    if (vec) {
-        constexpr int VB = 2;
-        const int64_t tiles = (batch + Cols<true, VB>::kTile - 1) / Cols<true, VB>::kTile;
-        csr_kernel<Q16, true, VB><<<dim3((unsigned)grid_for(nodes * tiles)), dim3(256), 0, st>>>(child, off, cid, lp, out,
-                                                                                                 nodes, batch, tiles);
-    } else {
-        constexpr int VB = 4;
-        const int64_t tiles = (batch + Cols<false, VB>::kTile - 1) / Cols<false, VB>::kTile;
-        csr_kernel<Q16, false, VB><<<dim3((unsigned)grid_for(nodes * tiles)), dim3(256), 0, st>>>(child, off, cid, lp,
-                                                                                                  out, nodes, batch, tiles);
-    }
-}
-
-template <bool Q16, bool LOGP>
-static void launch_blocked(float* nm, const float* em, const float* params, const int64_t* nids, const int64_t* cids,
-                           const int64_t* pids, int64_t nb, int64_t ne, int64_t bs, int64_t batch, hipStream_t st) {
-    const bool vec = (batch % 4 == 0) && ((reinterpret_cast<uintptr_t>(nm) | reinterpret_cast<uintptr_t>(em)) & 15) == 0;
-    if (vec) {
-        constexpr int VB = 2;
-        const int64_t tiles = (batch + Cols<true, VB>::kTile - 1) / Cols<true, VB>::kTile;
-        blocked_kernel<Q16, true, VB, LOGP><<<dim3((unsigned)grid_for(nb * bs * tiles)), dim3(256), 0, st>>>(
-            nm, em, params, nids, cids, pids, nb, ne, bs, batch, tiles);
-    } else {
-        constexpr int VB = 4;
-        const int64_t tiles = (batch + Cols<false, VB>::kTile - 1) / Cols<false, VB>::kTile;
-        blocked_kernel<Q16, false, VB, LOGP><<<dim3((unsigned)grid_for(nb * bs * tiles)), dim3(256), 0, st>>>(
-            nm, em, params, nids, cids, pids, nb, ne, bs, batch, tiles);
-    }
+template <bool Q16, typename LAYOUT>
+static void launch(const LAYOUT& L, const float* child, const float* out_any, int64_t items, int64_t batch,
+                   hipStream_t st) {
+    const bool vec = (batch % 4 == 0) &&
+                     ((reinterpret_cast<uintptr_t>(child) | reinterpret_cast<uintptr_t>(out_any)) & 15) == 0;
+    const int64_t tiles = (batch + kTile - 1) / kTile;
+    const dim3 grid((unsigned)((items + 3) / 4), (unsigned)tiles);
+    if (vec)
+        sparse_kernel<Q16, true, LAYOUT><<<grid, dim3(256), 0, st>>>(L, child, batch, items);
+    else
+        sparse_kernel<Q16, false, LAYOUT><<<grid, dim3(256), 0, st>>>(L, child, batch, items);
 }
 
 }  // namespace sparse
@@ -359,10 +354,11 @@ extern "C" int fl_sparse_csr_fwd(const float* child, const int64_t* offsets, con
     if (num_nodes == 0 || batch == 0) return ok();
     FL_CHECK(child && offsets && out, "%s: NULL pointer argument", name);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const sparse::CsrLayout L{offsets, child_ids, logparams, out, batch};
     if (q16)
-        sparse::launch_csr<true>(child, offsets, child_ids, logparams, out, num_nodes, batch, st);
+        sparse::launch<true>(L, child, out, num_nodes, batch, st);
     else
-        sparse::launch_csr<false>(child, offsets, child_ids, logparams, out, num_nodes, batch, st);
+        sparse::launch<false>(L, child, out, num_nodes, batch, st);
     return launch_status(name);
 }
 
@@ -376,12 +372,15 @@ extern "C" int fl_sparse_blocked_fwd(float* node_mars, const float* element_mars
     FL_CHECK(node_mars && element_mars && params && nids && (num_edges == 0 || (cids && pids)),
              "%s: NULL pointer argument", name);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const int sel = (q16 ? 2 : 0) | (params_are_log ? 1 : 0);
-    switch (sel) {
-    case 0: sparse::launch_blocked<false, false>(node_mars, element_mars, params, nids, cids, pids, num_nblocks, num_edges, block_size, batch, st); break;
-    case 1: sparse::launch_blocked<false, true>(node_mars, element_mars, params, nids, cids, pids, num_nblocks, num_edges, block_size, batch, st); break;
-    case 2: sparse::launch_blocked<true, false>(node_mars, element_mars, params, nids, cids, pids, num_nblocks, num_edges, block_size, batch, st); break;
-    default: sparse::launch_blocked<true, true>(node_mars, element_mars, params, nids, cids, pids, num_nblocks, num_edges, block_size, batch, st); break;
+    const int64_t items = num_nblocks * block_size;
+    if (params_are_log) {
+        const sparse::BlockLayout<true> L{node_mars, params, nids, cids, pids, num_edges, block_size, batch};
+        if (q16) sparse::launch<true>(L, element_mars, node_mars, items, batch, st);
+        else sparse::launch<false>(L, element_mars, node_mars, items, batch, st);
+    } else {
+        const sparse::BlockLayout<false> L{node_mars, params, nids, cids, pids, num_edges, block_size, batch};
+        if (q16) sparse::launch<true>(L, element_mars, node_mars, items, batch, st);
+        else sparse::launch<false>(L, element_mars, node_mars, items, batch, st);
     }
     return launch_status(name);
 }
