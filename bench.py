@@ -134,6 +134,31 @@ def _time_calls(torch, stream, fn, nbuf, iters):
     return a.elapsed_time(b) / iters
 
 
+def _time_graph(torch, fn, iters, result):
+    """Average per-call duration (ms) of fn(i, stream), i < iters, captured in
+    one HIP graph and replayed three times; and result() after the replays."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(3):
+            fn(i, s.cuda_stream)
+    s.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for i in range(iters):
+            fn(i, s.cuda_stream)
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(s):
+        a.record(s)
+        for _ in range(3):
+            g.replay()
+        b.record(s)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / (3 * iters), result()
+
+
 def measure_configs(torch, ext, dev, stream, iters=50):
     """The other BASELINE configs: fp16/bf16 forward (C3), IntLSE Q16.16 fp32 /
     int32 and Q10.6 int16 (C4), sparse PC at 1M nodes (C5).  Each input set
@@ -162,6 +187,38 @@ def measure_configs(torch, ext, dev, stream, iters=50):
             ms = _time_calls(torch, stream, lambda i: fn(bufs[i % nb]), nb, iters)
             rec(f"C3_{tag}_fwd_{b}x{n}", ms, 2 * b * n + 4 * b)
             del bufs
+    # Few long rows (fp32, robust): the split-row path (fl_lse_fwd_f32_ws, the
+    # Python shim's choice for B < 320) beside the one-block-per-row kernel of
+    # fl_lse_fwd_f32, the reference's geometry.  These calls take a few us of
+    # GPU time, less than their host-side launch cost, so each is timed by
+    # replaying a HIP graph of captured calls.
+    from fuselse_amd import _lib
+
+    lib = _lib.load()
+    n = 128256
+    for b in (1, 8, 64, 256):
+        nb = nbuf_for(4 * b * n)
+        bufs = [torch.randn(b, n, device=dev, generator=gen) * 3 for _ in range(nb)]
+        out = torch.empty(b, device=dev)
+        wsb = lib.fl_lse_fwd_workspace_bytes(b, n, 4)
+        ws = torch.empty(max(wsb, 8), dtype=torch.uint8, device=dev)
+
+        def split(i, st):
+            _lib.call("fl_lse_fwd_f32_ws", bufs[i % nb].data_ptr(), out.data_ptr(), b, n, 1, ws.data_ptr(),
+                      ws.numel(), st)
+
+        def one(i, st):
+            _lib.call("fl_lse_fwd_f32", bufs[i % nb].data_ptr(), out.data_ptr(), b, n, 1, st)
+
+        # every buffer once per replay: the replayed working set exceeds the
+        # Infinity Cache twice over
+        calls = max(iters, nb)
+        ms, ok = _time_graph(torch, split, calls, lambda: out.clone())
+        ms1, ok1 = _time_graph(torch, one, calls, lambda: out.clone())
+        want = torch.logsumexp(bufs[(calls - 1) % nb], dim=-1)
+        assert torch.allclose(ok, want, rtol=1e-5) and torch.allclose(ok1, want, rtol=1e-5), "graph replay mismatch"
+        rec(f"split_fp32_fwd_{b}x{n}", ms, 4 * b * n + 4 * b, one_pass_us=round(ms1 * 1e3, 2), workspace_bytes=wsb)
+        del bufs
     # C4: IntLSE fixed point
     b, n = 512, 128256
     nb = 3

@@ -8,6 +8,8 @@
 //   * group rows  : LPR lanes per row (4..64), 64/LPR rows per wave, for rows
 //                   of up to a few thousand vectors;
 //   * block rows  : one 256..1024-thread block per row for long rows;
+//   * split rows  : S blocks per row for few long rows, then a merge kernel
+//                   (partials in a caller workspace);
 // Backward: grad * exp2((x - lse) * log2 e), 16-byte loads and stores, with
 // grad[r] and lse[r] wave-uniform.
 #include <stdint.h>
@@ -107,6 +109,131 @@ __global__ __launch_bounds__(256) void lse_fwd_group_rows(const T* __restrict__ 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Split rows, for few long rows (one block per row would leave most of the
+// 256 CUs idle).  Two kernels on the caller's stream:
+//   * lse_fwd_split_partials, grid (S, B): block k of row r folds the body
+//     vectors [k*seg, (k+1)*seg) of row r (block 0 also its scalar head and
+//     tail) and stores its partial (m, s) in part[r*S + k];
+//   * lse_fwd_split_merge: LPR >= S lanes per row merge the S partials with a
+//     fixed tree, so the result is deterministic.
+// The kernel boundary orders the two.  (A single kernel whose last block per
+// row merges needs a device-scope release per block, which on this GPU writes
+// back the XCD's L2 each time and measured slower than the second launch.)
+// ---------------------------------------------------------------------------
+template <typename T, bool ROBUST, int THREADS, int U>
+__global__ __launch_bounds__(THREADS) void lse_fwd_split_partials(const T* __restrict__ x, int64_t N, int64_t seg,
+                                                                  float2* __restrict__ part) {
+    constexpr int VE = Elem<T>::kVec;
+    constexpr int WAVES = THREADS / 64;
+    __shared__ float sh_m[WAVES], sh_s[WAVES];
+    const int tid = threadIdx.x;
+    const int S = (int)gridDim.x;
+    const int k = (int)blockIdx.x;
+    const int64_t row = blockIdx.y;
+    const T* p = x + row * N;
+    const RowSplit sp = split_row(p, N);
+    float m = -kInf, s = 0.0f;
+    if (k == 0) {
+        if (tid < sp.head) fold_scalar<T, ROBUST>(m, s, p + tid);
+        if (tid < sp.tail) fold_scalar<T, ROBUST>(m, s, p + sp.head + sp.nvec * VE + tid);
+    }
+    const int64_t v0 = (int64_t)k * seg;
+    const int64_t v1 = v0 + seg < sp.nvec ? v0 + seg : sp.nvec;
+    fold_body<T, ROBUST, THREADS, U>(m, s, p + sp.head, v0 + tid, v1);
+    group_merge<64>(m, s);
+    if ((tid & 63) == 0) {
+        sh_m[tid >> 6] = m;
+        sh_s[tid >> 6] = s;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        m = tid < WAVES ? sh_m[tid] : -kInf;
+        s = tid < WAVES ? sh_s[tid] : 0.0f;
+        group_merge<WAVES>(m, s);
+        if (tid == 0) part[row * S + k] = make_float2(m, s);
+    }
+}
+
+// LPR lanes per row (LPR >= S), 64/LPR rows per wave, 4 waves per block.
+template <bool ROBUST, int LPR>
+__global__ __launch_bounds__(256) void lse_fwd_split_merge(const float2* __restrict__ part, float* __restrict__ out,
+                                                           int64_t B, int S) {
+    const int j = (int)(threadIdx.x % LPR);
+    const int64_t row = (int64_t)blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
+    float m = -kInf, s = 0.0f;
+    if (row < B && j < S) {
+        const float2 pv = part[row * S + j];
+        m = pv.x;
+        s = pv.y;
+    }
+    group_merge<LPR>(m, s);
+    if (j == 0 && row < B) out[row] = lse_finish<ROBUST>(m, s);
+}
+
+// The split is used for B < kSplitMaxRows and rows of more than 4096 body
+// vectors; S (<= 64) aims at kSplitBlocks blocks in all, with segments of at
+// least kSplitMinVecs vectors, rounded to whole folds of the block.  Measured
+// at N = 128256 fp32 (one-pass -> split): B=1 22.4 -> 6.4 us, B=64 24.8 ->
+// 10.1 us, B=256 28.3 -> 24.1 us; equal at B=384, one-pass ahead at B=511.
+constexpr int kSplitThreads = 256;
+constexpr int kSplitU = 2;
+constexpr int64_t kSplitMaxRows = 320;
+constexpr int64_t kSplitBlocks = 2048;
+constexpr int64_t kSplitMinVecs = 1024;
+
+struct SplitPlan {
+    int64_t S, seg;
+};
+
+static SplitPlan split_plan(int64_t B, int64_t N, int64_t ve, int64_t max_rows, int64_t blocks, int64_t min_vecs,
+                            int64_t fold) {
+    const int64_t vecs = (N + ve - 1) / ve;  // >= the body vectors of any alignment
+    if (B <= 0 || B >= max_rows || B > 65535 || vecs <= 4096) return {1, 0};
+    int64_t S = (blocks + B - 1) / B;
+    if (S > 64) S = 64;
+    if (S > vecs / min_vecs) S = vecs / min_vecs;
+    if (S < 2) return {1, 0};
+    int64_t seg = (vecs + S - 1) / S;
+    seg = (seg + fold - 1) / fold * fold;
+    S = (vecs + seg - 1) / seg;
+    if (S < 2) return {1, 0};
+    return {S, seg};
+}
+
+static SplitPlan default_split_plan(int64_t B, int64_t N, int64_t elem_bytes) {
+    return split_plan(B, N, 16 / elem_bytes, kSplitMaxRows, kSplitBlocks, kSplitMinVecs,
+                      (int64_t)kSplitThreads * kSplitU);
+}
+
+static int64_t split_ws_bytes(int64_t B, const SplitPlan& pl) {
+    return pl.S < 2 ? 0 : B * pl.S * (int64_t)sizeof(float2);
+}
+
+template <bool ROBUST>
+static void launch_split_merge(const float2* part, float* out, int64_t B, int S, hipStream_t st) {
+    int lpr = 4;
+    while (lpr < S) lpr <<= 1;
+    const int64_t rpb = 256 / lpr;
+    const dim3 g((unsigned)((B + rpb - 1) / rpb)), blk(256);
+    switch (lpr) {
+    case 4: lse_fwd_split_merge<ROBUST, 4><<<g, blk, 0, st>>>(part, out, B, S); break;
+    case 8: lse_fwd_split_merge<ROBUST, 8><<<g, blk, 0, st>>>(part, out, B, S); break;
+    case 16: lse_fwd_split_merge<ROBUST, 16><<<g, blk, 0, st>>>(part, out, B, S); break;
+    case 32: lse_fwd_split_merge<ROBUST, 32><<<g, blk, 0, st>>>(part, out, B, S); break;
+    default: lse_fwd_split_merge<ROBUST, 64><<<g, blk, 0, st>>>(part, out, B, S); break;
+    }
+}
+
+template <typename T, bool ROBUST, int THREADS, int U>
+static void launch_split(const T* x, float* out, int64_t B, int64_t N, const SplitPlan& pl, void* ws,
+                         hipStream_t st) {
+    float2* part = static_cast<float2*>(ws);
+    lse_fwd_split_partials<T, ROBUST, THREADS, U>
+        <<<dim3((unsigned)pl.S, (unsigned)B), dim3(THREADS), 0, st>>>(x, N, pl.seg, part);
+    launch_split_merge<ROBUST>(part, out, B, (int)pl.S, st);
+}
+
 static int64_t pow2_ceil(int64_t v) {
     int64_t p = 1;
     while (p < v) p <<= 1;
@@ -140,18 +267,33 @@ static void launch_fwd(const T* x, float* out, int64_t B, int64_t N, hipStream_t
     }
 }
 
+// ws == nullptr: the one-pass kernels for every shape.  Otherwise the split
+// kernel where default_split_plan() chooses it, with ws_bytes checked against
+// what that plan needs.
 template <typename T>
-static int fwd_entry(const char* name, const T* x, float* out, int64_t B, int64_t N, int robust, void* stream) {
+static int fwd_entry(const char* name, const T* x, float* out, int64_t B, int64_t N, int robust, void* ws,
+                     size_t ws_bytes, void* stream) {
     FL_CHECK(B >= 0 && N >= 0, "%s: negative shape (B=%lld, N=%lld)", name, (long long)B, (long long)N);
     if (B == 0) return ok();
     FL_CHECK(out != nullptr, "%s: out is NULL", name);
     FL_CHECK(x != nullptr || N == 0, "%s: x is NULL", name);
     FL_CHECK((reinterpret_cast<uintptr_t>(x) % sizeof(T)) == 0, "%s: x is not element-aligned", name);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    if (robust)
+    const SplitPlan pl = ws ? default_split_plan(B, N, (int64_t)sizeof(T)) : SplitPlan{1, 0};
+    if (pl.S >= 2) {
+        const int64_t need = split_ws_bytes(B, pl);
+        FL_CHECK((int64_t)ws_bytes >= need, "%s: workspace of %llu bytes, %lld needed", name,
+                 (unsigned long long)ws_bytes, (long long)need);
+        FL_CHECK((reinterpret_cast<uintptr_t>(ws) & 7u) == 0, "%s: workspace is not 8-byte aligned", name);
+        if (robust)
+            launch_split<T, true, kSplitThreads, kSplitU>(x, out, B, N, pl, ws, st);
+        else
+            launch_split<T, false, kSplitThreads, kSplitU>(x, out, B, N, pl, ws, st);
+    } else if (robust) {
         launch_fwd<T, true>(x, out, B, N, st);
-    else
+    } else {
         launch_fwd<T, false>(x, out, B, N, st);
+    }
     return launch_status(name);
 }
 
@@ -296,15 +438,39 @@ static void launch_bwd(const float* g, const float* x, const float* lse, float* 
 using namespace fl;
 
 extern "C" int fl_lse_fwd_f32(const float* x, float* out, int64_t B, int64_t N, int robust, void* stream) {
-    return fwd_entry<float>("fl_lse_fwd_f32", x, out, B, N, robust, stream);
+    return fwd_entry<float>("fl_lse_fwd_f32", x, out, B, N, robust, nullptr, 0, stream);
 }
 
 extern "C" int fl_lse_fwd_f16(const void* x, float* out, int64_t B, int64_t N, int robust, void* stream) {
-    return fwd_entry<_Float16>("fl_lse_fwd_f16", static_cast<const _Float16*>(x), out, B, N, robust, stream);
+    return fwd_entry<_Float16>("fl_lse_fwd_f16", static_cast<const _Float16*>(x), out, B, N, robust, nullptr, 0,
+                               stream);
 }
 
 extern "C" int fl_lse_fwd_bf16(const void* x, float* out, int64_t B, int64_t N, int robust, void* stream) {
-    return fwd_entry<bf16_t>("fl_lse_fwd_bf16", static_cast<const bf16_t*>(x), out, B, N, robust, stream);
+    return fwd_entry<bf16_t>("fl_lse_fwd_bf16", static_cast<const bf16_t*>(x), out, B, N, robust, nullptr, 0,
+                             stream);
+}
+
+extern "C" size_t fl_lse_fwd_workspace_bytes(int64_t B, int64_t N, int elem_bytes) {
+    if (elem_bytes != 2 && elem_bytes != 4) return 0;
+    return (size_t)split_ws_bytes(B, default_split_plan(B, N, elem_bytes));
+}
+
+extern "C" int fl_lse_fwd_f32_ws(const float* x, float* out, int64_t B, int64_t N, int robust, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+    return fwd_entry<float>("fl_lse_fwd_f32_ws", x, out, B, N, robust, workspace, workspace_bytes, stream);
+}
+
+extern "C" int fl_lse_fwd_f16_ws(const void* x, float* out, int64_t B, int64_t N, int robust, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+    return fwd_entry<_Float16>("fl_lse_fwd_f16_ws", static_cast<const _Float16*>(x), out, B, N, robust, workspace,
+                               workspace_bytes, stream);
+}
+
+extern "C" int fl_lse_fwd_bf16_ws(const void* x, float* out, int64_t B, int64_t N, int robust, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+    return fwd_entry<bf16_t>("fl_lse_fwd_bf16_ws", static_cast<const bf16_t*>(x), out, B, N, robust, workspace,
+                             workspace_bytes, stream);
 }
 
 extern "C" int fl_lse_bwd_f32(const float* grad, const float* x, const float* lse, float* grad_x, int64_t B,

@@ -39,6 +39,22 @@ def _on_device(t: torch.Tensor):
             yield
 
 
+def _launch_fwd(entry: str, x: torch.Tensor, out: torch.Tensor, elem_bytes: int, robust: bool) -> None:
+    """One-pass kernels, or the split-row kernels (entry + "_ws") for few long
+    rows, where the library asks for a workspace."""
+    B, N = x.shape
+    with _on_device(x):
+        nbytes = _lib.load().fl_lse_fwd_workspace_bytes(B, N, elem_bytes)
+        if nbytes:
+            # partials between the two split kernels; stream-ordered reuse by
+            # torch's caching allocator keeps it valid until they have run
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+            _lib.call(entry + "_ws", x.data_ptr(), out.data_ptr(), B, N, int(robust), ws.data_ptr(), ws.numel(),
+                      _stream(x))
+        else:
+            _lib.call(entry, x.data_ptr(), out.data_ptr(), B, N, int(robust), _stream(x))
+
+
 def _fwd_f32(x: torch.Tensor, robust: bool) -> torch.Tensor:
     # fused_fp32_kernel.cu:155-158 / :176-179
     _check(x.is_cuda, "x must be CUDA")
@@ -49,8 +65,7 @@ def _fwd_f32(x: torch.Tensor, robust: bool) -> torch.Tensor:
     out = torch.empty((B,), dtype=torch.float32, device=x.device)
     if B == 0:
         return out
-    with _on_device(x):
-        _lib.call("fl_lse_fwd_f32", x.data_ptr(), out.data_ptr(), B, N, int(robust), _stream(x))
+    _launch_fwd("fl_lse_fwd_f32", x, out, 4, robust)
     return out
 
 
@@ -101,8 +116,7 @@ def _fwd_half(x: torch.Tensor, dtype: torch.dtype, entry: str, dtype_msg: str, r
     out = torch.empty((B,), dtype=torch.float32, device=x.device)
     if B == 0:
         return out
-    with _on_device(x):
-        _lib.call(entry, x.data_ptr(), out.data_ptr(), B, N, int(robust), _stream(x))
+    _launch_fwd(entry, x, out, 2, robust)
     return out
 
 

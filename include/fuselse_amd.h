@@ -19,6 +19,7 @@
 #ifndef FUSELSE_AMD_H
 #define FUSELSE_AMD_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -57,6 +58,31 @@ int fl_lse_bwd_f32(const float* grad, const float* x, const float* lse, float* g
  * ------------------------------------------------------------------------- */
 int fl_lse_fwd_f16(const void* x, float* out, int64_t B, int64_t N, int robust, void* stream);
 int fl_lse_fwd_bf16(const void* x, float* out, int64_t B, int64_t N, int robust, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Forward with a caller workspace, for few long rows.  The reference launches
+ * one block per row (fused_fp32_kernel.cu:168-170, fused_fp16_kernel.cu:
+ * 127-129), which leaves most of the GPU idle when B is small against the
+ * CU count; these entries split each such row over several blocks and merge
+ * the partial (max, sum) pairs in a fixed order, so results are deterministic.
+ * Same results contract as fl_lse_fwd_f32 / _f16 / _bf16 (same tolerance; not
+ * bit-identical to the one-pass kernels, whose summation order differs).
+ *
+ * fl_lse_fwd_workspace_bytes: bytes the _ws entries need for a (B, N) problem
+ *   of elem_bytes-sized elements (4 = fp32, 2 = fp16/bf16); 0 when the
+ *   one-pass kernels cover the shape (then workspace may be NULL).
+ * workspace: device memory of at least that many bytes, 8-byte aligned, any
+ *   contents; it holds per-segment partials between the two kernels the call
+ *   enqueues, so calls that may run concurrently (other streams) need
+ *   separate buffers.
+ * ------------------------------------------------------------------------- */
+size_t fl_lse_fwd_workspace_bytes(int64_t B, int64_t N, int elem_bytes);
+int fl_lse_fwd_f32_ws(const float* x, float* out, int64_t B, int64_t N, int robust, void* workspace,
+                      size_t workspace_bytes, void* stream);
+int fl_lse_fwd_f16_ws(const void* x, float* out, int64_t B, int64_t N, int robust, void* workspace,
+                      size_t workspace_bytes, void* stream);
+int fl_lse_fwd_bf16_ws(const void* x, float* out, int64_t B, int64_t N, int robust, void* workspace,
+                       size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
  * IntLSE fixed-point row LSE, bit-exact to the reference's GPU reduction tree

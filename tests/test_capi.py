@@ -52,3 +52,36 @@ def test_shim_messages_match_reference(fn, args, msg):
 
     with pytest.raises(RuntimeError, match=msg.replace("(", r"\(").replace(")", r"\)")):
         getattr(fuselse_amd.ext, fn)(*args)
+
+
+def test_split_workspace_plan():
+    """fl_lse_fwd_workspace_bytes: zero where the one-pass kernels cover the
+    shape (many rows, or rows of at most 4096 vectors), otherwise one
+    (max, sum) pair of fp32 per row segment, 2..64 segments per row."""
+    lib = _lib.load()
+    ws = lib.fl_lse_fwd_workspace_bytes
+    assert ws(512, 128256, 4) == 0          # C2: one block per row fills the GPU
+    assert ws(4096, 128256, 4) == 0
+    assert ws(320, 128256, 4) == 0          # enough rows for one block per row
+    assert ws(319, 128256, 4) > 0
+    assert ws(64, 16384, 4) == 0            # 4096 vectors: one-pass
+    assert ws(64, 32768, 2) == 0            # 4096 half vectors
+    assert ws(64, 128256, 3) == 0           # unsupported element size
+    assert ws(0, 128256, 4) == 0
+    for B, N, eb in [(1, 128256, 4), (64, 128256, 4), (1, 300001, 2), (7, 300001, 2)]:
+        n = ws(B, N, eb)
+        assert n > 0 and n % (8 * B) == 0
+        S = n // (8 * B)
+        assert 2 <= S <= 64, (B, N, S)
+
+
+def test_split_entry_rejects_small_workspace_without_launch():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(1 << 40)  # never dereferenced: the size check comes first
+    need = lib.fl_lse_fwd_workspace_bytes(8, 128256, 4)
+    assert need > 0
+    assert lib.fl_lse_fwd_f32_ws(fake, fake, 8, 128256, 1, fake, need - 1, None) == 1
+    assert b"workspace of" in lib.fl_last_error()
+    unaligned = ctypes.c_void_p((1 << 40) + 4)
+    assert lib.fl_lse_fwd_f32_ws(fake, fake, 8, 128256, 1, unaligned, need, None) == 1
+    assert b"8-byte aligned" in lib.fl_last_error()
