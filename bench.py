@@ -219,6 +219,33 @@ def measure_configs(torch, ext, dev, stream, iters=50):
         assert torch.allclose(ok, want, rtol=1e-5) and torch.allclose(ok1, want, rtol=1e-5), "graph replay mismatch"
         rec(f"split_fp32_fwd_{b}x{n}", ms, 4 * b * n + 4 * b, one_pass_us=round(ms1 * 1e3, 2), workspace_bytes=wsb)
         del bufs
+    # Selective log-softmax at the reference RLHF experiment's shapes
+    # (experiment_rlhf_logsumexp/run_rlhf.py:64-76: T = 1024, logits
+    # (B, T-1, V) fp32), synthetic N(0, 2^2) logits and uniform targets: the
+    # fused kernel, trl's algorithm in torch ops on the same GPU, and trl's
+    # algorithm with torch.logsumexp replaced by this library's drop-in (the
+    # reference's "fused" measurement).
+    import fuselse_amd
+    from fuselse_amd.selective import _trl_algorithm
+
+    for name, v, bt in [("llama2", 32000, 8), ("gpt2", 50257, 8), ("llama3", 128256, 4), ("gemma", 256128, 2)]:
+        rows = bt * 1023
+        bufs = [torch.randn(bt, 1023, v, device=dev, generator=gen) * 2 for _ in range(2)]
+        idx = torch.randint(0, v, (bt, 1023), device=dev, generator=gen)
+        ms = _time_calls(torch, stream, lambda i: fuselse_amd.selective_log_softmax(bufs[i % 2], idx), 2, 20)
+        ms_trl = _time_calls(torch, stream, lambda i: _trl_algorithm(bufs[i % 2], idx), 2, 10)
+        saved = torch.logsumexp
+        torch.logsumexp = fuselse_amd.logsumexp
+        try:
+            ms_trl_fl = _time_calls(torch, stream, lambda i: _trl_algorithm(bufs[i % 2], idx), 2, 10)
+        finally:
+            torch.logsumexp = saved
+        got = fuselse_amd.selective_log_softmax(bufs[0], idx)
+        ref = _trl_algorithm(bufs[0], idx)
+        assert torch.allclose(got, ref, rtol=1e-4, atol=1e-4), "selective log-softmax mismatch"
+        rec(f"sls_fwd_{name}_{bt}x1023x{v}", ms, 4 * rows * v + 16 * rows, trl_torch_us=round(ms_trl * 1e3, 1),
+            trl_with_fuselse_lse_us=round(ms_trl_fl * 1e3, 1))
+        del bufs
     # C4: IntLSE fixed point
     b, n = 512, 128256
     nb = 3

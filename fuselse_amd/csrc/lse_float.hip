@@ -49,15 +49,53 @@ __device__ __forceinline__ void fold_body(float& m, float& s, const T* body, int
     }
 }
 
+// ---------------------------------------------------------------------------
+// Row outputs of the forward kernels.  begin(row) runs when a row starts, on
+// the lane that later calls end(row, r, lse), so a policy's own loads are in
+// flight during the row's reduction.
+// ---------------------------------------------------------------------------
+struct LseOut {
+    float* __restrict__ out;
+    struct Row {};
+    __device__ __forceinline__ Row begin(int64_t) const { return {}; }
+    __device__ __forceinline__ void end(int64_t row, Row, float lse) const { out[row] = lse; }
+};
+
+// Selective log-softmax: logp[row] = x[row, index[row]] - lse[row], and lse[row]
+// when lse is not NULL.  An index outside [0, N) gives NaN (torch.gather would
+// raise); the special values follow from the robust LSE (a +inf target in a
+// row whose LSE is +inf gives NaN, as torch.log_softmax does).
+template <typename T>
+struct SelectOut {
+    const T* __restrict__ x;
+    const int64_t* __restrict__ index;
+    float* __restrict__ logp;
+    float* __restrict__ lse;
+    int64_t N;
+    struct Row {
+        float xt;
+    };
+    __device__ __forceinline__ Row begin(int64_t row) const {
+        const int64_t t = index[row];
+        return {t >= 0 && t < N ? Elem<T>::scalar(x + row * N + t) : __builtin_nanf("")};
+    }
+    __device__ __forceinline__ void end(int64_t row, Row r, float l) const {
+        if (lse) lse[row] = l;
+        logp[row] = r.xt - l;
+    }
+};
+
 // One block per row (grid-stride over rows).
-template <typename T, bool ROBUST, int THREADS, int U>
-__global__ __launch_bounds__(THREADS) void lse_fwd_block_rows(const T* __restrict__ x, float* __restrict__ out,
-                                                              int64_t B, int64_t N) {
+template <typename T, bool ROBUST, int THREADS, int U, typename OUT>
+__global__ __launch_bounds__(THREADS) void lse_fwd_block_rows(const T* __restrict__ x, OUT out, int64_t B,
+                                                              int64_t N) {
     constexpr int VE = Elem<T>::kVec;
     constexpr int WAVES = THREADS / 64;
     __shared__ float sh_m[WAVES], sh_s[WAVES];
     const int tid = threadIdx.x;
     for (int64_t row = blockIdx.x; row < B; row += gridDim.x) {
+        typename OUT::Row orow{};
+        if (tid == 0) orow = out.begin(row);
         const T* p = x + row * N;
         const RowSplit sp = split_row(p, N);
         float m = -kInf, s = 0.0f;
@@ -74,7 +112,7 @@ __global__ __launch_bounds__(THREADS) void lse_fwd_block_rows(const T* __restric
             m = tid < WAVES ? sh_m[tid] : -kInf;
             s = tid < WAVES ? sh_s[tid] : 0.0f;
             group_merge<WAVES>(m, s);
-            if (tid == 0) out[row] = lse_finish<ROBUST>(m, s);
+            if (tid == 0) out.end(row, orow, lse_finish<ROBUST>(m, s));
         }
         __syncthreads();
     }
@@ -82,9 +120,8 @@ __global__ __launch_bounds__(THREADS) void lse_fwd_block_rows(const T* __restric
 
 // LPR lanes per row, 64/LPR rows per wave, WAVES waves per block
 // (grid-stride over row groups).
-template <typename T, bool ROBUST, int LPR, int U>
-__global__ __launch_bounds__(256) void lse_fwd_group_rows(const T* __restrict__ x, float* __restrict__ out,
-                                                          int64_t B, int64_t N) {
+template <typename T, bool ROBUST, int LPR, int U, typename OUT>
+__global__ __launch_bounds__(256) void lse_fwd_group_rows(const T* __restrict__ x, OUT out, int64_t B, int64_t N) {
     constexpr int VE = Elem<T>::kVec;
     constexpr int RPW = 64 / LPR;
     constexpr int WAVES = 4;
@@ -95,6 +132,8 @@ __global__ __launch_bounds__(256) void lse_fwd_group_rows(const T* __restrict__ 
     const int64_t step = (int64_t)gridDim.x * WAVES * RPW;
     for (int64_t base = ((int64_t)blockIdx.x * WAVES + wave) * RPW; base < B; base += step) {
         const int64_t row = base + g;
+        typename OUT::Row orow{};
+        if (j == 0 && row < B) orow = out.begin(row);
         float m = -kInf, s = 0.0f;
         if (row < B) {
             const T* p = x + row * N;
@@ -105,7 +144,7 @@ __global__ __launch_bounds__(256) void lse_fwd_group_rows(const T* __restrict__ 
             fold_body<T, ROBUST, LPR, U>(m, s, p + sp.head, j, sp.nvec);
         }
         group_merge<LPR>(m, s);
-        if (j == 0 && row < B) out[row] = lse_finish<ROBUST>(m, s);
+        if (j == 0 && row < B) out.end(row, orow, lse_finish<ROBUST>(m, s));
     }
 }
 
@@ -156,11 +195,13 @@ __global__ __launch_bounds__(THREADS) void lse_fwd_split_partials(const T* __res
 }
 
 // LPR lanes per row (LPR >= S), 64/LPR rows per wave, 4 waves per block.
-template <bool ROBUST, int LPR>
-__global__ __launch_bounds__(256) void lse_fwd_split_merge(const float2* __restrict__ part, float* __restrict__ out,
-                                                           int64_t B, int S) {
+template <bool ROBUST, int LPR, typename OUT>
+__global__ __launch_bounds__(256) void lse_fwd_split_merge(const float2* __restrict__ part, OUT out, int64_t B,
+                                                           int S) {
     const int j = (int)(threadIdx.x % LPR);
     const int64_t row = (int64_t)blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
+    typename OUT::Row orow{};
+    if (j == 0 && row < B) orow = out.begin(row);
     float m = -kInf, s = 0.0f;
     if (row < B && j < S) {
         const float2 pv = part[row * S + j];
@@ -168,7 +209,7 @@ __global__ __launch_bounds__(256) void lse_fwd_split_merge(const float2* __restr
         s = pv.y;
     }
     group_merge<LPR>(m, s);
-    if (j == 0 && row < B) out[row] = lse_finish<ROBUST>(m, s);
+    if (j == 0 && row < B) out.end(row, orow, lse_finish<ROBUST>(m, s));
 }
 
 // The split is used for B < kSplitMaxRows and rows of more than 4096 body
@@ -210,24 +251,23 @@ static int64_t split_ws_bytes(int64_t B, const SplitPlan& pl) {
     return pl.S < 2 ? 0 : B * pl.S * (int64_t)sizeof(float2);
 }
 
-template <bool ROBUST>
-static void launch_split_merge(const float2* part, float* out, int64_t B, int S, hipStream_t st) {
+template <bool ROBUST, typename OUT>
+static void launch_split_merge(const float2* part, OUT out, int64_t B, int S, hipStream_t st) {
     int lpr = 4;
     while (lpr < S) lpr <<= 1;
     const int64_t rpb = 256 / lpr;
     const dim3 g((unsigned)((B + rpb - 1) / rpb)), blk(256);
     switch (lpr) {
-    case 4: lse_fwd_split_merge<ROBUST, 4><<<g, blk, 0, st>>>(part, out, B, S); break;
-    case 8: lse_fwd_split_merge<ROBUST, 8><<<g, blk, 0, st>>>(part, out, B, S); break;
-    case 16: lse_fwd_split_merge<ROBUST, 16><<<g, blk, 0, st>>>(part, out, B, S); break;
-    case 32: lse_fwd_split_merge<ROBUST, 32><<<g, blk, 0, st>>>(part, out, B, S); break;
-    default: lse_fwd_split_merge<ROBUST, 64><<<g, blk, 0, st>>>(part, out, B, S); break;
+    case 4: lse_fwd_split_merge<ROBUST, 4, OUT><<<g, blk, 0, st>>>(part, out, B, S); break;
+    case 8: lse_fwd_split_merge<ROBUST, 8, OUT><<<g, blk, 0, st>>>(part, out, B, S); break;
+    case 16: lse_fwd_split_merge<ROBUST, 16, OUT><<<g, blk, 0, st>>>(part, out, B, S); break;
+    case 32: lse_fwd_split_merge<ROBUST, 32, OUT><<<g, blk, 0, st>>>(part, out, B, S); break;
+    default: lse_fwd_split_merge<ROBUST, 64, OUT><<<g, blk, 0, st>>>(part, out, B, S); break;
     }
 }
 
-template <typename T, bool ROBUST, int THREADS, int U>
-static void launch_split(const T* x, float* out, int64_t B, int64_t N, const SplitPlan& pl, void* ws,
-                         hipStream_t st) {
+template <typename T, bool ROBUST, int THREADS, int U, typename OUT>
+static void launch_split(const T* x, OUT out, int64_t B, int64_t N, const SplitPlan& pl, void* ws, hipStream_t st) {
     float2* part = static_cast<float2*>(ws);
     lse_fwd_split_partials<T, ROBUST, THREADS, U>
         <<<dim3((unsigned)pl.S, (unsigned)B), dim3(THREADS), 0, st>>>(x, N, pl.seg, part);
@@ -240,15 +280,15 @@ static int64_t pow2_ceil(int64_t v) {
     return p;
 }
 
-template <typename T, bool ROBUST>
-static void launch_fwd(const T* x, float* out, int64_t B, int64_t N, hipStream_t st) {
+template <typename T, bool ROBUST, typename OUT>
+static void launch_fwd(const T* x, OUT out, int64_t B, int64_t N, hipStream_t st) {
     constexpr int VE = Elem<T>::kVec;
     const int64_t vecs = (N + VE - 1) / VE;
     if (vecs > 4096) {
         // one 512-thread block per row, two 16-byte loads per lane per fold:
         // measured best at (512, 128256) among 256..1024 threads x 1..8 loads
         int64_t grid = B < ((int64_t)1 << 30) ? B : ((int64_t)1 << 30);
-        lse_fwd_block_rows<T, ROBUST, 512, 2><<<dim3((unsigned)grid), dim3(512), 0, st>>>(x, out, B, N);
+        lse_fwd_block_rows<T, ROBUST, 512, 2, OUT><<<dim3((unsigned)grid), dim3(512), 0, st>>>(x, out, B, N);
         return;
     }
     int64_t lpr = pow2_ceil((vecs + 3) / 4);
@@ -259,26 +299,23 @@ static void launch_fwd(const T* x, float* out, int64_t B, int64_t N, hipStream_t
     if (grid > (int64_t)1 << 30) grid = (int64_t)1 << 30;
     const dim3 g((unsigned)grid), blk(256);
     switch (lpr) {
-    case 4: lse_fwd_group_rows<T, ROBUST, 4, 4><<<g, blk, 0, st>>>(x, out, B, N); break;
-    case 8: lse_fwd_group_rows<T, ROBUST, 8, 4><<<g, blk, 0, st>>>(x, out, B, N); break;
-    case 16: lse_fwd_group_rows<T, ROBUST, 16, 4><<<g, blk, 0, st>>>(x, out, B, N); break;
-    case 32: lse_fwd_group_rows<T, ROBUST, 32, 4><<<g, blk, 0, st>>>(x, out, B, N); break;
-    default: lse_fwd_group_rows<T, ROBUST, 64, 4><<<g, blk, 0, st>>>(x, out, B, N); break;
+    case 4: lse_fwd_group_rows<T, ROBUST, 4, 4, OUT><<<g, blk, 0, st>>>(x, out, B, N); break;
+    case 8: lse_fwd_group_rows<T, ROBUST, 8, 4, OUT><<<g, blk, 0, st>>>(x, out, B, N); break;
+    case 16: lse_fwd_group_rows<T, ROBUST, 16, 4, OUT><<<g, blk, 0, st>>>(x, out, B, N); break;
+    case 32: lse_fwd_group_rows<T, ROBUST, 32, 4, OUT><<<g, blk, 0, st>>>(x, out, B, N); break;
+    default: lse_fwd_group_rows<T, ROBUST, 64, 4, OUT><<<g, blk, 0, st>>>(x, out, B, N); break;
     }
 }
 
 // ws == nullptr: the one-pass kernels for every shape.  Otherwise the split
-// kernel where default_split_plan() chooses it, with ws_bytes checked against
-// what that plan needs.
-template <typename T>
-static int fwd_entry(const char* name, const T* x, float* out, int64_t B, int64_t N, int robust, void* ws,
-                     size_t ws_bytes, void* stream) {
-    FL_CHECK(B >= 0 && N >= 0, "%s: negative shape (B=%lld, N=%lld)", name, (long long)B, (long long)N);
-    if (B == 0) return ok();
-    FL_CHECK(out != nullptr, "%s: out is NULL", name);
+// kernels where default_split_plan() chooses them, with ws_bytes checked
+// against what that plan needs.  Argument checks other than x's are the
+// caller's.
+template <typename T, typename OUT>
+static int fwd_launch(const char* name, const T* x, OUT out, int64_t B, int64_t N, int robust, void* ws,
+                      size_t ws_bytes, hipStream_t st) {
     FL_CHECK(x != nullptr || N == 0, "%s: x is NULL", name);
     FL_CHECK((reinterpret_cast<uintptr_t>(x) % sizeof(T)) == 0, "%s: x is not element-aligned", name);
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const SplitPlan pl = ws ? default_split_plan(B, N, (int64_t)sizeof(T)) : SplitPlan{1, 0};
     if (pl.S >= 2) {
         const int64_t need = split_ws_bytes(B, pl);
@@ -295,6 +332,15 @@ static int fwd_entry(const char* name, const T* x, float* out, int64_t B, int64_
         launch_fwd<T, false>(x, out, B, N, st);
     }
     return launch_status(name);
+}
+
+template <typename T>
+static int fwd_entry(const char* name, const T* x, float* out, int64_t B, int64_t N, int robust, void* ws,
+                     size_t ws_bytes, void* stream) {
+    FL_CHECK(B >= 0 && N >= 0, "%s: negative shape (B=%lld, N=%lld)", name, (long long)B, (long long)N);
+    if (B == 0) return ok();
+    FL_CHECK(out != nullptr, "%s: out is NULL", name);
+    return fwd_launch<T>(name, x, LseOut{out}, B, N, robust, ws, ws_bytes, reinterpret_cast<hipStream_t>(stream));
 }
 
 // ---------------------------------------------------------------------------
@@ -324,12 +370,43 @@ __device__ __forceinline__ f32x4 bwd_vec(float gv, float lv, bool fma_ok, f32x4 
     return r;
 }
 
+// Backward targets.  LseGrad: grad_x = g * softmax.  SelGrad (selective
+// log-softmax, logp = x[t] - lse): grad_x = g * (onehot(t) - softmax), i.e.
+// the softmax term with -g plus g at column t; an index outside [0, N) adds
+// nothing (its forward was NaN).
+struct LseGrad {
+    static constexpr bool kSel = false;
+    __device__ __forceinline__ float coef(int64_t, float gv) const { return gv; }
+    __device__ __forceinline__ int64_t target(int64_t) const { return -1; }
+};
+struct SelGrad {
+    static constexpr bool kSel = true;
+    const int64_t* __restrict__ index;
+    __device__ __forceinline__ float coef(int64_t, float gv) const { return -gv; }
+    __device__ __forceinline__ int64_t target(int64_t row) const { return index[row]; }
+};
+
+// SEL: adds gv to the element of r that sits at column t, if any; c0 is the
+// column of r.x.
+template <bool SEL>
+__device__ __forceinline__ f32x4 add_at(f32x4 r, int64_t c0, int64_t t, float gv) {
+    if constexpr (!SEL) return r;
+    const int64_t d = t - c0;
+    if ((uint64_t)d < 4u) {
+        r.x += d == 0 ? gv : 0.0f;
+        r.y += d == 1 ? gv : 0.0f;
+        r.z += d == 2 ? gv : 0.0f;
+        r.w += d == 3 ? gv : 0.0f;
+    }
+    return r;
+}
+
 // Long rows: grid = B * chunks_per_row blocks of 256 threads; a block covers
 // 256*U consecutive vectors of one row.  x and grad_x share their alignment.
-template <int U>
+template <int U, typename GR>
 __global__ __launch_bounds__(256) void lse_bwd_row_chunks(const float* __restrict__ g, const float* __restrict__ x,
                                                           const float* __restrict__ lse, float* __restrict__ gx,
-                                                          int64_t N, int64_t chunks_per_row) {
+                                                          int64_t N, int64_t chunks_per_row, GR gr_t) {
     const int64_t blk = blockIdx.x;
     const int64_t row = blk / chunks_per_row;
     const int64_t chunk = blk - row * chunks_per_row;
@@ -337,12 +414,14 @@ __global__ __launch_bounds__(256) void lse_bwd_row_chunks(const float* __restric
     const float* xr = x + row * N;
     float* gr = gx + row * N;
     const RowSplit sp = split_row(xr, N);
-    const float gv = g[row];
+    const float g0 = g[row];
+    const float gv = gr_t.coef(row, g0);
+    const int64_t t = gr_t.target(row);
     const float lv = lse[row];
     if (chunk == 0) {
-        if (tid < sp.head) gr[tid] = bwd_elem(gv, lv, xr[tid]);
+        if (tid < sp.head) gr[tid] = bwd_elem(gv, lv, xr[tid]) + (GR::kSel && tid == t ? g0 : 0.0f);
         const int64_t t0 = sp.head + sp.nvec * 4;
-        if (tid < sp.tail) gr[t0 + tid] = bwd_elem(gv, lv, xr[t0 + tid]);
+        if (tid < sp.tail) gr[t0 + tid] = bwd_elem(gv, lv, xr[t0 + tid]) + (GR::kSel && t0 + tid == t ? g0 : 0.0f);
     }
     const f32x4* xb = reinterpret_cast<const f32x4*>(xr + sp.head);
     f32x4* gb = reinterpret_cast<f32x4*>(gr + sp.head);
@@ -357,15 +436,16 @@ __global__ __launch_bounds__(256) void lse_bwd_row_chunks(const float* __restric
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int64_t i = i0 + (int64_t)u * 256;
-        if (i < sp.nvec) store_stream<f32x4>(bwd_vec(gv, lv, fma_ok, v[u]), gb + i);
+        if (i < sp.nvec)
+            store_stream<f32x4>(add_at<GR::kSel>(bwd_vec(gv, lv, fma_ok, v[u]), sp.head + 4 * i, t, g0), gb + i);
     }
 }
 
 // Short rows: LPR lanes per row, 256/LPR rows per block, grid-stride.
-template <int LPR>
+template <int LPR, typename GR>
 __global__ __launch_bounds__(256) void lse_bwd_group_rows(const float* __restrict__ g, const float* __restrict__ x,
                                                           const float* __restrict__ lse, float* __restrict__ gx,
-                                                          int64_t B, int64_t N) {
+                                                          int64_t B, int64_t N, GR gr_t) {
     constexpr int RPB = 256 / LPR;
     const int gi = threadIdx.x / LPR;
     const int j = threadIdx.x % LPR;
@@ -373,39 +453,47 @@ __global__ __launch_bounds__(256) void lse_bwd_group_rows(const float* __restric
         const float* xr = x + row * N;
         float* gr = gx + row * N;
         const RowSplit sp = split_row(xr, N);
-        const float gv = g[row];
+        const float g0 = g[row];
+        const float gv = gr_t.coef(row, g0);
+        const int64_t t = gr_t.target(row);
         const float lv = lse[row];
-        for (int64_t h = j; h < sp.head; h += LPR) gr[h] = bwd_elem(gv, lv, xr[h]);
+        for (int64_t h = j; h < sp.head; h += LPR) gr[h] = bwd_elem(gv, lv, xr[h]) + (GR::kSel && h == t ? g0 : 0.0f);
         const int64_t t0 = sp.head + sp.nvec * 4;
-        for (int64_t t = j; t < sp.tail; t += LPR) gr[t0 + t] = bwd_elem(gv, lv, xr[t0 + t]);
+        for (int64_t c = j; c < sp.tail; c += LPR)
+            gr[t0 + c] = bwd_elem(gv, lv, xr[t0 + c]) + (GR::kSel && t0 + c == t ? g0 : 0.0f);
         const f32x4* xb = reinterpret_cast<const f32x4*>(xr + sp.head);
         f32x4* gb = reinterpret_cast<f32x4*>(gr + sp.head);
         const bool fma_ok = __builtin_fabsf(lv) < 64.0f;
         for (int64_t i = j; i < sp.nvec; i += LPR)
-            store_stream<f32x4>(bwd_vec(gv, lv, fma_ok, load_stream<f32x4>(xb + i)), gb + i);
+            store_stream<f32x4>(
+                add_at<GR::kSel>(bwd_vec(gv, lv, fma_ok, load_stream<f32x4>(xb + i)), sp.head + 4 * i, t, g0), gb + i);
     }
 }
 
 // Fallback when x and grad_x differ in 16-byte alignment: scalar grid-stride.
+template <typename GR>
 __global__ __launch_bounds__(256) void lse_bwd_scalar(const float* __restrict__ g, const float* __restrict__ x,
                                                       const float* __restrict__ lse, float* __restrict__ gx,
-                                                      int64_t B, int64_t N) {
+                                                      int64_t B, int64_t N, GR gr_t) {
     for (int64_t row = blockIdx.y; row < B; row += gridDim.y) {
-        const float gv = g[row];
+        const float g0 = g[row];
+        const float gv = gr_t.coef(row, g0);
+        const int64_t t = gr_t.target(row);
         const float lv = lse[row];
         for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < N; i += (int64_t)gridDim.x * 256)
-            gx[row * N + i] = bwd_elem(gv, lv, x[row * N + i]);
+            gx[row * N + i] = bwd_elem(gv, lv, x[row * N + i]) + (GR::kSel && i == t ? g0 : 0.0f);
     }
 }
 
-static void launch_bwd(const float* g, const float* x, const float* lse, float* gx, int64_t B, int64_t N,
+template <typename GR>
+static void launch_bwd(const float* g, const float* x, const float* lse, float* gx, int64_t B, int64_t N, GR gr_t,
                        hipStream_t st) {
     const bool same_align = ((reinterpret_cast<uintptr_t>(x) ^ reinterpret_cast<uintptr_t>(gx)) & 15u) == 0;
     if (!same_align) {
         int64_t gxdim = (N + 255) / 256;
         if (gxdim > 1024) gxdim = 1024;
         int64_t gydim = B < 65535 ? B : 65535;
-        lse_bwd_scalar<<<dim3((unsigned)gxdim, (unsigned)gydim), dim3(256), 0, st>>>(g, x, lse, gx, B, N);
+        lse_bwd_scalar<<<dim3((unsigned)gxdim, (unsigned)gydim), dim3(256), 0, st>>>(g, x, lse, gx, B, N, gr_t);
         return;
     }
     const int64_t vecs = N / 4 + 1;
@@ -413,7 +501,7 @@ static void launch_bwd(const float* g, const float* x, const float* lse, float* 
         // one 16-byte vector per lane: measured best (with 128x2 and 1024x1)
         constexpr int U = 1;
         const int64_t cpr = (vecs + 256 * U - 1) / (256 * U);
-        lse_bwd_row_chunks<U><<<dim3((unsigned)(B * cpr)), dim3(256), 0, st>>>(g, x, lse, gx, N, cpr);
+        lse_bwd_row_chunks<U><<<dim3((unsigned)(B * cpr)), dim3(256), 0, st>>>(g, x, lse, gx, N, cpr, gr_t);
         return;
     }
     int64_t lpr = pow2_ceil((vecs + 3) / 4);
@@ -423,14 +511,27 @@ static void launch_bwd(const float* g, const float* x, const float* lse, float* 
     if (grid > (int64_t)1 << 30) grid = (int64_t)1 << 30;
     const dim3 gd((unsigned)grid), blk(256);
     switch (lpr) {
-    case 4: lse_bwd_group_rows<4><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N); break;
-    case 8: lse_bwd_group_rows<8><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N); break;
-    case 16: lse_bwd_group_rows<16><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N); break;
-    case 32: lse_bwd_group_rows<32><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N); break;
-    case 64: lse_bwd_group_rows<64><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N); break;
-    case 128: lse_bwd_group_rows<128><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N); break;
-    default: lse_bwd_group_rows<256><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N); break;
+    case 4: lse_bwd_group_rows<4><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
+    case 8: lse_bwd_group_rows<8><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
+    case 16: lse_bwd_group_rows<16><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
+    case 32: lse_bwd_group_rows<32><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
+    case 64: lse_bwd_group_rows<64><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
+    case 128: lse_bwd_group_rows<128><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
+    default: lse_bwd_group_rows<256><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
     }
+}
+
+template <typename GR>
+static int bwd_entry(const char* name, const float* grad, const float* x, const float* lse, float* grad_x, int64_t B,
+                     int64_t N, GR gr_t, void* stream) {
+    FL_CHECK(B >= 0 && N >= 0, "%s: negative shape (B=%lld, N=%lld)", name, (long long)B, (long long)N);
+    if (B == 0 || N == 0) return ok();
+    FL_CHECK(grad && x && lse && grad_x, "%s: NULL pointer argument", name);
+    FL_CHECK((reinterpret_cast<uintptr_t>(x) & 3u) == 0 && (reinterpret_cast<uintptr_t>(grad_x) & 3u) == 0,
+             "%s: x / grad_x are not 4-byte aligned", name);
+    FL_CHECK(B * ((N / 4 + 1 + 255) / 256) < ((int64_t)1 << 32), "%s: B*N too large for the grid", name);
+    launch_bwd(grad, x, lse, grad_x, B, N, gr_t, reinterpret_cast<hipStream_t>(stream));
+    return launch_status(name);
 }
 
 }  // namespace fl
@@ -475,13 +576,23 @@ extern "C" int fl_lse_fwd_bf16_ws(const void* x, float* out, int64_t B, int64_t 
 
 extern "C" int fl_lse_bwd_f32(const float* grad, const float* x, const float* lse, float* grad_x, int64_t B,
                               int64_t N, void* stream) {
-    const char* name = "fl_lse_bwd_f32";
+    return bwd_entry("fl_lse_bwd_f32", grad, x, lse, grad_x, B, N, LseGrad{}, stream);
+}
+
+extern "C" int fl_selective_logsoftmax_f32(const float* x, const int64_t* index, float* logp, float* lse, int64_t B,
+                                           int64_t N, int robust, void* workspace, size_t workspace_bytes,
+                                           void* stream) {
+    const char* name = "fl_selective_logsoftmax_f32";
     FL_CHECK(B >= 0 && N >= 0, "%s: negative shape (B=%lld, N=%lld)", name, (long long)B, (long long)N);
-    if (B == 0 || N == 0) return ok();
-    FL_CHECK(grad && x && lse && grad_x, "%s: NULL pointer argument", name);
-    FL_CHECK((reinterpret_cast<uintptr_t>(x) & 3u) == 0 && (reinterpret_cast<uintptr_t>(grad_x) & 3u) == 0,
-             "%s: x / grad_x are not 4-byte aligned", name);
-    FL_CHECK(B * ((N / 4 + 1 + 255) / 256) < ((int64_t)1 << 32), "%s: B*N too large for the grid", name);
-    launch_bwd(grad, x, lse, grad_x, B, N, reinterpret_cast<hipStream_t>(stream));
-    return launch_status(name);
+    if (B == 0) return ok();
+    FL_CHECK(index != nullptr && logp != nullptr, "%s: NULL pointer argument", name);
+    return fwd_launch<float>(name, x, SelectOut<float>{x, index, logp, lse, N}, B, N, robust, workspace,
+                             workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int fl_selective_logsoftmax_bwd_f32(const float* grad, const float* x, const int64_t* index,
+                                               const float* lse, float* grad_x, int64_t B, int64_t N, void* stream) {
+    const char* name = "fl_selective_logsoftmax_bwd_f32";
+    FL_CHECK(index != nullptr || B == 0 || N == 0, "%s: NULL pointer argument", name);
+    return bwd_entry(name, grad, x, lse, grad_x, B, N, SelGrad{index}, stream);
 }

@@ -107,6 +107,61 @@ def onepass_lse_float_backward(grad_output: torch.Tensor, x: torch.Tensor, lse_o
     return grad_input
 
 
+def selective_log_softmax_float(logits: torch.Tensor, index: torch.Tensor, robust: bool = True):
+    """Fused selective log-softmax over fp32 (B, N) logits and int64 (B,)
+    targets: returns (logp, lse) with logp[r] = logits[r, index[r]] - lse[r],
+    in one pass over the logits.  It fuses the fp32 branch of
+    trl.trainer.utils.selective_log_softmax (trl 1.0.0: gather, per-row
+    torch.logsumexp, subtraction), which the reference's RLHF experiment
+    times (experiment_rlhf_logsumexp/run_rlhf.py:28,145,155).  An index
+    outside [0, N) gives NaN."""
+    _check(logits.is_cuda, "logits must be CUDA")
+    _check(index.is_cuda, "index must be CUDA")
+    _check(logits.dtype == torch.float32, "logits must be float32")
+    _check(index.dtype == torch.int64, "index must be int64")
+    _check(logits.dim() == 2, "logits must be 2D (B, N)")
+    _check(index.dim() == 1, "index must be 1D (B)")
+    _check(logits.is_contiguous(), "logits must be contiguous")
+    _check(index.is_contiguous(), "index must be contiguous")
+    _check(index.size(0) == logits.size(0), "index batch dimension must match logits")
+    B, N = logits.shape
+    logp = torch.empty((B,), dtype=torch.float32, device=logits.device)
+    lse = torch.empty((B,), dtype=torch.float32, device=logits.device)
+    if B == 0:
+        return logp, lse
+    with _on_device(logits):
+        nbytes = _lib.load().fl_lse_fwd_workspace_bytes(B, N, 4)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=logits.device) if nbytes else None
+        _lib.call("fl_selective_logsoftmax_f32", logits.data_ptr(), index.data_ptr(), logp.data_ptr(),
+                  lse.data_ptr(), B, N, int(robust), ws.data_ptr() if ws is not None else None, nbytes,
+                  _stream(logits))
+    return logp, lse
+
+
+def selective_log_softmax_float_backward(grad_output: torch.Tensor, logits: torch.Tensor, index: torch.Tensor,
+                                         lse: torch.Tensor) -> torch.Tensor:
+    """grad_logits[r, i] = grad_output[r] * ((i == index[r]) - exp(logits[r, i] - lse[r])),
+    one pass over the logits."""
+    for t, nm in ((grad_output, "grad_output"), (logits, "logits"), (index, "index"), (lse, "lse")):
+        _check(t.is_cuda, f"{nm} must be CUDA")
+        _check(t.is_contiguous(), f"{nm} must be contiguous")
+    _check(logits.dtype == torch.float32 and grad_output.dtype == torch.float32 and lse.dtype == torch.float32,
+           "grad_output, logits and lse must be float32")
+    _check(index.dtype == torch.int64, "index must be int64")
+    _check(logits.dim() == 2, "logits must be 2D (B, N)")
+    _check(grad_output.dim() == 1 and index.dim() == 1 and lse.dim() == 1, "grad_output, index and lse must be 1D (B)")
+    B, N = logits.shape
+    _check(grad_output.size(0) == B and index.size(0) == B and lse.size(0) == B,
+           "grad_output, index and lse batch dimensions must match logits")
+    grad = torch.empty_like(logits)
+    if B * N == 0:
+        return grad
+    with _on_device(logits):
+        _lib.call("fl_selective_logsoftmax_bwd_f32", grad_output.data_ptr(), logits.data_ptr(), index.data_ptr(),
+                  lse.data_ptr(), grad.data_ptr(), B, N, _stream(logits))
+    return grad
+
+
 def _fwd_half(x: torch.Tensor, dtype: torch.dtype, entry: str, dtype_msg: str, robust: bool) -> torch.Tensor:
     # fused_fp16_kernel.cu:113-116
     _check(x.dim() == 2, "Expected 2-D tensor (B, N)")

@@ -51,6 +51,26 @@ int fl_lse_bwd_f32(const float* grad, const float* x, const float* lse, float* g
                    int64_t N, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Fused selective log-softmax over fp32 logits [B, N]:
+ *   logp[r] = x[r, index[r]] - log(sum_i exp(x[r, i])),
+ * with lse[r] (may be NULL) kept for the backward; one pass over x.  It fuses
+ * the gather, per-row torch.logsumexp and subtraction of
+ * trl.trainer.utils.selective_log_softmax (trl 1.0.0, its fp32 branch), the
+ * function the reference's RLHF experiment times with the LSE kernels patched
+ * in (experiment_rlhf_logsumexp/run_rlhf.py:28,143-158).  index is int64 [B];
+ * an index outside [0, N) gives NaN.  robust as for fl_lse_fwd_f32.
+ * workspace: as for fl_lse_fwd_f32_ws, sized by
+ * fl_lse_fwd_workspace_bytes(B, N, 4); NULL keeps the one-pass kernels.
+ *
+ * fl_selective_logsoftmax_bwd_f32:
+ *   grad_x[r, i] = grad[r] * ((i == index[r]) - exp(x[r, i] - lse[r])).
+ * ------------------------------------------------------------------------- */
+int fl_selective_logsoftmax_f32(const float* x, const int64_t* index, float* logp, float* lse, int64_t B,
+                                int64_t N, int robust, void* workspace, size_t workspace_bytes, void* stream);
+int fl_selective_logsoftmax_bwd_f32(const float* grad, const float* x, const int64_t* index, const float* lse,
+                                    float* grad_x, int64_t B, int64_t N, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Half-precision inputs with fp32 accumulation and fp32 output [B].
  * fl_lse_fwd_f16 replaces batched_logsumexp_fp16 (fuselse/gpu/fused_fp16_kernel.cu:
  * 112-132; kernel :25-110).  fl_lse_fwd_bf16 is the bf16 twin, which the

@@ -7,7 +7,7 @@ baseline).  The shipped package never imports it.
 Two kinds of oracle live here:
 
 * fp64 numpy restatements of the float paths (forward, robust forward,
-  backward, sparse gather-LSE).  They follow the mathematics the reference
+  backward, selective log-softmax forward and backward, sparse gather-LSE).  They follow the mathematics the reference
   implements (``fuselse/gpu/fused_fp32_kernel.cu:27-40,135-150``,
   ``experiment_pyjuice/run_pyjuice.py:103-118``) and torch.logsumexp's
   special-value rules, which the reference's robust variant reproduces.
@@ -129,6 +129,33 @@ def lse_bwd_fp64(g, x, lse) -> np.ndarray:
     x = np.asarray(x, dtype=np.float64)
     with np.errstate(invalid="ignore", over="ignore"):
         return np.asarray(g, np.float64)[..., None] * np.exp(x - np.asarray(lse, np.float64)[..., None])
+
+
+def selective_logsoftmax_fp64(x, index):
+    """Selective log-softmax in float64: logp[r] = x[r, index[r]] - LSE(x[r, :]),
+    NaN for an index outside [0, N).  This is the fp32 branch of
+    trl.trainer.utils.selective_log_softmax (trl 1.0.0, a dependency absent
+    here; its published algorithm is gather, per-row torch.logsumexp,
+    subtraction), which experiment_rlhf_logsumexp/run_rlhf.py:145,155 times.
+    Returns (logp, lse)."""
+    x = np.asarray(x, np.float64)
+    idx = np.asarray(index, np.int64)
+    lse = lse_fp64(x)
+    ok = (idx >= 0) & (idx < x.shape[-1])
+    xt = np.take_along_axis(x, np.where(ok, idx, 0)[..., None], axis=-1)[..., 0]
+    with np.errstate(invalid="ignore"):
+        return np.where(ok, xt - lse, np.nan), lse
+
+
+def selective_logsoftmax_bwd_fp64(g, x, index, lse):
+    """d logp[r] / d x[r, i] times g[r]: g[r] * ((i == index[r]) - exp(x[r, i] - lse[r]))."""
+    x = np.asarray(x, np.float64)
+    g = np.asarray(g, np.float64)
+    out = -lse_bwd_fp64(g, x, lse)
+    idx = np.asarray(index, np.int64)
+    rows = np.nonzero((idx >= 0) & (idx < x.shape[-1]))[0]
+    out[rows, idx[rows]] += g[rows]
+    return out
 
 
 def sparse_blocked_fp64(element_mars, params, nids, cids, pids, block_size, clamp=1e-45):

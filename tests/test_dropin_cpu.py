@@ -132,3 +132,65 @@ def test_no_grad_uses_direct_path():
     with torch.no_grad():
         lse(fake(x))
     assert [c[0] for c in ext.calls] == ["fwd_robust"]
+
+
+# ---------------------------------------------------------------------------
+# make_selective_log_softmax (trl.trainer.utils.selective_log_softmax drop-in)
+# ---------------------------------------------------------------------------
+class FakeSelExt:
+    def __init__(self):
+        self.calls = []
+
+    def selective_log_softmax_float(self, logits, index, robust=True):
+        self.calls.append(("fwd", tuple(logits.shape), tuple(index.shape), index.dtype, robust))
+        assert logits.dim() == 2 and logits.is_contiguous() and index.dim() == 1
+        lt = logits.as_subclass(torch.Tensor)
+        lse = torch.logsumexp(lt, -1)
+        logp = lt.gather(-1, index.as_subclass(torch.Tensor)[:, None])[:, 0] - lse
+        return logp.as_subclass(FakeCuda), lse.as_subclass(FakeCuda)
+
+    def selective_log_softmax_float_backward(self, g, logits, index, lse):
+        self.calls.append(("bwd", tuple(g.shape), tuple(logits.shape), tuple(index.shape), tuple(lse.shape)))
+        gt, lt, it, st = (t.as_subclass(torch.Tensor) for t in (g, logits, index, lse))
+        out = -gt[:, None] * torch.exp(lt - st[:, None])
+        out[torch.arange(len(it)), it] += gt
+        return out.as_subclass(FakeCuda)
+
+
+def test_selective_dispatch_shapes_and_autograd():
+    from fuselse_amd.selective import make_selective_log_softmax
+
+    ext = FakeSelExt()
+    sls = make_selective_log_softmax(ext)
+    logits = torch.randn(2, 3, 11, requires_grad=True)
+    index = torch.randint(0, 11, (2, 3), dtype=torch.int32)
+    y = sls(fake(logits), fake(index))
+    assert y.shape == (2, 3)
+    assert ext.calls[0] == ("fwd", (6, 11), (6,), torch.int64, True)
+    w = torch.randn(2, 3)
+    (y.as_subclass(torch.Tensor) * w).sum().backward()
+    assert ext.calls[-1][0] == "bwd" and ext.calls[-1][1:] == ((6,), (6, 11), (6,), (6,))
+    l2 = logits.detach().clone().requires_grad_(True)
+    ref = torch.log_softmax(l2, -1).gather(-1, index.long()[..., None])[..., 0]
+    (ref * w).sum().backward()
+    torch.testing.assert_close(logits.grad, l2.grad)
+    torch.testing.assert_close(y.as_subclass(torch.Tensor), ref.detach())
+
+
+def test_selective_fallbacks_do_not_touch_the_extension():
+    from fuselse_amd.selective import make_selective_log_softmax
+
+    seen = []
+
+    def original(logits, index):
+        seen.append(logits.dtype)
+        return torch.zeros(index.shape)
+
+    ext = FakeSelExt()
+    sls = make_selective_log_softmax(ext, original=original)
+    idx = torch.zeros(3, dtype=torch.int64)
+    sls(torch.randn(3, 5), idx)                                   # CPU
+    sls(fake(torch.randn(3, 5).bfloat16()), fake(idx))            # bf16
+    sls(fake(torch.randn(3, 5, dtype=torch.float64)), fake(idx))  # fp64
+    sls(fake(torch.randn(3, 5)), fake(torch.zeros(4, dtype=torch.int64)))  # shape mismatch
+    assert ext.calls == [] and len(seen) == 4

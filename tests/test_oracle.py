@@ -412,3 +412,74 @@ def test_fuselse_cpu_port_envelope_and_pair():
     x = (rng.random((64, 128256), dtype=np.float32) * np.float32(100.0) - np.float32(100.0))
     e = np.abs(O.fuselse_cpu_rows(x) - O.fp64_lse_ref(x)).mean()
     assert abs(e / 1.06e-4 - 1) < 0.25, e
+
+
+# ---------------------------------------------------------------------------
+# selective log-softmax (trl.trainer.utils.selective_log_softmax, fp32 branch)
+# ---------------------------------------------------------------------------
+def test_selective_logsoftmax_fp64_against_scipy_and_closed_forms():
+    from scipy.special import log_softmax
+
+    rng = np.random.default_rng(12)
+    x = (rng.standard_normal((40, 257)) * 4).astype(np.float32)
+    idx = rng.integers(0, 257, 40)
+    logp, lse = O.selective_logsoftmax_fp64(x, idx)
+    want = np.take_along_axis(log_softmax(x.astype(np.float64), axis=-1), idx[:, None], axis=-1)[:, 0]
+    np.testing.assert_allclose(logp, want, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(lse, O.lse_fp64(x), rtol=0)
+    # the probabilities of all targets of a row sum to one
+    allp = np.stack([O.selective_logsoftmax_fp64(x[:3], np.full(3, t))[0] for t in range(257)], axis=1)
+    np.testing.assert_allclose(np.exp(allp).sum(axis=1), 1.0, rtol=1e-12)
+    # N = 2: logp of the first of (a, b) is -log1p(exp(b - a))
+    a, b = 1.25, -2.0
+    lp, _ = O.selective_logsoftmax_fp64(np.array([[a, b]]), np.array([0]))
+    assert math.isclose(lp[0], -math.log1p(math.exp(b - a)), rel_tol=1e-13)
+    # an index outside [0, N) gives NaN
+    lp, _ = O.selective_logsoftmax_fp64(x[:4], np.array([-1, 257, 3, 10 ** 9]))
+    assert np.isnan(lp[0]) and np.isnan(lp[1]) and not np.isnan(lp[2]) and np.isnan(lp[3])
+
+
+def test_selective_logsoftmax_bwd_fp64_against_finite_differences_and_torch():
+    import torch
+
+    rng = np.random.default_rng(13)
+    x = rng.standard_normal((3, 9)) * 2
+    idx = np.array([0, 4, 8])
+    g = rng.standard_normal(3)
+    _, lse = O.selective_logsoftmax_fp64(x, idx)
+    got = O.selective_logsoftmax_bwd_fp64(g, x, idx, lse)
+    # central differences of sum_r g[r] * logp[r]
+    h = 1e-6
+    fd = np.zeros_like(x)
+    for r in range(3):
+        for i in range(9):
+            xp, xm = x.copy(), x.copy()
+            xp[r, i] += h
+            xm[r, i] -= h
+            fp = (g * O.selective_logsoftmax_fp64(xp, idx)[0]).sum()
+            fm = (g * O.selective_logsoftmax_fp64(xm, idx)[0]).sum()
+            fd[r, i] = (fp - fm) / (2 * h)
+    np.testing.assert_allclose(got, fd, rtol=1e-6, atol=1e-8)
+    np.testing.assert_allclose(got.sum(axis=1), 0.0, atol=1e-12)
+    xt = torch.from_numpy(x).requires_grad_(True)
+    lp = torch.log_softmax(xt, -1).gather(-1, torch.from_numpy(idx)[:, None])[:, 0]
+    (lp * torch.from_numpy(g)).sum().backward()
+    np.testing.assert_allclose(got, xt.grad.numpy(), rtol=1e-12, atol=1e-14)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float64", "bfloat16"])
+def test_trl_algorithm_fallback_matches_oracle(dtype):
+    """The package's restatement of trl's algorithm, used for inputs the kernels
+    do not take, against the fp64 oracle on the CPU."""
+    import torch
+
+    from fuselse_amd.selective import _trl_algorithm
+
+    rng = np.random.default_rng(14)
+    x = (rng.standard_normal((2, 5, 300)) * 3).astype(np.float32)
+    idx = rng.integers(0, 300, (2, 5))
+    xt = torch.from_numpy(x).to(getattr(torch, dtype))
+    got = _trl_algorithm(xt, torch.from_numpy(idx)).double().numpy()
+    want, _ = O.selective_logsoftmax_fp64(xt.double().numpy().reshape(10, 300), idx.reshape(10))
+    tol = 2e-2 if dtype == "bfloat16" else 1e-5
+    np.testing.assert_allclose(got.reshape(10), want, rtol=tol, atol=tol)
