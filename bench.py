@@ -186,6 +186,13 @@ def measure_configs(torch, ext, dev, stream, iters=50):
             bufs = [(torch.randn(b, n, device=dev, generator=gen) * 2).to(dt) for _ in range(nb)]
             ms = _time_calls(torch, stream, lambda i: fn(bufs[i % nb]), nb, iters)
             rec(f"C3_{tag}_fwd_{b}x{n}", ms, 2 * b * n + 4 * b)
+            if n > 256:
+                # the fused half backward (fp32 grad and lse, half x and grad_x)
+                gsv = torch.randn(b, device=dev, generator=gen)
+                lses = [fn(x) for x in bufs]
+                ms = _time_calls(torch, stream,
+                                 lambda i: ext.onepass_lse_half_backward(gsv, bufs[i % nb], lses[i % nb]), nb, iters)
+                rec(f"C3_{tag}_bwd_{b}x{n}", ms, 4 * b * n + 8 * b)
             del bufs
     # Few long rows (fp32, robust): the split-row path (fl_lse_fwd_f32_ws, the
     # Python shim's choice for B < 320) beside the one-block-per-row kernel of
@@ -442,10 +449,10 @@ def main():
                 "plain_us": round(fwd_plain_ms * 1e3, 2)},
         "bwd": {"us": round(bwd_ms * 1e3, 2), "gbps": round(bwd_gbps, 1),
                 "pct_peak": round(100 * bwd_gbps * 1e9 / HBM_PEAK, 2), "bytes": BWD_BYTES},
-        "roofline": {"bound": "hbm", "kernel": "lse_bwd_row_chunks<1> (fused backward)",
+        "roofline": {"bound": "hbm", "kernel": "lse_bwd_row_chunks<1, LseGrad> (fused backward)",
                      "achieved": round(bwd_gbps, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                      "frac": round(bwd_gbps * 1e9 / HBM_PEAK, 4), "traffic": traffic},
-        "roofline_fwd": {"bound": "hbm", "kernel": "lse_fwd_block_rows<float,robust,512,2>",
+        "roofline_fwd": {"bound": "hbm", "kernel": "lse_fwd_block_rows<float, true, 512, 2, LseOut> (robust forward)",
                          "achieved": round(fwd_gbps, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                          "frac": round(fwd_gbps * 1e9 / HBM_PEAK, 4)},
         "cpu_baseline": cpu,

@@ -16,6 +16,11 @@ contract (fuselse/gpu/autograd.py:6-61):
 * a contiguous 2-D input without grad calls the kernel directly; other shapes
   are flattened to (rows, N), made contiguous, and reshaped back;
 * ``keepdim`` unsqueezes the last dimension.
+
+``half_inputs=True`` (not in the reference, whose drop-in sends fp16 to torch,
+autograd.py:40) also routes CUDA fp16 / bf16 tensors to the kernels: fp32
+accumulation, the result rounded to the input dtype as ``torch.logsumexp``
+returns it, and a fused half backward from the fp32 LSE.
 """
 
 from __future__ import annotations
@@ -23,10 +28,15 @@ from __future__ import annotations
 import torch
 
 
-def make_fuselse_logsumexp(ext, robust: bool = True):
+def make_fuselse_logsumexp(ext, robust: bool = True, half_inputs: bool = False):
     fwd = ext.onepass_lse_float_robust if robust else ext.onepass_lse_float
     bwd = ext.onepass_lse_float_backward
     torch_logsumexp = torch.logsumexp
+    half_fwd = {}
+    if half_inputs:
+        half_fwd = {torch.float16: lambda x: ext.batched_logsumexp_fp16(x, robust),
+                    torch.bfloat16: lambda x: ext.batched_logsumexp_bf16(x, robust)}
+        half_bwd = ext.onepass_lse_half_backward
 
     class _RowLSE(torch.autograd.Function):
         @staticmethod
@@ -44,19 +54,41 @@ def make_fuselse_logsumexp(ext, robust: bool = True):
             g = bwd(grad_out.reshape(-1).contiguous(), rows, lse)
             return g.reshape(ctx.in_shape)
 
+    class _HalfRowLSE(torch.autograd.Function):
+        """fp16 / bf16 rows: fp32 accumulation, the output rounded to the input
+        dtype (torch.logsumexp's dtype contract); the backward uses the fp32
+        LSE, not the rounded output."""
+
+        @staticmethod
+        def forward(ctx, inp):
+            n = inp.shape[-1]
+            rows = inp.reshape(-1, n).contiguous()
+            lse = half_fwd[inp.dtype](rows)
+            ctx.save_for_backward(rows, lse)
+            ctx.in_shape = tuple(inp.shape)
+            return lse.to(inp.dtype).reshape(inp.shape[:-1])
+
+        @staticmethod
+        def backward(ctx, grad_out):
+            rows, lse = ctx.saved_tensors
+            g = half_bwd(grad_out.reshape(-1).to(torch.float32).contiguous(), rows, lse)
+            return g.reshape(ctx.in_shape)
+
     def logsumexp(input, dim=-1, keepdim=False):
         last = input.dim() - 1
         d = dim if dim >= 0 else input.dim() + dim
-        if not (input.is_cuda and input.dtype == torch.float32 and d == last and input.shape[-1] >= 2):
+        half = input.dtype in half_fwd
+        if not (input.is_cuda and (input.dtype == torch.float32 or half) and d == last and input.shape[-1] >= 2):
             return torch_logsumexp(input, dim=dim, keepdim=keepdim)
         if torch.is_grad_enabled() and input.requires_grad:
-            out = _RowLSE.apply(input)
-        elif input.dim() == 2 and input.is_contiguous():
-            out = fwd(input)
+            out = (_HalfRowLSE if half else _RowLSE).apply(input)
         else:
             n = input.shape[-1]
-            out = fwd(input.reshape(-1, n).contiguous()).reshape(input.shape[:-1])
+            rows = input if (input.dim() == 2 and input.is_contiguous()) else input.reshape(-1, n).contiguous()
+            out = half_fwd[input.dtype](rows).to(input.dtype) if half else fwd(rows)
+            out = out.reshape(input.shape[:-1])
         return out.unsqueeze(-1) if keepdim else out
 
     logsumexp.fuselse_robust = robust
+    logsumexp.fuselse_half_inputs = half_inputs
     return logsumexp

@@ -146,6 +146,13 @@ __device__ __forceinline__ void store_stream(V v, void* p) {
 }
 struct bf16_t { uint16_t bits; };
 
+// fp32 -> bfloat16, round to nearest even; NaN stays a (quiet) NaN.
+__device__ __forceinline__ uint32_t bf16_rne_bits(float f) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
 template <typename T> struct Elem;
 template <> struct Elem<float> {
     static constexpr int kVec = 4;
@@ -153,6 +160,12 @@ template <> struct Elem<float> {
     __device__ static __forceinline__ void vec(const float* p, float (&o)[4]) {
         f32x4 v = load_stream<f32x4>(p);
         o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+    }
+    __device__ static __forceinline__ void put(float* p, float v) { *p = v; }
+    __device__ static __forceinline__ void put_vec(float* p, const float (&v)[4]) {
+        f32x4 t;
+        t.x = v[0]; t.y = v[1]; t.z = v[2]; t.w = v[3];
+        store_stream<f32x4>(t, p);
     }
 };
 template <> struct Elem<_Float16> {
@@ -162,6 +175,14 @@ template <> struct Elem<_Float16> {
         f16x8 v = load_stream<f16x8>(p);
 #pragma unroll
         for (int k = 0; k < 8; ++k) o[k] = (float)v[k];
+    }
+    // fp32 -> binary16 with v_cvt_f16_f32 (round to nearest even)
+    __device__ static __forceinline__ void put(_Float16* p, float v) { *p = (_Float16)v; }
+    __device__ static __forceinline__ void put_vec(_Float16* p, const float (&v)[8]) {
+        f16x8 t;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) t[k] = (_Float16)v[k];
+        store_stream<f16x8>(t, p);
     }
 };
 template <> struct Elem<bf16_t> {
@@ -176,6 +197,13 @@ template <> struct Elem<bf16_t> {
             o[2 * k] = __builtin_bit_cast(float, v[k] << 16);
             o[2 * k + 1] = __builtin_bit_cast(float, v[k] & 0xFFFF0000u);
         }
+    }
+    __device__ static __forceinline__ void put(bf16_t* p, float v) { p->bits = (uint16_t)bf16_rne_bits(v); }
+    __device__ static __forceinline__ void put_vec(bf16_t* p, const float (&v)[8]) {
+        u32x4 t;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) t[k] = bf16_rne_bits(v[2 * k]) | (bf16_rne_bits(v[2 * k + 1]) << 16);
+        store_stream<u32x4>(t, p);
     }
 };
 

@@ -10,8 +10,9 @@
 //   * block rows  : one 256..1024-thread block per row for long rows;
 //   * split rows  : S blocks per row for few long rows, then a merge kernel
 //                   (partials in a caller workspace);
-// Backward: grad * exp2((x - lse) * log2 e), 16-byte loads and stores, with
-// grad[r] and lse[r] wave-uniform.
+// Backward: grad * exp2((x - lse) * log2 e), 16-byte loads and stores (fp32,
+// fp16 or bf16 x and grad_x, fp32 arithmetic), grad[r] and lse[r]
+// wave-uniform.
 #include <stdint.h>
 
 #include "../../include/fuselse_amd.h"
@@ -350,24 +351,20 @@ __device__ __forceinline__ float bwd_elem(float gv, float lse, float xv) {
     return gv * fexp2((xv - lse) * kLog2e);
 }
 
-// grad * exp(x - lse) for four elements.  For |lse| < 64 the exponent is one
-// FMA, x*log2e - lse*log2e, whose shared rounding of lse*log2e costs at most
-// 64*log2e*2^-24 (4e-6 relative); larger |lse| use the exact difference.
-__device__ __forceinline__ f32x4 bwd_vec(float gv, float lv, bool fma_ok, f32x4 v) {
-    f32x4 r;
+// grad * exp(x - lse) over one vector of VE values, in place.  For |lse| < 64
+// the exponent is one FMA, x*log2e - lse*log2e, whose shared rounding of
+// lse*log2e costs at most 64*log2e*2^-24 (4e-6 relative); larger |lse| use
+// the exact difference.
+template <int VE>
+__device__ __forceinline__ void bwd_vals(float gv, float lv, bool fma_ok, float (&v)[VE]) {
     if (fma_ok) {
         const float nb = -lv * kLog2e;
-        r.x = gv * fexp2(__builtin_fmaf(v.x, kLog2e, nb));
-        r.y = gv * fexp2(__builtin_fmaf(v.y, kLog2e, nb));
-        r.z = gv * fexp2(__builtin_fmaf(v.z, kLog2e, nb));
-        r.w = gv * fexp2(__builtin_fmaf(v.w, kLog2e, nb));
+#pragma unroll
+        for (int k = 0; k < VE; ++k) v[k] = gv * fexp2(__builtin_fmaf(v[k], kLog2e, nb));
     } else {
-        r.x = bwd_elem(gv, lv, v.x);
-        r.y = bwd_elem(gv, lv, v.y);
-        r.z = bwd_elem(gv, lv, v.z);
-        r.w = bwd_elem(gv, lv, v.w);
+#pragma unroll
+        for (int k = 0; k < VE; ++k) v[k] = bwd_elem(gv, lv, v[k]);
     }
-    return r;
 }
 
 // Backward targets.  LseGrad: grad_x = g * softmax.  SelGrad (selective
@@ -387,93 +384,103 @@ struct SelGrad {
 };
 
 // SEL: adds gv to the element of r that sits at column t, if any; c0 is the
-// column of r.x.
-template <bool SEL>
-__device__ __forceinline__ f32x4 add_at(f32x4 r, int64_t c0, int64_t t, float gv) {
-    if constexpr (!SEL) return r;
-    const int64_t d = t - c0;
-    if ((uint64_t)d < 4u) {
-        r.x += d == 0 ? gv : 0.0f;
-        r.y += d == 1 ? gv : 0.0f;
-        r.z += d == 2 ? gv : 0.0f;
-        r.w += d == 3 ? gv : 0.0f;
+// column of r[0].
+template <bool SEL, int VE>
+__device__ __forceinline__ void add_at(float (&r)[VE], int64_t c0, int64_t t, float gv) {
+    if constexpr (SEL) {
+        const int64_t d = t - c0;
+        if ((uint64_t)d < (uint64_t)VE) {
+#pragma unroll
+            for (int k = 0; k < VE; ++k) r[k] += d == k ? gv : 0.0f;
+        }
     }
-    return r;
+}
+
+// One element at column c of a row (scalar head / tail / fallback paths).
+template <typename T, typename GR>
+__device__ __forceinline__ void bwd_one(T* gr, const T* xr, int64_t c, float gv, float lv, int64_t t, float g0) {
+    Elem<T>::put(gr + c, bwd_elem(gv, lv, Elem<T>::scalar(xr + c)) + (GR::kSel && c == t ? g0 : 0.0f));
+}
+
+// One 16-byte vector i of a row body whose first column is head.
+template <typename T, typename GR>
+__device__ __forceinline__ void bwd_vec(T* body_g, const T* body_x, int64_t i, int64_t head, float gv, float lv,
+                                        bool fma_ok, int64_t t, float g0) {
+    constexpr int VE = Elem<T>::kVec;
+    float v[VE];
+    Elem<T>::vec(body_x + i * VE, v);
+    bwd_vals<VE>(gv, lv, fma_ok, v);
+    add_at<GR::kSel, VE>(v, head + VE * i, t, g0);
+    Elem<T>::put_vec(body_g + i * VE, v);
 }
 
 // Long rows: grid = B * chunks_per_row blocks of 256 threads; a block covers
 // 256*U consecutive vectors of one row.  x and grad_x share their alignment.
-template <int U, typename GR>
-__global__ __launch_bounds__(256) void lse_bwd_row_chunks(const float* __restrict__ g, const float* __restrict__ x,
-                                                          const float* __restrict__ lse, float* __restrict__ gx,
+template <typename T, int U, typename GR>
+__global__ __launch_bounds__(256) void lse_bwd_row_chunks(const float* __restrict__ g, const T* __restrict__ x,
+                                                          const float* __restrict__ lse, T* __restrict__ gx,
                                                           int64_t N, int64_t chunks_per_row, GR gr_t) {
+    constexpr int VE = Elem<T>::kVec;
     const int64_t blk = blockIdx.x;
     const int64_t row = blk / chunks_per_row;
     const int64_t chunk = blk - row * chunks_per_row;
     const int tid = threadIdx.x;
-    const float* xr = x + row * N;
-    float* gr = gx + row * N;
+    const T* xr = x + row * N;
+    T* gr = gx + row * N;
     const RowSplit sp = split_row(xr, N);
     const float g0 = g[row];
     const float gv = gr_t.coef(row, g0);
     const int64_t t = gr_t.target(row);
     const float lv = lse[row];
     if (chunk == 0) {
-        if (tid < sp.head) gr[tid] = bwd_elem(gv, lv, xr[tid]) + (GR::kSel && tid == t ? g0 : 0.0f);
-        const int64_t t0 = sp.head + sp.nvec * 4;
-        if (tid < sp.tail) gr[t0 + tid] = bwd_elem(gv, lv, xr[t0 + tid]) + (GR::kSel && t0 + tid == t ? g0 : 0.0f);
+        if (tid < sp.head) bwd_one<T, GR>(gr, xr, tid, gv, lv, t, g0);
+        if (tid < sp.tail) bwd_one<T, GR>(gr, xr, sp.head + sp.nvec * VE + tid, gv, lv, t, g0);
     }
-    const f32x4* xb = reinterpret_cast<const f32x4*>(xr + sp.head);
-    f32x4* gb = reinterpret_cast<f32x4*>(gr + sp.head);
+    const T* xb = xr + sp.head;
+    T* gb = gr + sp.head;
     const bool fma_ok = __builtin_fabsf(lv) < 64.0f;
     const int64_t i0 = chunk * 256 * U + tid;
-    f32x4 v[U];
+    if constexpr (U == 1) {
+        if (i0 < sp.nvec) bwd_vec<T, GR>(gb, xb, i0, sp.head, gv, lv, fma_ok, t, g0);
+    } else {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int64_t i = i0 + (int64_t)u * 256;
-        if (i < sp.nvec) v[u] = load_stream<f32x4>(xb + i);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int64_t i = i0 + (int64_t)u * 256;
-        if (i < sp.nvec)
-            store_stream<f32x4>(add_at<GR::kSel>(bwd_vec(gv, lv, fma_ok, v[u]), sp.head + 4 * i, t, g0), gb + i);
+        for (int u = 0; u < U; ++u) {
+            const int64_t i = i0 + (int64_t)u * 256;
+            if (i < sp.nvec) bwd_vec<T, GR>(gb, xb, i, sp.head, gv, lv, fma_ok, t, g0);
+        }
     }
 }
 
 // Short rows: LPR lanes per row, 256/LPR rows per block, grid-stride.
-template <int LPR, typename GR>
-__global__ __launch_bounds__(256) void lse_bwd_group_rows(const float* __restrict__ g, const float* __restrict__ x,
-                                                          const float* __restrict__ lse, float* __restrict__ gx,
+template <typename T, int LPR, typename GR>
+__global__ __launch_bounds__(256) void lse_bwd_group_rows(const float* __restrict__ g, const T* __restrict__ x,
+                                                          const float* __restrict__ lse, T* __restrict__ gx,
                                                           int64_t B, int64_t N, GR gr_t) {
+    constexpr int VE = Elem<T>::kVec;
     constexpr int RPB = 256 / LPR;
     const int gi = threadIdx.x / LPR;
     const int j = threadIdx.x % LPR;
     for (int64_t row = (int64_t)blockIdx.x * RPB + gi; row < B; row += (int64_t)gridDim.x * RPB) {
-        const float* xr = x + row * N;
-        float* gr = gx + row * N;
+        const T* xr = x + row * N;
+        T* gr = gx + row * N;
         const RowSplit sp = split_row(xr, N);
         const float g0 = g[row];
         const float gv = gr_t.coef(row, g0);
         const int64_t t = gr_t.target(row);
         const float lv = lse[row];
-        for (int64_t h = j; h < sp.head; h += LPR) gr[h] = bwd_elem(gv, lv, xr[h]) + (GR::kSel && h == t ? g0 : 0.0f);
-        const int64_t t0 = sp.head + sp.nvec * 4;
-        for (int64_t c = j; c < sp.tail; c += LPR)
-            gr[t0 + c] = bwd_elem(gv, lv, xr[t0 + c]) + (GR::kSel && t0 + c == t ? g0 : 0.0f);
-        const f32x4* xb = reinterpret_cast<const f32x4*>(xr + sp.head);
-        f32x4* gb = reinterpret_cast<f32x4*>(gr + sp.head);
+        for (int64_t h = j; h < sp.head; h += LPR) bwd_one<T, GR>(gr, xr, h, gv, lv, t, g0);
+        const int64_t t0 = sp.head + sp.nvec * VE;
+        for (int64_t c = j; c < sp.tail; c += LPR) bwd_one<T, GR>(gr, xr, t0 + c, gv, lv, t, g0);
         const bool fma_ok = __builtin_fabsf(lv) < 64.0f;
         for (int64_t i = j; i < sp.nvec; i += LPR)
-            store_stream<f32x4>(
-                add_at<GR::kSel>(bwd_vec(gv, lv, fma_ok, load_stream<f32x4>(xb + i)), sp.head + 4 * i, t, g0), gb + i);
+            bwd_vec<T, GR>(gr + sp.head, xr + sp.head, i, sp.head, gv, lv, fma_ok, t, g0);
     }
 }
 
 // Fallback when x and grad_x differ in 16-byte alignment: scalar grid-stride.
-template <typename GR>
-__global__ __launch_bounds__(256) void lse_bwd_scalar(const float* __restrict__ g, const float* __restrict__ x,
-                                                      const float* __restrict__ lse, float* __restrict__ gx,
+template <typename T, typename GR>
+__global__ __launch_bounds__(256) void lse_bwd_scalar(const float* __restrict__ g, const T* __restrict__ x,
+                                                      const float* __restrict__ lse, T* __restrict__ gx,
                                                       int64_t B, int64_t N, GR gr_t) {
     for (int64_t row = blockIdx.y; row < B; row += gridDim.y) {
         const float g0 = g[row];
@@ -481,27 +488,28 @@ __global__ __launch_bounds__(256) void lse_bwd_scalar(const float* __restrict__ 
         const int64_t t = gr_t.target(row);
         const float lv = lse[row];
         for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < N; i += (int64_t)gridDim.x * 256)
-            gx[row * N + i] = bwd_elem(gv, lv, x[row * N + i]) + (GR::kSel && i == t ? g0 : 0.0f);
+            bwd_one<T, GR>(gx + row * N, x + row * N, i, gv, lv, t, g0);
     }
 }
 
-template <typename GR>
-static void launch_bwd(const float* g, const float* x, const float* lse, float* gx, int64_t B, int64_t N, GR gr_t,
+template <typename T, typename GR>
+static void launch_bwd(const float* g, const T* x, const float* lse, T* gx, int64_t B, int64_t N, GR gr_t,
                        hipStream_t st) {
+    constexpr int VE = Elem<T>::kVec;
     const bool same_align = ((reinterpret_cast<uintptr_t>(x) ^ reinterpret_cast<uintptr_t>(gx)) & 15u) == 0;
     if (!same_align) {
         int64_t gxdim = (N + 255) / 256;
         if (gxdim > 1024) gxdim = 1024;
         int64_t gydim = B < 65535 ? B : 65535;
-        lse_bwd_scalar<<<dim3((unsigned)gxdim, (unsigned)gydim), dim3(256), 0, st>>>(g, x, lse, gx, B, N, gr_t);
+        lse_bwd_scalar<T><<<dim3((unsigned)gxdim, (unsigned)gydim), dim3(256), 0, st>>>(g, x, lse, gx, B, N, gr_t);
         return;
     }
-    const int64_t vecs = N / 4 + 1;
+    const int64_t vecs = N / VE + 1;
     if (vecs >= 1024) {
-        // one 16-byte vector per lane: measured best (with 128x2 and 1024x1)
+        // one 16-byte vector per lane: measured best for fp32 (with 128x2 and 1024x1)
         constexpr int U = 1;
         const int64_t cpr = (vecs + 256 * U - 1) / (256 * U);
-        lse_bwd_row_chunks<U><<<dim3((unsigned)(B * cpr)), dim3(256), 0, st>>>(g, x, lse, gx, N, cpr, gr_t);
+        lse_bwd_row_chunks<T, U><<<dim3((unsigned)(B * cpr)), dim3(256), 0, st>>>(g, x, lse, gx, N, cpr, gr_t);
         return;
     }
     int64_t lpr = pow2_ceil((vecs + 3) / 4);
@@ -511,26 +519,27 @@ static void launch_bwd(const float* g, const float* x, const float* lse, float* 
     if (grid > (int64_t)1 << 30) grid = (int64_t)1 << 30;
     const dim3 gd((unsigned)grid), blk(256);
     switch (lpr) {
-    case 4: lse_bwd_group_rows<4><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
-    case 8: lse_bwd_group_rows<8><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
-    case 16: lse_bwd_group_rows<16><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
-    case 32: lse_bwd_group_rows<32><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
-    case 64: lse_bwd_group_rows<64><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
-    case 128: lse_bwd_group_rows<128><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
-    default: lse_bwd_group_rows<256><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
+    case 4: lse_bwd_group_rows<T, 4><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
+    case 8: lse_bwd_group_rows<T, 8><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
+    case 16: lse_bwd_group_rows<T, 16><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
+    case 32: lse_bwd_group_rows<T, 32><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
+    case 64: lse_bwd_group_rows<T, 64><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
+    case 128: lse_bwd_group_rows<T, 128><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
+    default: lse_bwd_group_rows<T, 256><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
     }
 }
 
-template <typename GR>
-static int bwd_entry(const char* name, const float* grad, const float* x, const float* lse, float* grad_x, int64_t B,
+template <typename T, typename GR>
+static int bwd_entry(const char* name, const float* grad, const T* x, const float* lse, T* grad_x, int64_t B,
                      int64_t N, GR gr_t, void* stream) {
+    constexpr int VE = Elem<T>::kVec;
     FL_CHECK(B >= 0 && N >= 0, "%s: negative shape (B=%lld, N=%lld)", name, (long long)B, (long long)N);
     if (B == 0 || N == 0) return ok();
     FL_CHECK(grad && x && lse && grad_x, "%s: NULL pointer argument", name);
-    FL_CHECK((reinterpret_cast<uintptr_t>(x) & 3u) == 0 && (reinterpret_cast<uintptr_t>(grad_x) & 3u) == 0,
-             "%s: x / grad_x are not 4-byte aligned", name);
-    FL_CHECK(B * ((N / 4 + 1 + 255) / 256) < ((int64_t)1 << 32), "%s: B*N too large for the grid", name);
-    launch_bwd(grad, x, lse, grad_x, B, N, gr_t, reinterpret_cast<hipStream_t>(stream));
+    FL_CHECK((reinterpret_cast<uintptr_t>(x) % sizeof(T)) == 0 && (reinterpret_cast<uintptr_t>(grad_x) % sizeof(T)) == 0,
+             "%s: x / grad_x are not element-aligned", name);
+    FL_CHECK(B * ((N / VE + 1 + 255) / 256) < ((int64_t)1 << 32), "%s: B*N too large for the grid", name);
+    launch_bwd<T>(grad, x, lse, grad_x, B, N, gr_t, reinterpret_cast<hipStream_t>(stream));
     return launch_status(name);
 }
 
@@ -576,7 +585,19 @@ extern "C" int fl_lse_fwd_bf16_ws(const void* x, float* out, int64_t B, int64_t 
 
 extern "C" int fl_lse_bwd_f32(const float* grad, const float* x, const float* lse, float* grad_x, int64_t B,
                               int64_t N, void* stream) {
-    return bwd_entry("fl_lse_bwd_f32", grad, x, lse, grad_x, B, N, LseGrad{}, stream);
+    return bwd_entry<float>("fl_lse_bwd_f32", grad, x, lse, grad_x, B, N, LseGrad{}, stream);
+}
+
+extern "C" int fl_lse_bwd_f16(const float* grad, const void* x, const float* lse, void* grad_x, int64_t B, int64_t N,
+                              void* stream) {
+    return bwd_entry<_Float16>("fl_lse_bwd_f16", grad, static_cast<const _Float16*>(x), lse,
+                               static_cast<_Float16*>(grad_x), B, N, LseGrad{}, stream);
+}
+
+extern "C" int fl_lse_bwd_bf16(const float* grad, const void* x, const float* lse, void* grad_x, int64_t B,
+                               int64_t N, void* stream) {
+    return bwd_entry<bf16_t>("fl_lse_bwd_bf16", grad, static_cast<const bf16_t*>(x), lse,
+                             static_cast<bf16_t*>(grad_x), B, N, LseGrad{}, stream);
 }
 
 extern "C" int fl_selective_logsoftmax_f32(const float* x, const int64_t* index, float* logp, float* lse, int64_t B,
@@ -594,5 +615,5 @@ extern "C" int fl_selective_logsoftmax_bwd_f32(const float* grad, const float* x
                                                const float* lse, float* grad_x, int64_t B, int64_t N, void* stream) {
     const char* name = "fl_selective_logsoftmax_bwd_f32";
     FL_CHECK(index != nullptr || B == 0 || N == 0, "%s: NULL pointer argument", name);
-    return bwd_entry(name, grad, x, lse, grad_x, B, N, SelGrad{index}, stream);
+    return bwd_entry<float>(name, grad, x, lse, grad_x, B, N, SelGrad{index}, stream);
 }

@@ -175,6 +175,33 @@ def _fwd_half(x: torch.Tensor, dtype: torch.dtype, entry: str, dtype_msg: str, r
     return out
 
 
+def onepass_lse_half_backward(grad_output: torch.Tensor, x: torch.Tensor, lse_output: torch.Tensor) -> torch.Tensor:
+    """grad_input = grad_output[:, None] * exp(x - lse_output[:, None]) for fp16 or
+    bf16 x (B, N), fp32 grad_output and lse_output (B,); the result has x's
+    dtype (fp32 arithmetic, round to nearest even).  No reference
+    counterpart: the fp32 backward's contract (fused_fp32_kernel.cu:196-252)
+    at half storage."""
+    _check(grad_output.is_cuda and x.is_cuda and lse_output.is_cuda, "grad_output, x and lse_output must be CUDA")
+    _check(x.dtype in (torch.float16, torch.bfloat16), "x must be float16 or bfloat16")
+    _check(grad_output.dtype == torch.float32 and lse_output.dtype == torch.float32,
+           "grad_output and lse_output must be float32")
+    _check(x.dim() == 2, "x must be 2D (B, N)")
+    _check(grad_output.dim() == 1 and lse_output.dim() == 1, "grad_output and lse_output must be 1D (B)")
+    _check(x.is_contiguous() and grad_output.is_contiguous() and lse_output.is_contiguous(),
+           "inputs must be contiguous")
+    _check(grad_output.size(0) == x.size(0) and lse_output.size(0) == x.size(0),
+           "grad_output and lse_output batch dimensions must match x")
+    B, N = x.shape
+    grad_input = torch.empty_like(x)
+    if B * N == 0:
+        return grad_input
+    entry = "fl_lse_bwd_f16" if x.dtype == torch.float16 else "fl_lse_bwd_bf16"
+    with _on_device(x):
+        _lib.call(entry, grad_output.data_ptr(), x.data_ptr(), lse_output.data_ptr(), grad_input.data_ptr(), B, N,
+                  _stream(x))
+    return grad_input
+
+
 def batched_logsumexp_fp16(x: torch.Tensor, robust: bool = False) -> torch.Tensor:
     """fp16 (B, N) -> fp32 (B,) LSE with fp32 accumulation
     (fused_fp16_kernel.cu:112-132)."""

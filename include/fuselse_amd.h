@@ -80,6 +80,19 @@ int fl_lse_fwd_f16(const void* x, float* out, int64_t B, int64_t N, int robust, 
 int fl_lse_fwd_bf16(const void* x, float* out, int64_t B, int64_t N, int robust, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Half-precision backward: grad_x[r, i] = grad[r] * exp(x[r, i] - lse[r]),
+ * computed in fp32 and rounded to nearest even into the input type.  grad
+ * and lse are fp32 [B] (lse as the half forward above returns it), x and
+ * grad_x binary16 / bfloat16 [B, N].  The reference has no half backward
+ * (its drop-in sends fp16 to torch, fuselse/gpu/autograd.py:40); this is the
+ * fl_lse_bwd_f32 contract at half storage.
+ * ------------------------------------------------------------------------- */
+int fl_lse_bwd_f16(const float* grad, const void* x, const float* lse, void* grad_x, int64_t B, int64_t N,
+                   void* stream);
+int fl_lse_bwd_bf16(const float* grad, const void* x, const float* lse, void* grad_x, int64_t B, int64_t N,
+                    void* stream);
+
+/* ---------------------------------------------------------------------------
  * Forward with a caller workspace, for few long rows.  The reference launches
  * one block per row (fused_fp32_kernel.cu:168-170, fused_fp16_kernel.cu:
  * 127-129), which leaves most of the GPU idle when B is small against the

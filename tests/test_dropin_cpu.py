@@ -39,6 +39,22 @@ class FakeExt:
         assert x.dim() == 2 and x.is_contiguous()
         return torch.logsumexp(x.as_subclass(torch.Tensor), -1).as_subclass(FakeCuda)
 
+    def batched_logsumexp_fp16(self, x, robust=False):
+        self._rec("fwd_fp16", x)
+        assert x.dtype == torch.float16 and x.dim() == 2 and x.is_contiguous()
+        return torch.logsumexp(x.as_subclass(torch.Tensor).float(), -1).as_subclass(FakeCuda)
+
+    def batched_logsumexp_bf16(self, x, robust=False):
+        self._rec("fwd_bf16", x)
+        assert x.dtype == torch.bfloat16 and x.dim() == 2 and x.is_contiguous()
+        return torch.logsumexp(x.as_subclass(torch.Tensor).float(), -1).as_subclass(FakeCuda)
+
+    def onepass_lse_half_backward(self, g, x, lse):
+        self._rec("bwd_half", g, x, lse)
+        assert g.dtype == torch.float32 and lse.dtype == torch.float32 and x.dtype in (torch.float16, torch.bfloat16)
+        gt, xt, lt = (t.as_subclass(torch.Tensor) for t in (g, x, lse))
+        return (gt[:, None] * torch.exp(xt.float() - lt[:, None])).to(x.dtype).as_subclass(FakeCuda)
+
     def onepass_lse_float_backward(self, g, x, lse):
         self._rec("bwd", g, x, lse)
         assert g.dim() == 1 and x.dim() == 2 and lse.dim() == 1
@@ -194,3 +210,24 @@ def test_selective_fallbacks_do_not_touch_the_extension():
     sls(fake(torch.randn(3, 5, dtype=torch.float64)), fake(idx))  # fp64
     sls(fake(torch.randn(3, 5)), fake(torch.zeros(4, dtype=torch.int64)))  # shape mismatch
     assert ext.calls == [] and len(seen) == 4
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_half_inputs_policy(dtype):
+    """half_inputs=True sends CUDA fp16/bf16 rows to the half kernels; the result
+    has the input dtype; the backward gets the fp32 LSE and returns the input
+    dtype.  The default keeps the reference's fallback."""
+    ext = FakeExt()
+    tag = "fwd_fp16" if dtype == torch.float16 else "fwd_bf16"
+    lse = make_fuselse_logsumexp(ext, half_inputs=True)
+    x = torch.randn(2, 3, 10).to(dtype)
+    y = lse(fake(x))
+    assert y.dtype == dtype and y.shape == (2, 3) and ext.calls[-1][0] == tag
+    xg = x.clone().requires_grad_(True)
+    y = lse(fake(xg), -1)
+    (y.as_subclass(torch.Tensor).float() * torch.randn(2, 3)).sum().backward()
+    assert ext.calls[-1][0] == "bwd_half" and ext.calls[-1][1] == [(6,), (6, 10), (6,)]
+    assert xg.grad.dtype == dtype
+    ext2 = FakeExt()
+    make_fuselse_logsumexp(ext2)(fake(x))
+    assert ext2.calls == []

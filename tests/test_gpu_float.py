@@ -230,3 +230,63 @@ def test_dropin_is_native(cuda):
     assert _lib._lib is not None
     maps = open("/proc/self/maps").read()
     assert "libfuselse_amd.so" in maps
+
+
+# ---------------------------------------------------------------------------
+# fp16 / bf16 backward (fp32 arithmetic, round to nearest even on store)
+# ---------------------------------------------------------------------------
+def _half_ulp(want: np.ndarray, dtype) -> np.ndarray:
+    """One unit in the last place of the half type at |want| (its subnormal
+    step below the normal range)."""
+    a = np.abs(want)
+    if dtype == torch.float16:
+        e = np.floor(np.log2(np.maximum(a, 2.0 ** -14)))
+        return 2.0 ** (e - 10)
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -126)))
+    return 2.0 ** (e - 7)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("B,N,off", [(5, 7, 0), (300, 1000, 0), (64, 50257, 0), (4, 128256, 0), (7, 4099, 3),
+                                     (3, 20001, 1)])
+def test_bwd_half_matches_fp64(cuda, dtype, B, N, off):
+    """Within one half ulp of the fp64 value of g * exp(x - lse) on the half
+    inputs (the rounding of the store), plus the fp32 arithmetic's 1e-5."""
+    print(f"case bwd_half {dtype} B={B} N={N} off={off}", flush=True)
+    rng = np.random.default_rng(B * 13 + N)
+    xh = torch.from_numpy((rng.standard_normal((B, N)) * 2).astype(np.float32)).to(dtype)
+    g = rng.standard_normal(B).astype(np.float32)
+    x64 = xh.double().numpy()
+    ext = _ext()
+    xd = _offset_view(xh, cuda, off)
+    lse = (ext.batched_logsumexp_fp16 if dtype == torch.float16 else ext.batched_logsumexp_bf16)(xd)
+    got = ext.onepass_lse_half_backward(torch.from_numpy(g).to(cuda), xd, lse)
+    assert got.dtype == dtype
+    got = got.double().cpu().numpy()
+    want = O.lse_bwd_fp64(g, x64, O.lse_fp64(x64))
+    err = np.abs(got - want)
+    bound = _half_ulp(want, dtype) + 1e-5 * np.abs(want)
+    assert (err <= bound).all(), (err / bound).max()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_dropin_half_inputs_autograd(cuda, dtype):
+    print(f"case drop-in half {dtype}", flush=True)
+    from fuselse_amd import make_fuselse_logsumexp
+
+    lse_fn = make_fuselse_logsumexp(_ext(), robust=True, half_inputs=True)
+    rng = np.random.default_rng(21)
+    xh = torch.from_numpy((rng.standard_normal((3, 40, 3001)) * 2).astype(np.float32)).to(dtype)
+    w = rng.standard_normal((3, 40)).astype(np.float32)
+    xd = xh.to(cuda).requires_grad_(True)
+    y = lse_fn(xd, dim=-1)
+    assert y.dtype == dtype and y.shape == (3, 40)
+    (y.float() * torch.from_numpy(w).to(cuda)).sum().backward()
+    x64 = xh.double().numpy().reshape(120, 3001)
+    want_y = O.lse_fp64(x64).reshape(3, 40)
+    assert (np.abs(y.detach().double().cpu().numpy() - want_y) <= _half_ulp(want_y, dtype)).all()
+    # the gradient reaching the half output is w rounded to the half dtype
+    w_half = torch.from_numpy(w).to(dtype).double().numpy()
+    want_g = O.lse_bwd_fp64(w_half.reshape(-1), x64, O.lse_fp64(x64)).reshape(3, 40, 3001)
+    got_g = xd.grad.double().cpu().numpy()
+    assert (np.abs(got_g - want_g) <= _half_ulp(want_g, dtype) + 1e-5 * np.abs(want_g)).all()
