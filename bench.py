@@ -295,7 +295,16 @@ def measure_configs(torch, ext, dev, stream, iters=50):
         ms = _time_calls(torch, stream, lambda i: ext.sparse_csr_forward(child, d_off, d_cid, d_lp, q16=q16, out=out),
                          1, max(5, iters // 5))
         rec(f"C5_sparse_csr_{tag}_1M_nodes_b512", ms, sbytes, nnz=nnz, alpha=2.0)
-    del child, out
+    # the fp32 backward (flows) of the same layer: per edge it reads the
+    # parent's grad_out and out rows, per child it reads and writes one row
+    out = ext.sparse_csr_forward(child, d_off, d_cid, d_lp)
+    gout = torch.rand(nodes, batch, device=dev, generator=gen)
+    csc = ext.sparse_csr_transpose(d_off, d_cid, nodes)
+    ms = _time_calls(torch, stream, lambda i: ext.sparse_csr_backward(child, out, gout, d_off, d_cid, d_lp, csc),
+                     1, max(5, iters // 5))
+    bbytes = 2 * nnz * batch * 4 + nnz * (4 + 4 + 4 + 4) + (nodes + 1) * 8 + 2 * nodes * batch * 4
+    rec("C5_sparse_csr_bwd_fp32_1M_nodes_b512", ms, bbytes, nnz=nnz, alpha=2.0)
+    del child, out, gout
     return res
 
 

@@ -341,10 +341,151 @@ static void launch(const LAYOUT& L, const float* child, const float* out_any, in
         sparse_kernel<Q16, false, LAYOUT><<<grid, dim3(256), 0, st>>>(L, child, batch, items);
 }
 
+// ---------------------------------------------------------------------------
+// CSR backward (flows).  For out[n, b] = LSE_e(lw_e + child[c_e, b]) and an
+// upstream gradient gout:
+//   term[e, b]       = gout[n_e, b] * exp(lw_e + child[c_e, b] - out[n_e, b])
+//   grad_child[c, b] = sum of term[e, b] over the edges e with c_e = c
+//   grad_lw[e]       = sum of term[e, b] over b
+// A term whose out[n_e, b] is -inf is 0: nothing flows through a node of
+// probability 0 (torch's autograd of logsumexp would give NaN there).
+// The kernel walks the transposed structure (CSC: for child c the edges that
+// point at it, each with its parent node): one wave per child row, every
+// 256-column tile of the batch in turn.  Each child row and each edge belongs
+// to one wave, so both gradients are written once, without atomics, and the
+// summation order is fixed.
+// ---------------------------------------------------------------------------
+struct ParentMeta {
+    int64_t node;
+    int64_t edge;
+    float lw;
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+    v += reduce_partner<1>(v);
+    v += reduce_partner<2>(v);
+    v += reduce_partner<4>(v);
+    v += reduce_partner<8>(v);
+    v += reduce_partner<16>(v);
+    v += reduce_partner<32>(v);
+    return v;
+}
+
+template <bool VEC>
+__device__ __forceinline__ bool col_ok(int64_t b0, int l, int64_t batch, int i) {
+    return VEC ? b0 + 4 * l < batch : b0 + l + 64 * i < batch;
+}
+
+constexpr int GB = 2;  // parent edges per load group (two rows each)
+
+template <bool VEC>
+__device__ __forceinline__ void load_parents(float (&gv)[GB][P], float (&ov)[GB][P], const ParentMeta& pw, int j,
+                                             int wn, const float* __restrict__ gout, const float* __restrict__ out,
+                                             int64_t batch, int64_t b0, int l) {
+#pragma unroll
+    for (int g = 0; g < GB; ++g) {
+        if (j + g < wn) {
+            const int64_t n = bcast64(pw.node, j + g);
+            Cols<VEC>::load(gout + n * batch, b0, l, batch, gv[g]);
+            Cols<VEC>::load(out + n * batch, b0, l, batch, ov[g]);
+        }
+    }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void flow_group(const float (&gv)[GB][P], const float (&ov)[GB][P], const ParentMeta& pw,
+                                           int j, int wn, const float (&cv)[P], float (&acc)[P], bool first_tile,
+                                           float* __restrict__ glogp, int64_t batch, int64_t b0, int l) {
+#pragma unroll
+    for (int g = 0; g < GB; ++g) {
+        if (j + g < wn) {
+            const float lw = bcastf(pw.lw, j + g);
+            float tsum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < P; ++i) {
+                const bool live = col_ok<VEC>(b0, l, batch, i) && ov[g][i] != -kInf;
+                const float t = live ? gv[g][i] * fexp2((lw + cv[i] - ov[g][i]) * kLog2e) : 0.0f;
+                acc[i] += t;
+                tsum += t;
+            }
+            tsum = wave_sum(tsum);
+            const int64_t e = bcast64(pw.edge, j + g);
+            if (l == 0) glogp[e] = first_tile ? tsum : glogp[e] + tsum;
+        }
+    }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void csr_bwd_kernel(const float* __restrict__ child, const float* __restrict__ out,
+                                                      const float* __restrict__ gout, const float* __restrict__ logp,
+                                                      const int64_t* __restrict__ csc_off,
+                                                      const int32_t* __restrict__ csc_edge,
+                                                      const int32_t* __restrict__ csc_node,
+                                                      float* __restrict__ gchild, float* __restrict__ glogp,
+                                                      int64_t children, int64_t batch) {
+    const int l = lane_id();
+    const int64_t c = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (c >= children) return;
+    const int64_t p0 = uniform64(csc_off[c]);
+    const int64_t k = uniform64(csc_off[c + 1]) - p0;
+    for (int64_t b0 = 0; b0 < batch; b0 += kTile) {
+        float cv[P], acc[P];
+        Cols<VEC>::load(child + c * batch, b0, l, batch, cv);
+#pragma unroll
+        for (int i = 0; i < P; ++i) acc[i] = 0.0f;
+        for (int64_t w0 = 0; w0 < k; w0 += 64) {
+            ParentMeta pw{0, 0, 0.0f};
+            if (w0 + l < k) {
+                const int64_t e = csc_edge[p0 + w0 + l];
+                pw = {(int64_t)csc_node[p0 + w0 + l], e, logp[e]};
+            }
+            const int wn = (int)(k - w0 < 64 ? k - w0 : 64);
+            const int ng = (wn + GB - 1) / GB;
+            float ga[GB][P], oa[GB][P], gb[GB][P], ob[GB][P];
+            load_parents<VEC>(ga, oa, pw, 0, wn, gout, out, batch, b0, l);
+            int gi = 0;
+            for (; gi + 1 < ng; gi += 2) {
+                load_parents<VEC>(gb, ob, pw, (gi + 1) * GB, wn, gout, out, batch, b0, l);
+                flow_group<VEC>(ga, oa, pw, gi * GB, wn, cv, acc, b0 == 0, glogp, batch, b0, l);
+                if (gi + 2 < ng) load_parents<VEC>(ga, oa, pw, (gi + 2) * GB, wn, gout, out, batch, b0, l);
+                flow_group<VEC>(gb, ob, pw, (gi + 1) * GB, wn, cv, acc, b0 == 0, glogp, batch, b0, l);
+            }
+            if (gi < ng) flow_group<VEC>(ga, oa, pw, gi * GB, wn, cv, acc, b0 == 0, glogp, batch, b0, l);
+        }
+        Cols<VEC>::store(gchild + c * batch, b0, l, batch, acc);
+    }
+}
+
 }  // namespace sparse
 }  // namespace fl
 
 using namespace fl;
+
+extern "C" int fl_sparse_csr_bwd(const float* child, const float* out, const float* grad_out, const float* logparams,
+                                 const int64_t* csc_offsets, const int32_t* csc_edges, const int32_t* csc_nodes,
+                                 float* grad_child, float* grad_logparams, int64_t num_children, int64_t batch,
+                                 void* stream) {
+    const char* name = "fl_sparse_csr_bwd";
+    FL_CHECK(num_children >= 0 && batch >= 0, "%s: negative size", name);
+    if (num_children == 0 || batch == 0) return ok();
+    FL_CHECK(child && out && grad_out && logparams && csc_offsets && csc_edges && csc_nodes && grad_child &&
+                 grad_logparams,
+             "%s: NULL pointer argument", name);
+    const bool vec = (batch % 4 == 0) && ((reinterpret_cast<uintptr_t>(child) | reinterpret_cast<uintptr_t>(out) |
+                                           reinterpret_cast<uintptr_t>(grad_out) |
+                                           reinterpret_cast<uintptr_t>(grad_child)) & 15) == 0;
+    const dim3 grid((unsigned)((num_children + 3) / 4));
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (vec)
+        sparse::csr_bwd_kernel<true><<<grid, dim3(256), 0, st>>>(child, out, grad_out, logparams, csc_offsets,
+                                                                  csc_edges, csc_nodes, grad_child, grad_logparams,
+                                                                  num_children, batch);
+    else
+        sparse::csr_bwd_kernel<false><<<grid, dim3(256), 0, st>>>(child, out, grad_out, logparams, csc_offsets,
+                                                                   csc_edges, csc_nodes, grad_child, grad_logparams,
+                                                                   num_children, batch);
+    return launch_status(name);
+}
 
 extern "C" int fl_sparse_csr_fwd(const float* child, const int64_t* offsets, const int32_t* child_ids,
                                  const float* logparams, float* out, int64_t num_nodes, int64_t batch, int q16,

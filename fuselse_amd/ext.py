@@ -356,3 +356,61 @@ def sparse_csr_forward(child, offsets, child_ids, logparams, q16=False, out=None
         _lib.call("fl_sparse_csr_fwd", child.data_ptr(), offsets.data_ptr(), child_ids.data_ptr(), logparams.data_ptr(),
                   out.data_ptr(), num_nodes, batch, int(q16), _stream(child))
     return out
+
+
+def sparse_csr_transpose(offsets, child_ids, num_children):
+    """The transposed (CSC) edge structure fl_sparse_csr_bwd walks: returns
+    (csc_offsets int64 [num_children + 1], csc_edges int32 [nnz] with the ids
+    of the edges pointing at each child in increasing order, csc_nodes int32
+    [nnz] with each of those edges' parent node).  Built once per layer with
+    torch's sort on the device; the structure does not depend on the batch."""
+    _check(offsets.is_cuda and offsets.dtype == torch.int64 and offsets.dim() == 1,
+           "offsets must be a CUDA int64 [num_nodes + 1] tensor")
+    _check(child_ids.is_cuda and child_ids.dtype == torch.int32, "child_ids must be a CUDA int32 tensor")
+    nnz = child_ids.numel()
+    _check(nnz < 2 ** 31 and num_children < 2 ** 31, "CSC ids are int32: nnz and num_children must be < 2^31")
+    num_nodes = offsets.numel() - 1
+    dev = child_ids.device
+    node_of_edge = torch.repeat_interleave(torch.arange(num_nodes, device=dev), offsets.diff(), output_size=nnz)
+    order = torch.sort(child_ids.long(), stable=True).indices
+    counts = torch.bincount(child_ids.long(), minlength=num_children)
+    _check(counts.numel() == num_children, "child_ids hold ids >= num_children")
+    csc_offsets = torch.zeros(num_children + 1, dtype=torch.int64, device=dev)
+    torch.cumsum(counts, 0, out=csc_offsets[1:])
+    return csc_offsets, order.to(torch.int32), node_of_edge[order].to(torch.int32)
+
+
+def sparse_csr_backward(child, out, grad_out, offsets, child_ids, logparams, csc=None):
+    """Backward (flows) of sparse_csr_forward in fp32: returns (grad_child,
+    grad_logparams) with
+      term[e, b] = grad_out[n_e, b] * exp(logparams[e] + child[c_e, b] - out[n_e, b])
+    summed over the edges of each child and over the batch of each edge, and
+    term = 0 where out is -inf.  csc: the result of sparse_csr_transpose for
+    this layer (built here when None)."""
+    for t, nm in ((child, "child"), (out, "out"), (grad_out, "grad_out"), (logparams, "logparams")):
+        _check(t.is_cuda and t.dtype == torch.float32 and t.is_contiguous(), f"{nm} must be contiguous CUDA float32")
+    _check(child.dim() == 2 and out.dim() == 2 and tuple(grad_out.shape) == tuple(out.shape),
+           "child [num_children, batch], out and grad_out [num_nodes, batch]")
+    _check(out.size(1) == child.size(1), "out and child batch dimensions must match")
+    _check(logparams.numel() == child_ids.numel(), "logparams must hold one value per edge")
+    num_children, batch = child.shape
+    _check(out.size(0) == offsets.numel() - 1, "out rows must match offsets")
+    if csc is None:
+        csc = sparse_csr_transpose(offsets, child_ids, num_children)
+    csc_off, csc_edge, csc_node = csc
+    _check(csc_off.dtype == torch.int64 and csc_off.numel() == num_children + 1 and csc_edge.dtype == torch.int32
+           and csc_node.dtype == torch.int32 and csc_edge.numel() == child_ids.numel(), "csc does not fit this layer")
+    grad_child = torch.empty_like(child)
+    grad_logp = torch.empty_like(logparams)
+    if num_children == 0 or batch == 0:
+        grad_child.zero_()
+        grad_logp.zero_()
+        return grad_child, grad_logp
+    if child_ids.numel() == 0:
+        grad_child.zero_()
+        return grad_child, grad_logp
+    with _on_device(child):
+        _lib.call("fl_sparse_csr_bwd", child.data_ptr(), out.data_ptr(), grad_out.data_ptr(), logparams.data_ptr(),
+                  csc_off.data_ptr(), csc_edge.data_ptr(), csc_node.data_ptr(), grad_child.data_ptr(),
+                  grad_logp.data_ptr(), num_children, batch, _stream(child))
+    return grad_child, grad_logp

@@ -161,6 +161,24 @@ int fl_sparse_blocked_fwd(float* node_mars, const float* element_mars, const flo
                           const int64_t* cids, const int64_t* pids, int64_t num_nblocks, int64_t num_edges,
                           int64_t block_size, int64_t batch, int q16, int params_are_log, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Sparse CSR backward ("flows"; the reference has no backward for its sparse
+ * kernels).  For out = fl_sparse_csr_fwd(child, offsets, child_ids,
+ * logparams) in fp32 and an upstream gradient grad_out [num_nodes, batch]:
+ *   term[e, b]          = grad_out[n_e, b] * exp(logparams[e] + child[c_e, b] - out[n_e, b])
+ *   grad_child[c, b]     = sum of term[e, b] over edges e with child_ids[e] = c
+ *   grad_logparams[e]    = sum of term[e, b] over b
+ * with term = 0 where out[n_e, b] is -inf.  The edges are given transposed
+ * (CSC): csc_offsets int64 [num_children + 1]; csc_edges int32 [nnz], the
+ * edge ids pointing at each child in increasing order; csc_nodes int32 [nnz],
+ * the parent node of each of those edges.  child, grad_child: fp32
+ * [num_children, batch]; out, grad_out: fp32 [num_nodes, batch]; both
+ * gradients are written (not accumulated).  Deterministic: no atomics.
+ * ------------------------------------------------------------------------- */
+int fl_sparse_csr_bwd(const float* child, const float* out, const float* grad_out, const float* logparams,
+                      const int64_t* csc_offsets, const int32_t* csc_edges, const int32_t* csc_nodes,
+                      float* grad_child, float* grad_logparams, int64_t num_children, int64_t batch, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -158,6 +158,28 @@ def selective_logsoftmax_bwd_fp64(g, x, index, lse):
     return out
 
 
+def sparse_csr_bwd_fp64(child, out, gout, offsets, child_ids, logp):
+    """Flows of the CSR sum layer in float64: term[e, b] = gout[n_e, b] *
+    exp(logp[e] + child[c_e, b] - out[n_e, b]) (0 where out is -inf);
+    returns (grad_child, grad_logp) = (per-child sum of terms, per-edge sum
+    over b).  The reference has no sparse backward; this is the derivative
+    of its forward (sparse_float_kernel.cu:40-105), pyjuice's element and
+    parameter flows."""
+    child = np.asarray(child, np.float64)
+    out = np.asarray(out, np.float64)
+    gout = np.asarray(gout, np.float64)
+    off = np.asarray(offsets, np.int64)
+    cid = np.asarray(child_ids, np.int64)
+    lw = np.asarray(logp, np.float64)
+    node = np.repeat(np.arange(len(off) - 1), np.diff(off))
+    with np.errstate(invalid="ignore", over="ignore"):
+        term = gout[node] * np.exp(lw[:, None] + child[cid] - out[node])
+    term[np.isneginf(out[node])] = 0.0
+    gchild = np.zeros_like(child)
+    np.add.at(gchild, cid, term)
+    return gchild, term.sum(axis=1)
+
+
 def sparse_blocked_fp64(element_mars, params, nids, cids, pids, block_size, clamp=1e-45):
     """pyjuice block-layout weighted gather-LSE in fp64
     (sparse_float_kernel.cu:40-105; torch form run_pyjuice.py:103-118):

@@ -231,3 +231,35 @@ def test_half_inputs_policy(dtype):
     ext2 = FakeExt()
     make_fuselse_logsumexp(ext2)(fake(x))
     assert ext2.calls == []
+
+
+# ---------------------------------------------------------------------------
+# pyjuice _forward_sparse dispatcher (experiment_pyjuice/run_pyjuice.py:63-77)
+# ---------------------------------------------------------------------------
+def test_sparse_dispatcher_local_ids_and_fallback():
+    from fuselse_amd.pc import make_sparse_dispatcher
+
+    calls, fb = [], []
+
+    def ext_call(node_mars, element_mars, params, nids, cids, pids, block_size):
+        calls.append((nids.tolist(), cids.tolist(), pids.tolist(), block_size))
+
+    def original(self, *a, **kw):
+        fb.append(kw["propagation_alg"])
+        return "fallback"
+
+    class Layer:
+        block_size = 4
+
+    fwd = make_sparse_dispatcher(ext_call, fallback=original)
+    nids = torch.tensor([0, 4, 8])
+    cids = torch.tensor([[1, 2], [3, 4], [5, 6]])
+    pids = torch.tensor([[10, 20], [30, 40], [50, 60]])
+    assert fwd(Layer(), None, None, None, nids, cids, pids, local_ids=torch.tensor([2, 0])) is None
+    assert calls[-1] == ([8, 0], [[5, 6], [1, 2]], [[50, 60], [10, 20]], 4)
+    fwd(Layer(), None, None, None, nids, cids, pids)
+    assert calls[-1][0] == [0, 4, 8]
+    assert fwd(Layer(), None, None, None, nids, cids, pids, propagation_alg="MPE") == "fallback"
+    assert fb == ["MPE"] and len(calls) == 2
+    with pytest.raises(NotImplementedError):
+        make_sparse_dispatcher(ext_call)(Layer(), None, None, None, nids, cids, pids, propagation_alg="GeneralLL")

@@ -143,3 +143,99 @@ def test_dispatcher_contract(cuda):
     assert (got[other] == 0).all()
     with pytest.raises(NotImplementedError):
         fwd(Layer(), nm, d_em, d_params, d_nids, d_cids, d_pids, propagation_alg="MPE")
+
+
+# ---------------------------------------------------------------------------
+# CSR backward (flows): grad_child and grad_logparams against the fp64
+# oracle.  Flows are sums of positive terms when grad_out > 0 (pyjuice's node
+# flows), so they are checked to 1e-5 relative; with signed grad_out the
+# bound is 1e-5 of the sum of |terms|.
+# ---------------------------------------------------------------------------
+def _abs_terms(child, out, gout, off, cids, lp):
+    return O.sparse_csr_bwd_fp64(child, out, np.abs(gout), off, cids, lp)
+
+
+@pytest.mark.parametrize("batch", [1, 7, 130, 512, 600])
+@pytest.mark.parametrize("signed", [False, True])
+def test_csr_backward_matches_fp64(cuda, batch, signed):
+    print(f"case csr_bwd batch={batch} signed={signed}", flush=True)
+    rng = np.random.default_rng(batch + 100 * signed)
+    nodes, nch = 300, 200
+    fan = O.powerlaw_fanin(nodes, seed=batch + 7)
+    fan[:4] = [0, 1, 256, 65]   # empty node, single edge, max fan-in, across a 64-edge window
+    off, cids, lp = _csr(rng, nodes, nch, fanin=fan)
+    cids[:300] = 5              # one child with many parents (several 64-edge windows)
+    child = np.log(rng.random((nch, batch)) + 1e-12).astype(np.float32)
+    child[7, :] = -np.inf       # a child of probability 0
+    ext = _ext()
+    ch, offd, cid, lpd = _to(cuda, child, off, cids, lp)
+    out = ext.sparse_csr_forward(ch, offd, cid, lpd)
+    g = rng.standard_normal((nodes, batch)).astype(np.float32)
+    if not signed:
+        g = np.abs(g) + 0.1
+    gd = torch.from_numpy(g).to(cuda)
+    gc, gl = ext.sparse_csr_backward(ch, out, gd, offd, cid, lpd)
+    out64 = O.sparse_csr_fp64(child, off, cids, lp)
+    wc, wl = O.sparse_csr_bwd_fp64(child, out64, g, off, cids, lp)
+    ac, al = _abs_terms(child, out64, g, off, cids, lp)
+    gc, gl = gc.cpu().numpy(), gl.cpu().numpy()
+    assert np.isfinite(gc).all() and np.isfinite(gl).all()
+    assert (np.abs(gc - wc) <= 1e-5 * ac + 1e-30).all(), np.max(np.abs(gc - wc) / (ac + 1e-30))
+    assert (np.abs(gl - wl) <= 1e-5 * al + 1e-30).all(), np.max(np.abs(gl - wl) / (al + 1e-30))
+    assert (gc[7] == 0).all()
+
+
+def test_csr_backward_deterministic_and_transpose(cuda):
+    print("case csr_bwd determinism", flush=True)
+    rng = np.random.default_rng(3)
+    off, cids, lp = _csr(rng, 2000, 500, seed=3)
+    child = np.log(rng.random((500, 256)) + 1e-12).astype(np.float32)
+    ext = _ext()
+    ch, offd, cid, lpd = _to(cuda, child, off, cids, lp)
+    csc = ext.sparse_csr_transpose(offd, cid, 500)
+    co, ce, cn = (t.cpu().numpy() for t in csc)
+    # the transpose: per child, its edge ids in increasing order and their parents
+    order = np.argsort(cids, kind="stable")
+    np.testing.assert_array_equal(ce, order)
+    np.testing.assert_array_equal(co, np.concatenate([[0], np.cumsum(np.bincount(cids, minlength=500))]))
+    np.testing.assert_array_equal(cn, np.repeat(np.arange(2000), np.diff(off))[order])
+    out = ext.sparse_csr_forward(ch, offd, cid, lpd)
+    g = torch.rand(2000, 256, device=cuda)
+    a = ext.sparse_csr_backward(ch, out, g, offd, cid, lpd, csc)
+    for _ in range(3):
+        b = ext.sparse_csr_backward(ch, out, g, offd, cid, lpd, csc)
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_csr_layer_autograd(cuda):
+    """pc.sparse_csr_layer: two stacked layers trained end to end; gradients
+    against torch fp64 autograd of gather + logsumexp."""
+    print("case csr_layer autograd", flush=True)
+    from fuselse_amd.pc import sparse_csr_layer
+
+    rng = np.random.default_rng(4)
+    batch = 64
+    off1, c1, l1 = _csr(rng, 50, 40, fanin=rng.integers(1, 9, 50))
+    off2, c2, l2 = _csr(rng, 10, 50, fanin=rng.integers(1, 9, 10))
+    x = np.log(rng.random((40, batch)) + 1e-6).astype(np.float32)
+    xd = torch.from_numpy(x).to(cuda).requires_grad_(True)
+    l1d = torch.from_numpy(l1).to(cuda).requires_grad_(True)
+    l2d = torch.from_numpy(l2).to(cuda).requires_grad_(True)
+    o1d, c1d, o2d, c2d = _to(cuda, off1, c1, off2, c2)
+    h = sparse_csr_layer(xd, o1d, c1d, l1d)
+    y = sparse_csr_layer(h, o2d, c2d, l2d)
+    y.sum().backward()
+
+    def layer_t(ch, off, cid, lw):
+        rows = [torch.logsumexp(lw[off[n]:off[n + 1], None] + ch[torch.from_numpy(cid[off[n]:off[n + 1]]).long()], 0)
+                for n in range(len(off) - 1)]
+        return torch.stack(rows)
+
+    xt = torch.from_numpy(x).double().requires_grad_(True)
+    l1t = torch.from_numpy(l1).double().requires_grad_(True)
+    l2t = torch.from_numpy(l2).double().requires_grad_(True)
+    yt = layer_t(layer_t(xt, off1, c1, l1t), off2, c2, l2t)
+    yt.sum().backward()
+    np.testing.assert_allclose(y.detach().cpu().numpy(), yt.detach().numpy(), rtol=1e-5, atol=1e-5)
+    for got, want in ((xd.grad, xt.grad), (l1d.grad, l1t.grad), (l2d.grad, l2t.grad)):
+        np.testing.assert_allclose(got.cpu().numpy(), want.numpy(), rtol=1e-4, atol=1e-5)

@@ -483,3 +483,72 @@ def test_trl_algorithm_fallback_matches_oracle(dtype):
     want, _ = O.selective_logsoftmax_fp64(xt.double().numpy().reshape(10, 300), idx.reshape(10))
     tol = 2e-2 if dtype == "bfloat16" else 1e-5
     np.testing.assert_allclose(got.reshape(10), want, rtol=tol, atol=tol)
+
+
+# ---------------------------------------------------------------------------
+# sparse CSR backward (flows)
+# ---------------------------------------------------------------------------
+def _tiny_csr(rng, nodes, children, batch, max_fan=6, empty_node=True):
+    fan = rng.integers(1, max_fan + 1, nodes)
+    if empty_node:
+        fan[1] = 0
+    off = np.concatenate([[0], np.cumsum(fan)]).astype(np.int64)
+    cid = rng.integers(0, children, int(off[-1]))
+    lw = rng.standard_normal(int(off[-1]))
+    child = rng.standard_normal((children, batch)) * 2
+    return off, cid, lw, child
+
+
+def test_sparse_csr_bwd_fp64_against_torch_autograd_and_closed_forms():
+    import torch
+
+    rng = np.random.default_rng(31)
+    off, cid, lw, child = _tiny_csr(rng, 9, 7, 5)
+    child[3, 2] = -np.inf                      # a -inf child value contributes 0
+    out = O.sparse_csr_fp64(child, off, cid, lw)
+    gout = rng.standard_normal(out.shape)
+    gc, gl = O.sparse_csr_bwd_fp64(child, out, gout, off, cid, lw)
+    # torch fp64 autograd of the same layer written with gather + logsumexp
+    ct = torch.from_numpy(np.where(np.isneginf(child), -1e300, child)).requires_grad_(True)
+    lt = torch.from_numpy(lw).requires_grad_(True)
+    rows = []
+    for n in range(9):
+        a, b = off[n], off[n + 1]
+        if a == b:
+            rows.append(torch.full((5,), -1e300, dtype=torch.float64))
+            continue
+        rows.append(torch.logsumexp(lt[a:b, None] + ct[torch.from_numpy(cid[a:b])], dim=0))
+    yt = torch.stack(rows)
+    (yt * torch.from_numpy(np.where(np.isneginf(out), 0.0, gout))).sum().backward()
+    np.testing.assert_allclose(gc, ct.grad.numpy(), rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(gl, lt.grad.numpy(), rtol=1e-12, atol=1e-14)
+    # the softmax weights of a node's edges sum to one per column, so the
+    # log-weight gradients of a node sum to the node's gradient over the batch
+    for n in range(9):
+        a, b = off[n], off[n + 1]
+        if a < b:
+            assert math.isclose(gl[a:b].sum(), gout[n].sum(), rel_tol=1e-12, abs_tol=1e-12)
+
+
+def test_sparse_csr_bwd_fp64_finite_differences():
+    rng = np.random.default_rng(32)
+    off, cid, lw, child = _tiny_csr(rng, 4, 5, 3, empty_node=False)
+    gout = rng.standard_normal((4, 3))
+
+    def f(ch, l):
+        return (gout * O.sparse_csr_fp64(ch, off, cid, l)).sum()
+
+    out = O.sparse_csr_fp64(child, off, cid, lw)
+    gc, gl = O.sparse_csr_bwd_fp64(child, out, gout, off, cid, lw)
+    h = 1e-6
+    for c in range(5):
+        for b in range(3):
+            p, m = child.copy(), child.copy()
+            p[c, b] += h
+            m[c, b] -= h
+            assert math.isclose(gc[c, b], (f(p, lw) - f(m, lw)) / (2 * h), rel_tol=1e-6, abs_tol=1e-8)
+    for e in range(len(lw)):
+        p, m = lw.copy(), lw.copy()
+        p[e] += h
+        m[e] -= h
+        assert math.isclose(gl[e], (f(child, p) - f(child, m)) / (2 * h), rel_tol=1e-6, abs_tol=1e-8)
