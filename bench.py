@@ -159,7 +159,7 @@ def _time_graph(torch, fn, iters, result):
     return a.elapsed_time(b) / (3 * iters), result()
 
 
-def measure_configs(torch, ext, dev, stream, iters=50):
+def measure_configs(torch, ext, dev, stream, iters=50, only=None):
     """The other BASELINE configs: fp16/bf16 forward (C3), IntLSE Q16.16 fp32 /
     int32 and Q10.6 int16 (C4), sparse PC at 1M nodes (C5).  Each input set
     rotates over enough buffers to exceed twice the 256 MB Infinity Cache."""
@@ -176,135 +176,143 @@ def measure_configs(torch, ext, dev, stream, iters=50):
     def nbuf_for(nbytes):
         return max(2, int(np.ceil(2 * 256e6 / nbytes)) + 1)
 
+    def want(section):
+        return only is None or section in only
+
     gen = torch.Generator(device=dev)
     gen.manual_seed(7)
-    # C3: half-precision inputs, x ~ N(0, 2^2)
-    for (b, n) in [(4096, 32000), (2048, 128256), (65536, 256)]:
-        for dt, fn, tag in [(torch.float16, ext.batched_logsumexp_fp16, "fp16"),
-                            (torch.bfloat16, ext.batched_logsumexp_bf16, "bf16")]:
-            nb = nbuf_for(2 * b * n)
-            bufs = [(torch.randn(b, n, device=dev, generator=gen) * 2).to(dt) for _ in range(nb)]
-            ms = _time_calls(torch, stream, lambda i: fn(bufs[i % nb]), nb, iters)
-            rec(f"C3_{tag}_fwd_{b}x{n}", ms, 2 * b * n + 4 * b)
-            if n > 256:
-                # the fused half backward (fp32 grad and lse, half x and grad_x)
-                gsv = torch.randn(b, device=dev, generator=gen)
-                lses = [fn(x) for x in bufs]
-                ms = _time_calls(torch, stream,
-                                 lambda i: ext.onepass_lse_half_backward(gsv, bufs[i % nb], lses[i % nb]), nb, iters)
-                rec(f"C3_{tag}_bwd_{b}x{n}", ms, 4 * b * n + 8 * b)
+    if want("C3"):
+        # C3: half-precision inputs, x ~ N(0, 2^2)
+        for (b, n) in [(4096, 32000), (2048, 128256), (65536, 256)]:
+            for dt, fn, tag in [(torch.float16, ext.batched_logsumexp_fp16, "fp16"),
+                                (torch.bfloat16, ext.batched_logsumexp_bf16, "bf16")]:
+                nb = nbuf_for(2 * b * n)
+                bufs = [(torch.randn(b, n, device=dev, generator=gen) * 2).to(dt) for _ in range(nb)]
+                ms = _time_calls(torch, stream, lambda i: fn(bufs[i % nb]), nb, iters)
+                rec(f"C3_{tag}_fwd_{b}x{n}", ms, 2 * b * n + 4 * b)
+                if n > 256:
+                    # the fused half backward (fp32 grad and lse, half x and grad_x)
+                    gsv = torch.randn(b, device=dev, generator=gen)
+                    lses = [fn(x) for x in bufs]
+                    ms = _time_calls(torch, stream,
+                                     lambda i: ext.onepass_lse_half_backward(gsv, bufs[i % nb], lses[i % nb]), nb, iters)
+                    rec(f"C3_{tag}_bwd_{b}x{n}", ms, 4 * b * n + 8 * b)
+                del bufs
+    if want("split"):
+        # Few long rows (fp32, robust): the split-row path (fl_lse_fwd_f32_ws, the
+        # Python shim's choice for B < 320) beside the one-block-per-row kernel of
+        # fl_lse_fwd_f32, the reference's geometry.  These calls take a few us of
+        # GPU time, less than their host-side launch cost, so each is timed by
+        # replaying a HIP graph of captured calls.
+        from fuselse_amd import _lib
+
+        lib = _lib.load()
+        n = 128256
+        for b in (1, 8, 64, 256):
+            nb = nbuf_for(4 * b * n)
+            bufs = [torch.randn(b, n, device=dev, generator=gen) * 3 for _ in range(nb)]
+            out = torch.empty(b, device=dev)
+            wsb = lib.fl_lse_fwd_workspace_bytes(b, n, 4)
+            ws = torch.empty(max(wsb, 8), dtype=torch.uint8, device=dev)
+
+            def split(i, st):
+                _lib.call("fl_lse_fwd_f32_ws", bufs[i % nb].data_ptr(), out.data_ptr(), b, n, 1, ws.data_ptr(),
+                          ws.numel(), st)
+
+            def one(i, st):
+                _lib.call("fl_lse_fwd_f32", bufs[i % nb].data_ptr(), out.data_ptr(), b, n, 1, st)
+
+            # every buffer once per replay: the replayed working set exceeds the
+            # Infinity Cache twice over
+            calls = max(iters, nb)
+            ms, ok = _time_graph(torch, split, calls, lambda: out.clone())
+            ms1, ok1 = _time_graph(torch, one, calls, lambda: out.clone())
+            want = torch.logsumexp(bufs[(calls - 1) % nb], dim=-1)
+            assert torch.allclose(ok, want, rtol=1e-5) and torch.allclose(ok1, want, rtol=1e-5), "graph replay mismatch"
+            rec(f"split_fp32_fwd_{b}x{n}", ms, 4 * b * n + 4 * b, one_pass_us=round(ms1 * 1e3, 2), workspace_bytes=wsb)
             del bufs
-    # Few long rows (fp32, robust): the split-row path (fl_lse_fwd_f32_ws, the
-    # Python shim's choice for B < 320) beside the one-block-per-row kernel of
-    # fl_lse_fwd_f32, the reference's geometry.  These calls take a few us of
-    # GPU time, less than their host-side launch cost, so each is timed by
-    # replaying a HIP graph of captured calls.
-    from fuselse_amd import _lib
+    if want("sls"):
+        # Selective log-softmax at the reference RLHF experiment's shapes
+        # (experiment_rlhf_logsumexp/run_rlhf.py:64-76: T = 1024, logits
+        # (B, T-1, V) fp32), synthetic N(0, 2^2) logits and uniform targets: the
+        # fused kernel, trl's algorithm in torch ops on the same GPU, and trl's
+        # algorithm with torch.logsumexp replaced by this library's drop-in (the
+        # reference's "fused" measurement).
+        import fuselse_amd
+        from fuselse_amd.selective import _trl_algorithm
 
-    lib = _lib.load()
-    n = 128256
-    for b in (1, 8, 64, 256):
-        nb = nbuf_for(4 * b * n)
-        bufs = [torch.randn(b, n, device=dev, generator=gen) * 3 for _ in range(nb)]
-        out = torch.empty(b, device=dev)
-        wsb = lib.fl_lse_fwd_workspace_bytes(b, n, 4)
-        ws = torch.empty(max(wsb, 8), dtype=torch.uint8, device=dev)
-
-        def split(i, st):
-            _lib.call("fl_lse_fwd_f32_ws", bufs[i % nb].data_ptr(), out.data_ptr(), b, n, 1, ws.data_ptr(),
-                      ws.numel(), st)
-
-        def one(i, st):
-            _lib.call("fl_lse_fwd_f32", bufs[i % nb].data_ptr(), out.data_ptr(), b, n, 1, st)
-
-        # every buffer once per replay: the replayed working set exceeds the
-        # Infinity Cache twice over
-        calls = max(iters, nb)
-        ms, ok = _time_graph(torch, split, calls, lambda: out.clone())
-        ms1, ok1 = _time_graph(torch, one, calls, lambda: out.clone())
-        want = torch.logsumexp(bufs[(calls - 1) % nb], dim=-1)
-        assert torch.allclose(ok, want, rtol=1e-5) and torch.allclose(ok1, want, rtol=1e-5), "graph replay mismatch"
-        rec(f"split_fp32_fwd_{b}x{n}", ms, 4 * b * n + 4 * b, one_pass_us=round(ms1 * 1e3, 2), workspace_bytes=wsb)
-        del bufs
-    # Selective log-softmax at the reference RLHF experiment's shapes
-    # (experiment_rlhf_logsumexp/run_rlhf.py:64-76: T = 1024, logits
-    # (B, T-1, V) fp32), synthetic N(0, 2^2) logits and uniform targets: the
-    # fused kernel, trl's algorithm in torch ops on the same GPU, and trl's
-    # algorithm with torch.logsumexp replaced by this library's drop-in (the
-    # reference's "fused" measurement).
-    import fuselse_amd
-    from fuselse_amd.selective import _trl_algorithm
-
-    for name, v, bt in [("llama2", 32000, 8), ("gpt2", 50257, 8), ("llama3", 128256, 4), ("gemma", 256128, 2)]:
-        rows = bt * 1023
-        bufs = [torch.randn(bt, 1023, v, device=dev, generator=gen) * 2 for _ in range(2)]
-        idx = torch.randint(0, v, (bt, 1023), device=dev, generator=gen)
-        ms = _time_calls(torch, stream, lambda i: fuselse_amd.selective_log_softmax(bufs[i % 2], idx), 2, 20)
-        ms_trl = _time_calls(torch, stream, lambda i: _trl_algorithm(bufs[i % 2], idx), 2, 10)
-        saved = torch.logsumexp
-        torch.logsumexp = fuselse_amd.logsumexp
-        try:
-            ms_trl_fl = _time_calls(torch, stream, lambda i: _trl_algorithm(bufs[i % 2], idx), 2, 10)
-        finally:
-            torch.logsumexp = saved
-        got = fuselse_amd.selective_log_softmax(bufs[0], idx)
-        ref = _trl_algorithm(bufs[0], idx)
-        assert torch.allclose(got, ref, rtol=1e-4, atol=1e-4), "selective log-softmax mismatch"
-        rec(f"sls_fwd_{name}_{bt}x1023x{v}", ms, 4 * rows * v + 16 * rows, trl_torch_us=round(ms_trl * 1e3, 1),
-            trl_with_fuselse_lse_us=round(ms_trl_fl * 1e3, 1))
-        del bufs
-    # C4: IntLSE fixed point
-    b, n = 512, 128256
-    nb = 3
-    xs = [torch.randn(b, n, device=dev, generator=gen) * 2 for _ in range(nb)]
-    ms = _time_calls(torch, stream, lambda i: ext.batched_logsumexp(xs[i % nb]), nb, iters)
-    rec("C4_q16_f32in_512x128256", ms, 4 * b * n + 4 * b)
-    ms = _time_calls(torch, stream, lambda i: ext.batched_logsumexp_nolut(xs[i % nb]), nb, iters)
-    rec("C4_q16_f32in_nolut_512x128256", ms, 4 * b * n + 4 * b)
-    qs = [torch.clamp(torch.round(x * 94548.4609375), -2 ** 31, 2 ** 31 - 1).to(torch.int32) for x in xs]
-    del xs
-    ms = _time_calls(torch, stream, lambda i: ext.batched_logsumexp_q16_i32(qs[i % nb]), nb, iters)
-    rec("C4_q16_i32in_512x128256", ms, 4 * b * n + 4 * b)
-    del qs
-    b, n = 1024, 32000
-    nb = nbuf_for(2 * b * n)
-    q6 = [torch.clamp(torch.round(torch.randn(b, n, device=dev, generator=gen) * 2 * 92.33248),
-                      -32768, 32767).to(torch.int16) for _ in range(nb)]
-    ms = _time_calls(torch, stream, lambda i: ext.batched_logsumexp_q10_6(q6[i % nb]), nb, iters)
-    rec("C4_q10_6_i16in_1024x32000", ms, 2 * b * n + 4 * b)
-    del q6
-    # C5: sparse PC, 1M sum nodes, power-law fan-in (alpha = 2) on [2, 256], batch 512
-    sys.path.insert(0, ROOT)
-    nodes, batch = 1_000_000, 512
-    rng = np.random.default_rng(11)
-    ks = np.arange(2, 257)
-    pk = ks.astype(np.float64) ** -2.0
-    fan = rng.choice(ks, size=nodes, p=pk / pk.sum())
-    off = np.concatenate([[0], np.cumsum(fan)]).astype(np.int64)
-    nnz = int(off[-1])
-    lp = rng.standard_normal(nnz)
-    seg = np.maximum.reduceat(lp, off[:-1])
-    lp = lp - np.repeat(seg + np.log(np.add.reduceat(np.exp(lp - np.repeat(seg, fan)), off[:-1])), fan)
-    child = torch.log(torch.rand(nodes, batch, device=dev, generator=gen).clamp_min_(1e-30))
-    d_off = torch.from_numpy(off).to(dev)
-    d_cid = torch.randint(0, nodes, (nnz,), device=dev, generator=gen, dtype=torch.int32)
-    d_lp = torch.from_numpy(lp.astype(np.float32)).to(dev)
-    out = torch.empty(nodes, batch, device=dev)
-    sbytes = nnz * batch * 4 + nnz * 8 + (nodes + 1) * 8 + nodes * batch * 4
-    for q16, tag in [(False, "fp32"), (True, "q16")]:
-        ms = _time_calls(torch, stream, lambda i: ext.sparse_csr_forward(child, d_off, d_cid, d_lp, q16=q16, out=out),
+        for name, v, bt in [("llama2", 32000, 8), ("gpt2", 50257, 8), ("llama3", 128256, 4), ("gemma", 256128, 2)]:
+            rows = bt * 1023
+            bufs = [torch.randn(bt, 1023, v, device=dev, generator=gen) * 2 for _ in range(2)]
+            idx = torch.randint(0, v, (bt, 1023), device=dev, generator=gen)
+            ms = _time_calls(torch, stream, lambda i: fuselse_amd.selective_log_softmax(bufs[i % 2], idx), 2, 20)
+            ms_trl = _time_calls(torch, stream, lambda i: _trl_algorithm(bufs[i % 2], idx), 2, 10)
+            saved = torch.logsumexp
+            torch.logsumexp = fuselse_amd.logsumexp
+            try:
+                ms_trl_fl = _time_calls(torch, stream, lambda i: _trl_algorithm(bufs[i % 2], idx), 2, 10)
+            finally:
+                torch.logsumexp = saved
+            got = fuselse_amd.selective_log_softmax(bufs[0], idx)
+            ref = _trl_algorithm(bufs[0], idx)
+            assert torch.allclose(got, ref, rtol=1e-4, atol=1e-4), "selective log-softmax mismatch"
+            rec(f"sls_fwd_{name}_{bt}x1023x{v}", ms, 4 * rows * v + 16 * rows, trl_torch_us=round(ms_trl * 1e3, 1),
+                trl_with_fuselse_lse_us=round(ms_trl_fl * 1e3, 1))
+            del bufs
+    if want("C4"):
+        # C4: IntLSE fixed point
+        b, n = 512, 128256
+        nb = 3
+        xs = [torch.randn(b, n, device=dev, generator=gen) * 2 for _ in range(nb)]
+        ms = _time_calls(torch, stream, lambda i: ext.batched_logsumexp(xs[i % nb]), nb, iters)
+        rec("C4_q16_f32in_512x128256", ms, 4 * b * n + 4 * b)
+        ms = _time_calls(torch, stream, lambda i: ext.batched_logsumexp_nolut(xs[i % nb]), nb, iters)
+        rec("C4_q16_f32in_nolut_512x128256", ms, 4 * b * n + 4 * b)
+        qs = [torch.clamp(torch.round(x * 94548.4609375), -2 ** 31, 2 ** 31 - 1).to(torch.int32) for x in xs]
+        del xs
+        ms = _time_calls(torch, stream, lambda i: ext.batched_logsumexp_q16_i32(qs[i % nb]), nb, iters)
+        rec("C4_q16_i32in_512x128256", ms, 4 * b * n + 4 * b)
+        del qs
+        b, n = 1024, 32000
+        nb = nbuf_for(2 * b * n)
+        q6 = [torch.clamp(torch.round(torch.randn(b, n, device=dev, generator=gen) * 2 * 92.33248),
+                          -32768, 32767).to(torch.int16) for _ in range(nb)]
+        ms = _time_calls(torch, stream, lambda i: ext.batched_logsumexp_q10_6(q6[i % nb]), nb, iters)
+        rec("C4_q10_6_i16in_1024x32000", ms, 2 * b * n + 4 * b)
+        del q6
+    if want("C5"):
+        # C5: sparse PC, 1M sum nodes, power-law fan-in (alpha = 2) on [2, 256], batch 512
+        sys.path.insert(0, ROOT)
+        nodes, batch = 1_000_000, 512
+        rng = np.random.default_rng(11)
+        ks = np.arange(2, 257)
+        pk = ks.astype(np.float64) ** -2.0
+        fan = rng.choice(ks, size=nodes, p=pk / pk.sum())
+        off = np.concatenate([[0], np.cumsum(fan)]).astype(np.int64)
+        nnz = int(off[-1])
+        lp = rng.standard_normal(nnz)
+        seg = np.maximum.reduceat(lp, off[:-1])
+        lp = lp - np.repeat(seg + np.log(np.add.reduceat(np.exp(lp - np.repeat(seg, fan)), off[:-1])), fan)
+        child = torch.log(torch.rand(nodes, batch, device=dev, generator=gen).clamp_min_(1e-30))
+        d_off = torch.from_numpy(off).to(dev)
+        d_cid = torch.randint(0, nodes, (nnz,), device=dev, generator=gen, dtype=torch.int32)
+        d_lp = torch.from_numpy(lp.astype(np.float32)).to(dev)
+        out = torch.empty(nodes, batch, device=dev)
+        sbytes = nnz * batch * 4 + nnz * 8 + (nodes + 1) * 8 + nodes * batch * 4
+        for q16, tag in [(False, "fp32"), (True, "q16")]:
+            ms = _time_calls(torch, stream, lambda i: ext.sparse_csr_forward(child, d_off, d_cid, d_lp, q16=q16, out=out),
+                             1, max(5, iters // 5))
+            rec(f"C5_sparse_csr_{tag}_1M_nodes_b512", ms, sbytes, nnz=nnz, alpha=2.0)
+        # the fp32 backward (flows) of the same layer: per edge it reads the
+        # parent's grad_out and out rows, per child it reads and writes one row
+        out = ext.sparse_csr_forward(child, d_off, d_cid, d_lp)
+        gout = torch.rand(nodes, batch, device=dev, generator=gen)
+        csc = ext.sparse_csr_transpose(d_off, d_cid, nodes)
+        ms = _time_calls(torch, stream, lambda i: ext.sparse_csr_backward(child, out, gout, d_off, d_cid, d_lp, csc),
                          1, max(5, iters // 5))
-        rec(f"C5_sparse_csr_{tag}_1M_nodes_b512", ms, sbytes, nnz=nnz, alpha=2.0)
-    # the fp32 backward (flows) of the same layer: per edge it reads the
-    # parent's grad_out and out rows, per child it reads and writes one row
-    out = ext.sparse_csr_forward(child, d_off, d_cid, d_lp)
-    gout = torch.rand(nodes, batch, device=dev, generator=gen)
-    csc = ext.sparse_csr_transpose(d_off, d_cid, nodes)
-    ms = _time_calls(torch, stream, lambda i: ext.sparse_csr_backward(child, out, gout, d_off, d_cid, d_lp, csc),
-                     1, max(5, iters // 5))
-    bbytes = 2 * nnz * batch * 4 + nnz * (4 + 4 + 4 + 4) + (nodes + 1) * 8 + 2 * nodes * batch * 4
-    rec("C5_sparse_csr_bwd_fp32_1M_nodes_b512", ms, bbytes, nnz=nnz, alpha=2.0)
-    del child, out, gout
+        bbytes = 2 * nnz * batch * 4 + nnz * (4 + 4 + 4 + 4) + (nodes + 1) * 8 + 2 * nodes * batch * 4
+        rec("C5_sparse_csr_bwd_fp32_1M_nodes_b512", ms, bbytes, nnz=nnz, alpha=2.0)
+        del child, out, gout
     return res
 
 
@@ -315,18 +323,33 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-configs", action="store_true", help="skip the other BASELINE configs")
+    ap.add_argument("--only", default=None,
+                    help="comma-separated config groups (C3, split, sls, C4, C5) to run alone, without the C2 "
+                         "step; for profiling passes over one group")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also launch one plain 1 GiB device copy (counter calibration runs)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         log("bench.py: this build measures one GPU only (each GPU box has one MI355X); "
-            "run with --gpus 1. Sharding over GPUs is described in DESIGN.md.")
+            "run with --gpus 1. Sharding over GPUs is design-only in this build.")
         sys.exit(2)
 
     import torch
 
     sys.path.insert(0, ROOT)
+    if args.only:
+        import fuselse_amd
+
+        groups = set(args.only.split(","))
+        unknown = groups - {"C3", "split", "sls", "C4", "C5"}
+        if unknown:
+            log(f"bench.py: unknown config groups {sorted(unknown)}")
+            sys.exit(2)
+        dev = torch.device("cuda:0")
+        res = measure_configs(torch, fuselse_amd.ext, dev, torch.cuda.current_stream(dev), only=groups)
+        print(json.dumps({"metric": METRIC, "only": sorted(groups), "other_configs": res}), flush=True)
+        return
     import fuselse_amd
     from fuselse_amd import _lib
 
@@ -416,6 +439,20 @@ def main():
 
     same_batch_ms = per_launch(same_batch)
 
+    # Reference streams over the same 263 MB buffers, for the roofline's
+    # context: torch's own elementwise read+write (mul with out=) and its
+    # write-only fill, on the same stream and rotation.
+    flat = [x.view(-1) for x in xs]
+    outs = [r.view(-1) for r in ring[:NBUF]]
+    mul_ms = per_launch(lambda i: torch.mul(flat[i % NBUF], 2.0, out=outs[(i + 1) % NBUF]))
+    fill_ms = per_launch(lambda i: outs[i % NBUF].fill_(1.0))
+    stream_ceilings = {
+        "torch_mul_read_write_gbps": round(2 * 4 * B * N / (mul_ms * 1e-3) / 1e9, 1),
+        "torch_fill_write_gbps": round(4 * B * N / (fill_ms * 1e-3) / 1e9, 1),
+    }
+    log(f"reference streams: torch mul r+w {stream_ceilings['torch_mul_read_write_gbps']} GB/s, "
+        f"fill {stream_ceilings['torch_fill_write_gbps']} GB/s")
+
     gbps = (FWD_BYTES + BWD_BYTES) / (ms_step * 1e-3) / 1e9
     fwd_gbps = FWD_BYTES / (fwd_ms * 1e-3) / 1e9
     bwd_gbps = BWD_BYTES / (bwd_ms * 1e-3) / 1e9
@@ -453,6 +490,7 @@ def main():
         "hbm_gbps": round(gbps, 1),
         "pct_hbm_peak": round(100 * gbps * 1e9 / HBM_PEAK, 2),
         "same_batch_step_us": round(same_batch_ms * 1e3, 2),
+        "stream_ceilings": stream_ceilings,
         "fwd": {"us": round(fwd_ms * 1e3, 2), "gbps": round(fwd_gbps, 1),
                 "pct_peak": round(100 * fwd_gbps * 1e9 / HBM_PEAK, 2), "bytes": FWD_BYTES,
                 "plain_us": round(fwd_plain_ms * 1e3, 2)},

@@ -111,7 +111,10 @@ __device__ __forceinline__ int q16_quant(float v) {
 struct SrcF32 {
     using T = float;
     using Raw = f32x4;
-    __device__ static __forceinline__ int one(const float* p) { return q16_quant(*p); }
+    __device__ static __forceinline__ int cvt(float v) { return q16_quant(v); }
+    __device__ static __forceinline__ float sload(__amdgpu_buffer_rsrc_t r, int voff) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0));
+    }
     __device__ static __forceinline__ Raw bload(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
         return __builtin_bit_cast(Raw, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kBufNT));
     }
@@ -122,7 +125,10 @@ struct SrcF32 {
 struct SrcI32 {
     using T = int32_t;
     using Raw = u32x4;
-    __device__ static __forceinline__ int one(const int32_t* p) { return *p; }
+    __device__ static __forceinline__ int cvt(int32_t v) { return v; }
+    __device__ static __forceinline__ int32_t sload(__amdgpu_buffer_rsrc_t r, int voff) {
+        return (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0);
+    }
     __device__ static __forceinline__ Raw bload(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
         return __builtin_bit_cast(Raw, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kBufNT));
     }
@@ -134,7 +140,10 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 struct SrcI16 {
     using T = int16_t;
     using Raw = u32x2;
-    __device__ static __forceinline__ int one(const int16_t* p) { return (int)*p; }
+    __device__ static __forceinline__ int cvt(int16_t v) { return (int)v; }
+    __device__ static __forceinline__ int16_t sload(__amdgpu_buffer_rsrc_t r, int voff) {
+        return (int16_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, 0, 0);
+    }
     __device__ static __forceinline__ Raw bload(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
         return __builtin_bit_cast(Raw, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, kBufNT));
     }
@@ -147,9 +156,15 @@ struct SrcI16 {
 // The reference tree over one row per block (grid-stride over rows).
 // ALIGN is the vector alignment the reference uses for the chunks (16 bytes
 // for 4-byte elements, 8 for int16); PAIR folds two accumulators.
-template <typename SRC, int ALIGN, int D, typename PAIR>
+// SETUP builds the kernel's LDS table on a block's first row in two steps:
+// issue() reads the table's source before any row load, finish() stores it
+// and syncs once the row's first loads are in flight.  The vector-memory
+// counter retires in order, so a table read issued after the row loads would
+// make its wait cover all of them.
+template <typename SRC, int ALIGN, int D, typename PAIR, typename SETUP>
 __device__ __forceinline__ int tree_row(const typename SRC::T* row, int64_t n, const int* __restrict__ tab, PAIR pair,
-                                        int* __restrict__ sh_warp) {
+                                        int* __restrict__ sh_warp, SETUP& setup) {
+    setup.issue();
     using T = typename SRC::T;
     const int t = threadIdx.x;
     const uint32_t mis = (uint32_t)(reinterpret_cast<uintptr_t>(row) & (ALIGN - 1));
@@ -159,12 +174,6 @@ __device__ __forceinline__ int tree_row(const typename SRC::T* row, int64_t n, c
     const int64_t tail = n - prefix - 4 * n4;
     const T* body = row + prefix;
 
-    int acc = kQNegInf;
-    bool has = false;
-    if (t < prefix) {
-        acc = SRC::one(row + t);
-        has = true;
-    }
     // Vector chunks of virtual thread t are c = t + 256*k.  Every thread owns
     // k = 0 .. kmain-1 with kmain = n4 / 256 (a block-uniform count), and
     // threads t < n4 % 256 own one more, k = kmain.  The uniform part runs
@@ -177,58 +186,79 @@ __device__ __forceinline__ int tree_row(const typename SRC::T* row, int64_t n, c
         const_cast<T*>(body), 0, (int)(n4 * CB), 0x00020000);
     const int vofs = (int)(t * CB);
     auto chunk = [&](int64_t k) { return SRC::bload(rsrc, vofs, (int)(k * 256 * CB)); };
+
+    // The loads the chain consumes outside the uniform loop (prefix element,
+    // the extra chunk, suffix element) are issued before it, so no lane waits
+    // a separate round trip for them at either end.  The extra chunk's load is
+    // unconditional: past the body the range check returns zero, unused.
+    // The scalar elements come through a buffer over the whole row: a lane
+    // without one addresses past the row's end, where the range check returns
+    // zero, so no lane branches around a load or selects its value (either
+    // would wait for the load).  They stay raw until used, for the same reason.
+    const __amdgpu_buffer_rsrc_t rrow = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<T*>(row), 0, (int)(n * (int64_t)sizeof(T)), 0x00020000);
+    const bool has_pre = t < prefix;
+    const T pre = SRC::sload(rrow, (int)((has_pre ? t : n) * (int64_t)sizeof(T)));
+    const bool has_extra = t < n4 - kmain * 256;
+    const typename SRC::Raw extra = chunk(kmain);
+    const bool has_suf = t < tail;
+    const T suf = SRC::sload(rrow, (int)((has_suf ? prefix + 4 * n4 + t : n) * (int64_t)sizeof(T)));
+
+    int acc = kQNegInf;
+    bool has = has_pre;
+    auto fold_first = [&](const typename SRC::Raw& raw) {
+        int qq[4];
+        SRC::unpack(raw, qq);
+        acc = has ? pair(acc, qq[0], tab) : qq[0];
+        has = true;
+        acc = pair(acc, qq[1], tab);
+        acc = pair(acc, qq[2], tab);
+        acc = pair(acc, qq[3], tab);
+    };
     auto fold = [&](const typename SRC::Raw& raw) {
         int qq[4];
         SRC::unpack(raw, qq);
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc = pair(acc, qq[i], tab);
     };
+    // Two register buffers of D chunks alternate: while one is folded the
+    // other's loads are in flight.  Chunk 0 comes from the first buffer.
+    // (loaded even when kmain == 0: the range check keeps the loads in the
+    // body, and an unconditional load leaves no merge of register values that
+    // would wait for it)
+    typename SRC::Raw bufa[D], bufb[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) bufa[d] = chunk(d);
+    setup.finish();
+    if (has_pre) acc = SRC::cvt(pre);
     if (kmain > 0) {
-        {
-            int qq[4];
-            SRC::unpack(chunk(0), qq);
-            acc = has ? pair(acc, qq[0], tab) : qq[0];
-            has = true;
-            acc = pair(acc, qq[1], tab);
-            acc = pair(acc, qq[2], tab);
-            acc = pair(acc, qq[3], tab);
-        }
-        // Two register buffers of D chunks alternate: while one is folded
-        // the other's loads are in flight.
-        typename SRC::Raw bufa[D], bufb[D];
-        int64_t k = 1;
-        if (k < kmain) {
+        int64_t k = 0;
+        for (;;) {
 #pragma unroll
-            for (int d = 0; d < D; ++d) bufa[d] = chunk(k + d);
-            for (;;) {
+            for (int d = 0; d < D; ++d) bufb[d] = chunk(k + D + d);
 #pragma unroll
-                for (int d = 0; d < D; ++d) bufb[d] = chunk(k + D + d);
-#pragma unroll
-                for (int d = 0; d < D; ++d)
-                    if (k + d < kmain) fold(bufa[d]);
-                k += D;
-                if (k >= kmain) break;
-#pragma unroll
-                for (int d = 0; d < D; ++d) bufa[d] = chunk(k + D + d);
-#pragma unroll
-                for (int d = 0; d < D; ++d)
-                    if (k + d < kmain) fold(bufb[d]);
-                k += D;
-                if (k >= kmain) break;
+            for (int d = 0; d < D; ++d) {
+                if (k + d < kmain) {
+                    if (d == 0 && k == 0)
+                        fold_first(bufa[0]);
+                    else
+                        fold(bufa[d]);
+                }
             }
+            k += D;
+            if (k >= kmain) break;
+#pragma unroll
+            for (int d = 0; d < D; ++d) bufa[d] = chunk(k + D + d);
+#pragma unroll
+            for (int d = 0; d < D; ++d)
+                if (k + d < kmain) fold(bufb[d]);
+            k += D;
+            if (k >= kmain) break;
         }
     }
-    if (t < n4 - kmain * 256) {
-        int qq[4];
-        SRC::unpack(chunk(kmain), qq);
-        acc = has ? pair(acc, qq[0], tab) : qq[0];
-        has = true;
-        acc = pair(acc, qq[1], tab);
-        acc = pair(acc, qq[2], tab);
-        acc = pair(acc, qq[3], tab);
-    }
-    if (t < tail) {
-        const int q = SRC::one(body + 4 * n4 + t);
+    if (has_extra) fold_first(extra);
+    if (has_suf) {
+        const int q = SRC::cvt(suf);
         acc = has ? pair(acc, q, tab) : q;
     }
     // virtual-warp butterfly (xor 16, 8, 4, 2, 1 inside each 32-lane half)
@@ -252,49 +282,95 @@ __device__ __forceinline__ int tree_row(const typename SRC::T* row, int64_t n, c
     return v;
 }
 
-template <typename SRC, bool USE_LUT>
+// One row per block: with no loop over rows, no load issued for a later
+// round (the prefetch runs past the end of a row's chunks) can be in flight
+// when the next row would reuse its registers, so nothing waits for it.
+template <bool USE_LUT>
+struct Q16Setup {
+    int* lut;
+    int v;
+    __device__ __forceinline__ void issue() {
+        if constexpr (USE_LUT) {
+            if (threadIdx.x < 64) v = kLutQ16[threadIdx.x];
+        }
+    }
+    __device__ __forceinline__ void finish() {
+        if constexpr (USE_LUT) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (threadIdx.x < 64) lut[threadIdx.x] = v;
+            __syncthreads();
+        }
+    }
+};
+
+template <typename SRC, bool USE_LUT, int D = kPrefetch>
 __global__ __launch_bounds__(256) void intlse_q16_rows(const typename SRC::T* __restrict__ x, float* __restrict__ out,
-                                                       int32_t* __restrict__ acc_out, int64_t B, int64_t N) {
+                                                       int32_t* __restrict__ acc_out, int64_t N) {
     __shared__ int lut[64];
     __shared__ int sh_warp[8];
-    if (threadIdx.x < 64) lut[threadIdx.x] = kLutQ16[threadIdx.x];
-    __syncthreads();
+    Q16Setup<USE_LUT> setup{lut, 0};
     auto pair = [](int a, int b, const int* t) { return q16_pair<USE_LUT>(a, b, t); };
-    for (int64_t row = blockIdx.x; row < B; row += gridDim.x) {
-        const int v = tree_row<SRC, 16, kPrefetch>(x + row * N, N, lut, pair, sh_warp);
-        if (threadIdx.x == 0) {
-            out[row] = (float)v * kQ16Out;
-            if (acc_out) acc_out[row] = v;
-        }
+    const int64_t row = blockIdx.x;
+    const int v = tree_row<SRC, 16, D>(x + row * N, N, lut, pair, sh_warp, setup);
+    if (threadIdx.x == 0) {
+        out[row] = (float)v * kQ16Out;
+        if (acc_out) acc_out[row] = v;
     }
 }
 
+// gap[d] = M + LUT[M & 63], M = (64 + ((-d) & 63)) >> ceil(d / 64), for
+// d <= 384; gap[385] = 0.  Thread t builds entries t and t + 256.
+struct Q10Setup {
+    int* gap;
+    int l0, l1;
+    __device__ static __forceinline__ int m_of(int d) {
+        const int sub = -d;
+        const uint32_t sh = (uint32_t)(-(sub >> 6));
+        return (int)((64u | ((uint32_t)sub & 63u)) >> (sh < 31u ? sh : 31u));
+    }
+    __device__ __forceinline__ void issue() {
+        const int d0 = threadIdx.x, d1 = threadIdx.x + 256;
+        l0 = kLutQ10[m_of(d0) & 63];
+        l1 = d1 <= 384 ? kLutQ10[m_of(d1) & 63] : 0;
+    }
+    __device__ __forceinline__ void finish() {
+        // keep the table stores (which wait for their reads) after the row's
+        // first loads are issued
+        __builtin_amdgcn_sched_barrier(0);
+        const int d0 = threadIdx.x, d1 = threadIdx.x + 256;
+        gap[d0] = m_of(d0) + l0;
+        if (d1 <= 384)
+            gap[d1] = m_of(d1) + l1;
+        else if (d1 == 385)
+            gap[d1] = 0;
+        __syncthreads();
+    }
+};
+
+template <int D = kPrefetch>
 __global__ __launch_bounds__(256) void intlse_q10_6_rows(const int16_t* __restrict__ x, float* __restrict__ out,
-                                                         int32_t* __restrict__ acc_out, int64_t B, int64_t N) {
+                                                         int32_t* __restrict__ acc_out, int64_t N) {
     __shared__ int gap[386];
     __shared__ int sh_warp[8];
-    // gap[d] = M + LUT[M & 63], M = (64 + ((-d) & 63)) >> ceil(d / 64), for d <= 384
-    for (int d = threadIdx.x; d < 386; d += 256) {
-        int g = 0;
-        if (d <= 384) {
-            const int sub = -d;
-            const uint32_t sh = (uint32_t)(-(sub >> 6));
-            const int m = (int)((64u | ((uint32_t)sub & 63u)) >> (sh < 31u ? sh : 31u));
-            g = m + kLutQ10[m & 63];
-        }
-        gap[d] = g;
-    }
-    __syncthreads();
-    for (int64_t row = blockIdx.x; row < B; row += gridDim.x) {
-        const int v = tree_row<SrcI16, 8, kPrefetch>(x + row * N, N, gap, q10_pair, sh_warp);
-        if (threadIdx.x == 0) {
-            out[row] = (float)v * kQ10Out;
-            if (acc_out) acc_out[row] = v;
-        }
+    Q10Setup setup{gap, 0, 0};
+    const int64_t row = blockIdx.x;
+    const int v = tree_row<SrcI16, 8, D>(x + row * N, N, gap, q10_pair, sh_warp, setup);
+    if (threadIdx.x == 0) {
+        out[row] = (float)v * kQ10Out;
+        if (acc_out) acc_out[row] = v;
     }
 }
 
-static unsigned row_grid(int64_t B) { return (unsigned)(B < ((int64_t)1 << 30) ? B : ((int64_t)1 << 30)); }
+// Calls launch(grid, x, out, acc) for consecutive chunks of at most 2^30 rows
+// (one block per row).
+template <typename T, typename LAUNCH>
+static void for_row_chunks(const T* x, float* out, int32_t* acc, int64_t B, int64_t N, LAUNCH launch) {
+    constexpr int64_t kMaxGrid = (int64_t)1 << 30;
+    for (int64_t r0 = 0; r0 < B; r0 += kMaxGrid) {
+        const int64_t rows = B - r0 < kMaxGrid ? B - r0 : kMaxGrid;
+        launch(dim3((unsigned)rows), x + r0 * N, out + r0, acc ? acc + r0 : nullptr);
+    }
+}
 
 template <typename T>
 static int int_entry_check(const char* name, const T* x, float* out, int64_t B, int64_t N) {
@@ -318,10 +394,12 @@ extern "C" int fl_intlse_q16_f32(const float* x, float* out, int32_t* acc_out, i
     if (int rc = int_entry_check(name, x, out, B, N)) return rc;
     if (B == 0) return ok();
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    if (use_lut)
-        intlse_q16_rows<SrcF32, true><<<dim3(row_grid(B)), dim3(256), 0, st>>>(x, out, acc_out, B, N);
-    else
-        intlse_q16_rows<SrcF32, false><<<dim3(row_grid(B)), dim3(256), 0, st>>>(x, out, acc_out, B, N);
+    for_row_chunks(x, out, acc_out, B, N, [&](dim3 g, const float* xc, float* oc, int32_t* ac) {
+        if (use_lut)
+            intlse_q16_rows<SrcF32, true><<<g, dim3(256), 0, st>>>(xc, oc, ac, N);
+        else
+            intlse_q16_rows<SrcF32, false><<<g, dim3(256), 0, st>>>(xc, oc, ac, N);
+    });
     return launch_status(name);
 }
 
@@ -331,10 +409,12 @@ extern "C" int fl_intlse_q16_i32(const int32_t* q, float* out, int32_t* acc_out,
     if (int rc = int_entry_check(name, q, out, B, N)) return rc;
     if (B == 0) return ok();
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    if (use_lut)
-        intlse_q16_rows<SrcI32, true><<<dim3(row_grid(B)), dim3(256), 0, st>>>(q, out, acc_out, B, N);
-    else
-        intlse_q16_rows<SrcI32, false><<<dim3(row_grid(B)), dim3(256), 0, st>>>(q, out, acc_out, B, N);
+    for_row_chunks(q, out, acc_out, B, N, [&](dim3 g, const int32_t* qc, float* oc, int32_t* ac) {
+        if (use_lut)
+            intlse_q16_rows<SrcI32, true><<<g, dim3(256), 0, st>>>(qc, oc, ac, N);
+        else
+            intlse_q16_rows<SrcI32, false><<<g, dim3(256), 0, st>>>(qc, oc, ac, N);
+    });
     return launch_status(name);
 }
 
@@ -342,7 +422,9 @@ extern "C" int fl_intlse_q10_6(const int16_t* q, float* out, int32_t* acc_out, i
     const char* name = "fl_intlse_q10_6";
     if (int rc = int_entry_check(name, q, out, B, N)) return rc;
     if (B == 0) return ok();
-    intlse_q10_6_rows<<<dim3(row_grid(B)), dim3(256), 0, reinterpret_cast<hipStream_t>(stream)>>>(q, out, acc_out, B,
-                                                                                                  N);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    for_row_chunks(q, out, acc_out, B, N, [&](dim3 g, const int16_t* qc, float* oc, int32_t* ac) {
+        intlse_q10_6_rows<><<<g, dim3(256), 0, st>>>(qc, oc, ac, N);
+    });
     return launch_status(name);
 }
