@@ -227,8 +227,8 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
             calls = max(iters, nb)
             ms, ok = _time_graph(torch, split, calls, lambda: out.clone())
             ms1, ok1 = _time_graph(torch, one, calls, lambda: out.clone())
-            want = torch.logsumexp(bufs[(calls - 1) % nb], dim=-1)
-            assert torch.allclose(ok, want, rtol=1e-5) and torch.allclose(ok1, want, rtol=1e-5), "graph replay mismatch"
+            expect = torch.logsumexp(bufs[(calls - 1) % nb], dim=-1)
+            assert torch.allclose(ok, expect, rtol=1e-5) and torch.allclose(ok1, expect, rtol=1e-5), "graph replay mismatch"
             rec(f"split_fp32_fwd_{b}x{n}", ms, 4 * b * n + 4 * b, one_pass_us=round(ms1 * 1e3, 2), workspace_bytes=wsb)
             del bufs
     if want("sls"):

@@ -290,3 +290,27 @@ def test_dropin_half_inputs_autograd(cuda, dtype):
     want_g = O.lse_bwd_fp64(w_half.reshape(-1), x64, O.lse_fp64(x64)).reshape(3, 40, 3001)
     got_g = xd.grad.double().cpu().numpy()
     assert (np.abs(got_g - want_g) <= _half_ulp(want_g, dtype) + 1e-5 * np.abs(want_g)).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("N", [300, 20000, 128256])
+def test_fwd_half_robust_special_values(cuda, dtype, N):
+    """Robust half forward (one-pass and, for few long rows, split path):
+    all -inf -> -inf, any +inf -> +inf, any NaN -> NaN, as torch.logsumexp on
+    the same values in fp32."""
+    print(f"case fwd_half_robust {dtype} N={N}", flush=True)
+    rng = np.random.default_rng(N)
+    x = torch.from_numpy((rng.standard_normal((6, N)) * 2).astype(np.float32))
+    x[0, :] = -float("inf")
+    x[1, N // 2] = float("inf")
+    x[2, N - 1] = float("nan")
+    x[3, 0] = float("inf")
+    x[3, N // 3] = -float("inf")
+    x[4, : N - 1] = -float("inf")
+    xh = x.to(dtype)
+    ext = _ext()
+    fn = ext.batched_logsumexp_fp16 if dtype == torch.float16 else ext.batched_logsumexp_bf16
+    got = fn(xh.to(cuda), robust=True).cpu().numpy()
+    want = torch.logsumexp(xh.float(), dim=-1).numpy()
+    assert got[0] == -np.inf and got[1] == np.inf and np.isnan(got[2]) and got[3] == np.inf
+    _close(got[4:], want[4:], RTOL16)
