@@ -416,3 +416,67 @@ def fp64_lse_ref(x_fp32) -> np.ndarray:
 
 
 LN2 = math.log(2.0)
+
+
+# ----------------------------------------------------------------------------
+# The reference's CPU wrappers around the AVX2 IntLSE (test infrastructure:
+# their dispatch and special-value handling, restated over either the C
+# restatement of the kernel or the compiled reference in oracle/_ref).
+# ----------------------------------------------------------------------------
+def _cpu_rows(backend):
+    return ref_intlse_cpu_rows if backend == "ref" else intlse_cpu_rows
+
+
+def logsumexp_intlse(a, axis=None, keepdims=False, backend="port"):
+    """lse_ctypes_wrapper.py:99-125: a NaN or +inf anywhere sends the whole call
+    to np.logaddexp.reduce; otherwise the -inf-identity kernel variant runs
+    over the flattened array (axis=None) or the last axis (1-D -> float,
+    2-D -> float32[B], higher ranks flattened to rows); other axes raise
+    NotImplementedError.  As in the reference, keepdims is ignored by the
+    finite full reduction (axis=None returns a float)."""
+    a = np.asarray(a, dtype=np.float32)
+    rows_fn = _cpu_rows(backend)
+    maximum = np.max(a) if a.size else -np.inf
+    if np.isnan(maximum) or np.isposinf(maximum):
+        if axis is None:
+            result = np.logaddexp.reduce(a.ravel())
+            if keepdims:
+                return np.full((1,) * a.ndim, result, dtype=np.float32)
+            return result
+        return np.logaddexp.reduce(a, axis=axis, keepdims=keepdims)
+
+    def one(v):  # lse_intlse_simd_neg_inf: a 1-D row -> Python float
+        return float(rows_fn(np.ascontiguousarray(v, np.float32)[None, :], True)[0])
+
+    if axis is None:
+        return one(a.ravel())
+    if axis == -1 or axis == a.ndim - 1:
+        if a.ndim == 1:
+            r = one(a)
+            return r if not keepdims else np.array([r], dtype=np.float32)
+        if a.ndim == 2:
+            r = rows_fn(a, True)
+            return r if not keepdims else r[..., None]
+        r = rows_fn(a.reshape(-1, a.shape[-1]), True)
+        out = r.reshape(a.shape[:-1])
+        return out if not keepdims else out[..., None]
+    raise NotImplementedError(f"axis={axis} not yet supported")
+
+
+def logsumexp_intlse_torch(input_tensor, dim=-1, keepdim=False, backend="port"):
+    """torch_wrapper.py:9-29: CPU fp32 tensors reduced over the last dimension
+    (N >= 2, no grad) go through logsumexp_intlse; everything else to
+    torch.logsumexp."""
+    import torch
+
+    normalized_dim = dim if dim >= 0 else input_tensor.dim() + dim
+    supported = (input_tensor.device.type == "cpu" and input_tensor.dtype == torch.float32
+                 and normalized_dim == input_tensor.dim() - 1 and input_tensor.shape[-1] >= 2
+                 and not input_tensor.requires_grad)
+    if not supported:
+        return torch.logsumexp(input_tensor, dim=dim, keepdim=keepdim)
+    output = logsumexp_intlse(input_tensor.detach().contiguous().numpy(), axis=-1, keepdims=keepdim,
+                              backend=backend)
+    if isinstance(output, np.ndarray):
+        return torch.from_numpy(output)
+    return torch.tensor(output, dtype=input_tensor.dtype)
