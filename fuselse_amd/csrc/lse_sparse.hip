@@ -221,16 +221,34 @@ __device__ __forceinline__ void fold_group_f32(const float (&v)[G][PP], const Ed
     }
 }
 
-template <int ET, int GS>
-__device__ __forceinline__ void fold_group_q16(const float (&v)[GS][P], const EdgeMeta& ew, int j, int wn,
-                                               int (&acc)[ET][P], const int* __restrict__ lut) {
+// Edge g of a group starting at window edge j belongs to chain (j + g) % ET.
+// Windows start at multiples of 64 and groups at multiples of G = 4, so for
+// ET <= 4 the chain is g % ET, and for ET = 8 it is C0 + g with C0 = j % 8,
+// 0 or 4: a wave-uniform choice between two static code paths.
+template <int ET, int C0>
+__device__ __forceinline__ void fold_group_q16_at(const float (&v)[G][P], const EdgeMeta& ew, int j, int wn,
+                                                  int (&acc)[ET][P], const int* __restrict__ lut) {
 #pragma unroll
-    for (int g = 0; g < GS; ++g) {
+    for (int g = 0; g < G; ++g) {
         if (j + g < wn) {
             const float lw = bcastf(ew.logw, j + g);
+            const int c = (C0 + g) % ET;
 #pragma unroll
-            for (int i = 0; i < P; ++i) acc[g % ET][i] = pair(acc[g % ET][i], quant(lw + v[g][i]), lut);
+            for (int i = 0; i < P; ++i) acc[c][i] = pair(acc[c][i], quant(lw + v[g][i]), lut);
         }
+    }
+}
+
+template <int ET>
+__device__ __forceinline__ void fold_group_q16(const float (&v)[G][P], const EdgeMeta& ew, int j, int wn,
+                                               int (&acc)[ET][P], const int* __restrict__ lut) {
+    if constexpr (ET == 8) {
+        if (j & 4)
+            fold_group_q16_at<ET, 4>(v, ew, j, wn, acc, lut);
+        else
+            fold_group_q16_at<ET, 0>(v, ew, j, wn, acc, lut);
+    } else {
+        fold_group_q16_at<ET, 0>(v, ew, j, wn, acc, lut);
     }
 }
 
@@ -277,18 +295,15 @@ template <int ET, bool VEC, typename LAYOUT, typename DESC>
 __device__ __forceinline__ void reduce_q16_et(const LAYOUT& L, const DESC& d, const EdgeMeta& first,
                                               const float* __restrict__ child, int64_t batch, int64_t b0, int l,
                                               const int* __restrict__ lut) {
-    // group start edges are multiples of GS (and of 64 across windows), so
-    // edge g of a group belongs to chain g % ET
-    constexpr int GS = ET > G ? ET : G;
     int acc[ET][P];
 #pragma unroll
     for (int c = 0; c < ET; ++c)
 #pragma unroll
         for (int i = 0; i < P; ++i) acc[c][i] = kNegInfQ;
-    walk_edges<GS, VEC, P>(L, d, first, child, batch, b0, l,
-                        [&](const float (&v)[GS][P], int j, int wn, const EdgeMeta& ew) {
-                            fold_group_q16<ET, GS>(v, ew, j, wn, acc, lut);
-                        });
+    walk_edges<G, VEC, P>(L, d, first, child, batch, b0, l,
+                          [&](const float (&v)[G][P], int j, int wn, const EdgeMeta& ew) {
+                              fold_group_q16<ET>(v, ew, j, wn, acc, lut);
+                          });
     float res[P];
 #pragma unroll
     for (int i = 0; i < P; ++i) {
