@@ -348,7 +348,9 @@ __global__ __launch_bounds__(256) void sparse_kernel(LAYOUT L, const float* __re
         __syncthreads();
     }
     const int l = lane_id();
-    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    // the wave index made wave-uniform explicitly, so the node's descriptor
+    // comes through scalar loads
+    const int64_t item = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (item >= items) return;
     const auto desc = L.node(item);
     const EdgeMeta first = l < desc.k ? L.meta(desc, l) : EdgeMeta{0, 0.0f};
@@ -455,7 +457,7 @@ __global__ __launch_bounds__(256) void csr_bwd_kernel(const float* __restrict__ 
                                                       float* __restrict__ gchild, float* __restrict__ glogp,
                                                       int64_t children, int64_t batch) {
     const int l = lane_id();
-    const int64_t c = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t c = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (c >= children) return;
     const int64_t p0 = uniform64(csc_off[c]);
     const int64_t k = uniform64(csc_off[c + 1]) - p0;
