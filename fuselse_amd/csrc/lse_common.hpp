@@ -146,6 +146,13 @@ __device__ __forceinline__ void store_stream(V v, void* p) {
 }
 struct bf16_t { uint16_t bits; };
 
+// Cache policy of streamed 16-byte result stores through a buffer resource:
+// device scope (sc1) and nontemporal (nt).  Written through to memory instead
+// of left dirty in the XCD's L2, a row of results streams out in one pass;
+// the (512, 128256) fp32 backward measured 79.9 us with it against 85.2 us
+// with nt alone.
+constexpr int kStoreStreamAux = 16 | 2;
+
 // fp32 -> bfloat16, round to nearest even; NaN stays a (quiet) NaN.
 __device__ __forceinline__ uint32_t bf16_rne_bits(float f) {
     const uint32_t u = __builtin_bit_cast(uint32_t, f);
@@ -167,6 +174,11 @@ template <> struct Elem<float> {
         t.x = v[0]; t.y = v[1]; t.z = v[2]; t.w = v[3];
         store_stream<f32x4>(t, p);
     }
+    __device__ static __forceinline__ void put_vec_buf(__amdgpu_buffer_rsrc_t r, int off, const float (&v)[4]) {
+        f32x4 t;
+        t.x = v[0]; t.y = v[1]; t.z = v[2]; t.w = v[3];
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, t), r, off, 0, kStoreStreamAux);
+    }
 };
 template <> struct Elem<_Float16> {
     static constexpr int kVec = 8;
@@ -184,6 +196,12 @@ template <> struct Elem<_Float16> {
         for (int k = 0; k < 8; ++k) t[k] = (_Float16)v[k];
         store_stream<f16x8>(t, p);
     }
+    __device__ static __forceinline__ void put_vec_buf(__amdgpu_buffer_rsrc_t r, int off, const float (&v)[8]) {
+        f16x8 t;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) t[k] = (_Float16)v[k];
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, t), r, off, 0, kStoreStreamAux);
+    }
 };
 template <> struct Elem<bf16_t> {
     static constexpr int kVec = 8;
@@ -200,10 +218,16 @@ template <> struct Elem<bf16_t> {
     }
     __device__ static __forceinline__ void put(bf16_t* p, float v) { p->bits = (uint16_t)bf16_rne_bits(v); }
     __device__ static __forceinline__ void put_vec(bf16_t* p, const float (&v)[8]) {
+        store_stream<u32x4>(pack(v), p);
+    }
+    __device__ static __forceinline__ void put_vec_buf(__amdgpu_buffer_rsrc_t r, int off, const float (&v)[8]) {
+        __builtin_amdgcn_raw_buffer_store_b128(pack(v), r, off, 0, kStoreStreamAux);
+    }
+    __device__ static __forceinline__ u32x4 pack(const float (&v)[8]) {
         u32x4 t;
 #pragma unroll
         for (int k = 0; k < 4; ++k) t[k] = bf16_rne_bits(v[2 * k]) | (bf16_rne_bits(v[2 * k + 1]) << 16);
-        store_stream<u32x4>(t, p);
+        return t;
     }
 };
 

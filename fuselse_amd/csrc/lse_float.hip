@@ -402,21 +402,40 @@ __device__ __forceinline__ void bwd_one(T* gr, const T* xr, int64_t c, float gv,
     Elem<T>::put(gr + c, bwd_elem(gv, lv, Elem<T>::scalar(xr + c)) + (GR::kSel && c == t ? g0 : 0.0f));
 }
 
+// Destination of a row body's 16-byte result vectors.  BUF: a buffer
+// resource over the body, stored with kStoreStreamAux (rows under 2 GiB);
+// otherwise plain nontemporal pointer stores.
+template <typename T, bool BUF>
+struct RowOut {
+    T* body;
+    __amdgpu_buffer_rsrc_t rsrc;
+    __device__ __forceinline__ RowOut(T* b, int64_t nvec) : body(b) {
+        if constexpr (BUF)
+            rsrc = __builtin_amdgcn_make_buffer_rsrc(b, 0, (int)(nvec * 16), 0x00020000);
+    }
+    __device__ __forceinline__ void put(int64_t i, const float (&v)[Elem<T>::kVec]) const {
+        if constexpr (BUF)
+            Elem<T>::put_vec_buf(rsrc, (int)(i * 16), v);
+        else
+            Elem<T>::put_vec(body + i * Elem<T>::kVec, v);
+    }
+};
+
 // One 16-byte vector i of a row body whose first column is head.
-template <typename T, typename GR>
-__device__ __forceinline__ void bwd_vec(T* body_g, const T* body_x, int64_t i, int64_t head, float gv, float lv,
-                                        bool fma_ok, int64_t t, float g0) {
+template <typename T, typename GR, bool BUF>
+__device__ __forceinline__ void bwd_vec(const RowOut<T, BUF>& dst, const T* body_x, int64_t i, int64_t head, float gv,
+                                        float lv, bool fma_ok, int64_t t, float g0) {
     constexpr int VE = Elem<T>::kVec;
     float v[VE];
     Elem<T>::vec(body_x + i * VE, v);
     bwd_vals<VE>(gv, lv, fma_ok, v);
     add_at<GR::kSel, VE>(v, head + VE * i, t, g0);
-    Elem<T>::put_vec(body_g + i * VE, v);
+    dst.put(i, v);
 }
 
 // Long rows: grid = B * chunks_per_row blocks of 256 threads; a block covers
 // 256*U consecutive vectors of one row.  x and grad_x share their alignment.
-template <typename T, int U, typename GR>
+template <typename T, int U, typename GR, bool BUF>
 __global__ __launch_bounds__(256) void lse_bwd_row_chunks(const float* __restrict__ g, const T* __restrict__ x,
                                                           const float* __restrict__ lse, T* __restrict__ gx,
                                                           int64_t N, int64_t chunks_per_row, GR gr_t) {
@@ -437,7 +456,7 @@ __global__ __launch_bounds__(256) void lse_bwd_row_chunks(const float* __restric
         if (tid < sp.tail) bwd_one<T, GR>(gr, xr, sp.head + sp.nvec * VE + tid, gv, lv, t, g0);
     }
     const T* xb = xr + sp.head;
-    T* gb = gr + sp.head;
+    const RowOut<T, BUF> gb(gr + sp.head, sp.nvec);
     const bool fma_ok = __builtin_fabsf(lv) < 64.0f;
     const int64_t i0 = chunk * 256 * U + tid;
     if constexpr (U == 1) {
@@ -452,7 +471,7 @@ __global__ __launch_bounds__(256) void lse_bwd_row_chunks(const float* __restric
 }
 
 // Short rows: LPR lanes per row, 256/LPR rows per block, grid-stride.
-template <typename T, int LPR, typename GR>
+template <typename T, int LPR, typename GR, bool BUF>
 __global__ __launch_bounds__(256) void lse_bwd_group_rows(const float* __restrict__ g, const T* __restrict__ x,
                                                           const float* __restrict__ lse, T* __restrict__ gx,
                                                           int64_t B, int64_t N, GR gr_t) {
@@ -472,8 +491,8 @@ __global__ __launch_bounds__(256) void lse_bwd_group_rows(const float* __restric
         const int64_t t0 = sp.head + sp.nvec * VE;
         for (int64_t c = j; c < sp.tail; c += LPR) bwd_one<T, GR>(gr, xr, t0 + c, gv, lv, t, g0);
         const bool fma_ok = __builtin_fabsf(lv) < 64.0f;
-        for (int64_t i = j; i < sp.nvec; i += LPR)
-            bwd_vec<T, GR>(gr + sp.head, xr + sp.head, i, sp.head, gv, lv, fma_ok, t, g0);
+        const RowOut<T, BUF> gb(gr + sp.head, sp.nvec);
+        for (int64_t i = j; i < sp.nvec; i += LPR) bwd_vec<T, GR>(gb, xr + sp.head, i, sp.head, gv, lv, fma_ok, t, g0);
     }
 }
 
@@ -492,24 +511,17 @@ __global__ __launch_bounds__(256) void lse_bwd_scalar(const float* __restrict__ 
     }
 }
 
-template <typename T, typename GR>
-static void launch_bwd(const float* g, const T* x, const float* lse, T* gx, int64_t B, int64_t N, GR gr_t,
-                       hipStream_t st) {
+template <typename T, typename GR, bool BUF>
+static void launch_bwd_vec(const float* g, const T* x, const float* lse, T* gx, int64_t B, int64_t N, GR gr_t,
+                           hipStream_t st) {
     constexpr int VE = Elem<T>::kVec;
-    const bool same_align = ((reinterpret_cast<uintptr_t>(x) ^ reinterpret_cast<uintptr_t>(gx)) & 15u) == 0;
-    if (!same_align) {
-        int64_t gxdim = (N + 255) / 256;
-        if (gxdim > 1024) gxdim = 1024;
-        int64_t gydim = B < 65535 ? B : 65535;
-        lse_bwd_scalar<T><<<dim3((unsigned)gxdim, (unsigned)gydim), dim3(256), 0, st>>>(g, x, lse, gx, B, N, gr_t);
-        return;
-    }
     const int64_t vecs = N / VE + 1;
     if (vecs >= 1024) {
         // one 16-byte vector per lane: measured best for fp32 (with 128x2 and 1024x1)
         constexpr int U = 1;
         const int64_t cpr = (vecs + 256 * U - 1) / (256 * U);
-        lse_bwd_row_chunks<T, U><<<dim3((unsigned)(B * cpr)), dim3(256), 0, st>>>(g, x, lse, gx, N, cpr, gr_t);
+        lse_bwd_row_chunks<T, U, GR, BUF>
+            <<<dim3((unsigned)(B * cpr)), dim3(256), 0, st>>>(g, x, lse, gx, N, cpr, gr_t);
         return;
     }
     int64_t lpr = pow2_ceil((vecs + 3) / 4);
@@ -519,14 +531,32 @@ static void launch_bwd(const float* g, const T* x, const float* lse, T* gx, int6
     if (grid > (int64_t)1 << 30) grid = (int64_t)1 << 30;
     const dim3 gd((unsigned)grid), blk(256);
     switch (lpr) {
-    case 4: lse_bwd_group_rows<T, 4><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
-    case 8: lse_bwd_group_rows<T, 8><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
-    case 16: lse_bwd_group_rows<T, 16><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
-    case 32: lse_bwd_group_rows<T, 32><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
-    case 64: lse_bwd_group_rows<T, 64><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
-    case 128: lse_bwd_group_rows<T, 128><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
-    default: lse_bwd_group_rows<T, 256><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
+    case 4: lse_bwd_group_rows<T, 4, GR, BUF><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
+    case 8: lse_bwd_group_rows<T, 8, GR, BUF><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
+    case 16: lse_bwd_group_rows<T, 16, GR, BUF><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
+    case 32: lse_bwd_group_rows<T, 32, GR, BUF><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
+    case 64: lse_bwd_group_rows<T, 64, GR, BUF><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
+    case 128: lse_bwd_group_rows<T, 128, GR, BUF><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
+    default: lse_bwd_group_rows<T, 256, GR, BUF><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
     }
+}
+
+template <typename T, typename GR>
+static void launch_bwd(const float* g, const T* x, const float* lse, T* gx, int64_t B, int64_t N, GR gr_t,
+                       hipStream_t st) {
+    const bool same_align = ((reinterpret_cast<uintptr_t>(x) ^ reinterpret_cast<uintptr_t>(gx)) & 15u) == 0;
+    if (!same_align) {
+        int64_t gxdim = (N + 255) / 256;
+        if (gxdim > 1024) gxdim = 1024;
+        int64_t gydim = B < 65535 ? B : 65535;
+        lse_bwd_scalar<T><<<dim3((unsigned)gxdim, (unsigned)gydim), dim3(256), 0, st>>>(g, x, lse, gx, B, N, gr_t);
+        return;
+    }
+    // buffer stores take 32-bit offsets: rows of 2 GiB or more keep pointer stores
+    if (N * (int64_t)sizeof(T) < ((int64_t)1 << 31))
+        launch_bwd_vec<T, GR, true>(g, x, lse, gx, B, N, gr_t, st);
+    else
+        launch_bwd_vec<T, GR, false>(g, x, lse, gx, B, N, gr_t, st);
 }
 
 template <typename T, typename GR>
