@@ -153,11 +153,14 @@ struct bf16_t { uint16_t bits; };
 // with nt alone.
 constexpr int kStoreStreamAux = 16 | 2;
 
-// fp32 -> bfloat16, round to nearest even; NaN stays a (quiet) NaN.
-__device__ __forceinline__ uint32_t bf16_rne_bits(float f) {
-    const uint32_t u = __builtin_bit_cast(uint32_t, f);
-    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+// fp32 -> bfloat16 pairs with gfx950's v_cvt_pk_bf16_f32 (round to nearest
+// even, NaN stays NaN): lo in bits 0-15, hi in bits 16-31.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t bf16_pack2(float lo, float hi) {
+    bf16x2_t v;
+    v[0] = (__bf16)lo;
+    v[1] = (__bf16)hi;
+    return __builtin_bit_cast(uint32_t, v);
 }
 
 template <typename T> struct Elem;
@@ -216,7 +219,9 @@ template <> struct Elem<bf16_t> {
             o[2 * k + 1] = __builtin_bit_cast(float, v[k] & 0xFFFF0000u);
         }
     }
-    __device__ static __forceinline__ void put(bf16_t* p, float v) { p->bits = (uint16_t)bf16_rne_bits(v); }
+    __device__ static __forceinline__ void put(bf16_t* p, float v) {
+        p->bits = __builtin_bit_cast(uint16_t, (__bf16)v);
+    }
     __device__ static __forceinline__ void put_vec(bf16_t* p, const float (&v)[8]) {
         store_stream<u32x4>(pack(v), p);
     }
@@ -226,7 +231,7 @@ template <> struct Elem<bf16_t> {
     __device__ static __forceinline__ u32x4 pack(const float (&v)[8]) {
         u32x4 t;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) t[k] = bf16_rne_bits(v[2 * k]) | (bf16_rne_bits(v[2 * k + 1]) << 16);
+        for (int k = 0; k < 4; ++k) t[k] = bf16_pack2(v[2 * k], v[2 * k + 1]);
         return t;
     }
 };
