@@ -292,6 +292,14 @@ static void launch_fwd(const T* x, OUT out, int64_t B, int64_t N, hipStream_t st
         lse_fwd_block_rows<T, ROBUST, 512, 2, OUT><<<dim3((unsigned)grid), dim3(512), 0, st>>>(x, out, B, N);
         return;
     }
+    if (vecs > 1024 && B <= 1024) {
+        // few mid-length rows: one wave per row leaves the GPU under-filled;
+        // a 256-thread block per row measured 13-37% faster for B <= 1024 and
+        // 1125..4000 vectors (fp16, N = 9000..32000), and within 2% above
+        const int64_t grid = B;
+        lse_fwd_block_rows<T, ROBUST, 256, 2, OUT><<<dim3((unsigned)grid), dim3(256), 0, st>>>(x, out, B, N);
+        return;
+    }
     int64_t lpr = pow2_ceil((vecs + 3) / 4);
     if (lpr < 4) lpr = 4;
     if (lpr > 64) lpr = 64;

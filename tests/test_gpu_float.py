@@ -314,3 +314,27 @@ def test_fwd_half_robust_special_values(cuda, dtype, N):
     want = torch.logsumexp(xh.float(), dim=-1).numpy()
     assert got[0] == -np.inf and got[1] == np.inf and np.isnan(got[2]) and got[3] == np.inf
     _close(got[4:], want[4:], RTOL16)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("B,N,off", [(3, 9000, 0), (1024, 16000, 0), (77, 32000, 3), (5, 8193, 1)])
+def test_fwd_mid_rows_block_geometry(cuda, dtype, B, N, off):
+    """Few mid-length rows (1024 < vectors <= 4096, B <= 1024) take one
+    256-thread block per row; parity with fp64 at the tolerance of the dtype,
+    robust and plain, aligned and offset rows."""
+    print(f"case fwd_mid {dtype} B={B} N={N} off={off}", flush=True)
+    rng = np.random.default_rng(B + N + off)
+    x32 = (rng.standard_normal((B, N)) * 2).astype(np.float32)
+    xt = torch.from_numpy(x32).to(dtype)
+    xd = _offset_view(xt, cuda, off)
+    ext = _ext()
+    want = O.lse_fp64(xt.double().numpy())
+    for robust in (False, True):
+        if dtype == torch.float32:
+            got = (ext.onepass_lse_float_robust if robust else ext.onepass_lse_float)(xd)
+            tol = RTOL32
+        else:
+            fn = ext.batched_logsumexp_fp16 if dtype == torch.float16 else ext.batched_logsumexp_bf16
+            got = fn(xd, robust=robust)
+            tol = RTOL16
+        _close(got.cpu().numpy(), want, tol, atol=1e-6)
