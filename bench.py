@@ -496,7 +496,7 @@ def main():
                 "plain_us": round(fwd_plain_ms * 1e3, 2)},
         "bwd": {"us": round(bwd_ms * 1e3, 2), "gbps": round(bwd_gbps, 1),
                 "pct_peak": round(100 * bwd_gbps * 1e9 / HBM_PEAK, 2), "bytes": BWD_BYTES},
-        "roofline": {"bound": "hbm", "kernel": "lse_bwd_row_chunks<1, LseGrad> (fused backward)",
+        "roofline": {"bound": "hbm", "kernel": "lse_bwd_row_chunks<float, 1, LseGrad, true> (fused backward)",
                      "achieved": round(bwd_gbps, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                      "frac": round(bwd_gbps * 1e9 / HBM_PEAK, 4), "traffic": traffic},
         "roofline_fwd": {"bound": "hbm", "kernel": "lse_fwd_block_rows<float, true, 512, 2, LseOut> (robust forward)",
