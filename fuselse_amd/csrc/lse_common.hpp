@@ -152,6 +152,8 @@ struct bf16_t { uint16_t bits; };
 // the (512, 128256) fp32 backward measured 79.9 us with it against 85.2 us
 // with nt alone.
 constexpr int kStoreStreamAux = 16 | 2;
+// Streamed loads through a buffer resource: nontemporal (nt), as load_stream.
+constexpr int kLoadStreamAux = 2;
 
 // fp32 -> bfloat16 pairs with gfx950's v_cvt_pk_bf16_f32 (round to nearest
 // even, NaN stays NaN): lo in bits 0-15, hi in bits 16-31.
@@ -166,7 +168,18 @@ __device__ __forceinline__ uint32_t bf16_pack2(float lo, float hi) {
 template <typename T> struct Elem;
 template <> struct Elem<float> {
     static constexpr int kVec = 4;
+    static constexpr uint32_t kNegInfBits = 0xFF800000u;  // -inf in each 32-bit word
     __device__ static __forceinline__ float scalar(const float* p) { return *p; }
+    // cvt widens one raw 16-byte vector (as loaded by load_stream<u32x4>).
+    // Each lane goes through a scalar temporary: this clang folds a bit_cast
+    // whose operand is an ext-vector element to element 0.
+    __device__ static __forceinline__ void cvt(u32x4 r, float (&o)[4]) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t e = r[k];
+            o[k] = __builtin_bit_cast(float, e);
+        }
+    }
     __device__ static __forceinline__ void vec(const float* p, float (&o)[4]) {
         f32x4 v = load_stream<f32x4>(p);
         o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
@@ -185,7 +198,13 @@ template <> struct Elem<float> {
 };
 template <> struct Elem<_Float16> {
     static constexpr int kVec = 8;
+    static constexpr uint32_t kNegInfBits = 0xFC00FC00u;
     __device__ static __forceinline__ float scalar(const _Float16* p) { return (float)*p; }
+    __device__ static __forceinline__ void cvt(u32x4 r, float (&o)[8]) {
+        const f16x8 v = __builtin_bit_cast(f16x8, r);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) o[k] = (float)v[k];
+    }
     __device__ static __forceinline__ void vec(const _Float16* p, float (&o)[8]) {
         f16x8 v = load_stream<f16x8>(p);
 #pragma unroll
@@ -208,17 +227,18 @@ template <> struct Elem<_Float16> {
 };
 template <> struct Elem<bf16_t> {
     static constexpr int kVec = 8;
+    static constexpr uint32_t kNegInfBits = 0xFF80FF80u;
     __device__ static __forceinline__ float scalar(const bf16_t* p) {
         return __builtin_bit_cast(float, (uint32_t)p->bits << 16);
     }
-    __device__ static __forceinline__ void vec(const bf16_t* p, float (&o)[8]) {
-        u32x4 v = load_stream<u32x4>(p);
+    __device__ static __forceinline__ void cvt(u32x4 v, float (&o)[8]) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             o[2 * k] = __builtin_bit_cast(float, v[k] << 16);
             o[2 * k + 1] = __builtin_bit_cast(float, v[k] & 0xFFFF0000u);
         }
     }
+    __device__ static __forceinline__ void vec(const bf16_t* p, float (&o)[8]) { cvt(load_stream<u32x4>(p), o); }
     __device__ static __forceinline__ void put(bf16_t* p, float v) {
         p->bits = __builtin_bit_cast(uint16_t, (__bf16)v);
     }

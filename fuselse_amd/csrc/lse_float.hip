@@ -28,9 +28,12 @@ __device__ __forceinline__ void fold_scalar(float& m, float& s, const T* p) {
 }
 
 // Folds the vectors body[i], body[i + STRIDE], ... (i < nvec) into (m, s),
-// U vectors per rescale.
+// U vectors per rescale, one burst of U loads at a time: each iteration
+// issues its U loads and folds them once they land.  Where other waves cover
+// the load latency (fp32 rows, short rows) this beats the pipelined loop
+// below, whose extra loads in flight measured 2-10% slower there.
 template <typename T, bool ROBUST, int STRIDE, int U>
-__device__ __forceinline__ void fold_body(float& m, float& s, const T* body, int64_t i, int64_t nvec) {
+__device__ __forceinline__ void fold_body_burst(float& m, float& s, const T* body, int64_t i, int64_t nvec) {
     constexpr int VE = Elem<T>::kVec;
     for (; i + (int64_t)(U - 1) * STRIDE < nvec; i += (int64_t)U * STRIDE) {
         float v[U * VE];
@@ -48,6 +51,121 @@ __device__ __forceinline__ void fold_body(float& m, float& s, const T* body, int
         Elem<T>::vec(body + i * VE, v);
         lse_fold<ROBUST, VE>(m, s, v);
     }
+}
+
+// Folds the raw vectors a[0..U) into (m, s) with one rescale.
+template <typename T, bool ROBUST, int U>
+__device__ __forceinline__ void fold_raw(float& m, float& s, const u32x4 (&a)[U]) {
+    constexpr int VE = Elem<T>::kVec;
+    float v[U * VE];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        float t[VE];
+        Elem<T>::cvt(a[u], t);
+#pragma unroll
+        for (int k = 0; k < VE; ++k) v[u * VE + k] = t[k];
+    }
+    lse_fold<ROBUST, U * VE>(m, s, v);
+}
+
+// Loads batch t of a lane: its vectors t * STEP + l + u * STRIDE (u < U).
+// The batch goes through a buffer resource based at the batch's start
+// (wave-uniform, so it lives in scalar registers), which keeps the 32-bit
+// offsets small for rows of any length; the resource's range check returns
+// zeros, without a memory access, for the bytes past `region`.
+template <int STRIDE, int U>
+__device__ __forceinline__ void load_batch(u32x4 (&a)[U], const char* base, int64_t region, int lane_off,
+                                           int64_t t) {
+    constexpr int64_t STEP_BYTES = (int64_t)U * STRIDE * 16;
+    const int64_t left = region - t * STEP_BYTES;
+    const int nrec = left <= 0 ? 0 : (left > 0x7fffffff ? 0x7fffffff : (int)left);
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base + t * STEP_BYTES), 0, nrec, 0x00020000);
+#pragma unroll
+    for (int u = 0; u < U; ++u) a[u] = __builtin_amdgcn_raw_buffer_load_b128(r, lane_off + u * STRIDE * 16, 0, kLoadStreamAux);
+}
+
+// Folds the last batch: the lane's vectors at or past `count` (counted from
+// the batch start) become -inf in their raw form, then the robust fold runs.
+// It keeps (m, s) = (-inf, 0) for a lane with nothing yet and equals the
+// plain fold on finite values, so both variants use it here.  Masking the raw
+// bits first also leaves nothing in common with the whole-batch fold that the
+// compiler could hoist above the loads that precede it.
+template <typename T, int STRIDE, int U>
+__device__ __forceinline__ void fold_last(float& m, float& s, const u32x4 (&a)[U], int l, int64_t count) {
+    u32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const bool ok = l + (int64_t)u * STRIDE < count;
+        const uint32_t ninf = Elem<T>::kNegInfBits;
+        v[u] = ok ? a[u] : u32x4{ninf, ninf, ninf, ninf};
+    }
+    fold_raw<T, true, U>(m, s, v);
+}
+
+// Folds the body vectors l, l + STRIDE, ... below `end` of this lane's row
+// into (m, s), U vectors per rescale, for a lane l in [0, STRIDE).  Vector v
+// of the row lies at base + lane_off + (v - l) * 16, with base wave-uniform;
+// `region` bounds the bytes at base that may be read.  The caller passes
+// `trips`, a wave-uniform batch count with (trips - 1) * U * STRIDE <= end <=
+// trips * U * STRIDE for every row of the wave: batches 0 .. trips - 2 are
+// whole for every lane and batch trips - 1 is masked.  The batches are
+// software-pipelined: batch t + 1 is issued before batch t is folded, in two
+// alternating register sets, so no register copy has to wait for a load in
+// flight and each lane keeps 2U loads outstanding while it computes.  The
+// sched_barrier after each issue keeps the scheduler from moving the fold
+// (and its wait) above the new loads; the uniform trip count keeps every
+// branch scalar.
+// A wave-uniform 64-bit value in scalar registers.  Values the compiler
+// computes inside a divergent branch are treated as divergent even when every
+// lane holds the same; a buffer resource built from such a value would be
+// issued once per distinct value (a waterfall loop).
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)v >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+template <typename T, bool ROBUST, int STRIDE, int U>
+__device__ __forceinline__ void fold_body(float& m, float& s, const char* base, int64_t region, int lane_off, int l,
+                                          int64_t end, int64_t trips) {
+    constexpr int64_t STEP = (int64_t)U * STRIDE;
+    base = reinterpret_cast<const char*>(uniform64(reinterpret_cast<int64_t>(base)));
+    region = uniform64(region);
+    trips = uniform64(trips);
+    if (trips <= 0) return;
+    const int64_t count = end - (trips - 1) * STEP;
+    u32x4 a[U], c[U];
+    load_batch<STRIDE, U>(a, base, region, lane_off, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (trips == 1) {
+        fold_last<T, STRIDE, U>(m, s, a, l, count);
+        return;
+    }
+    int64_t t = 1;  // batches issued
+    while (true) {
+        load_batch<STRIDE, U>(c, base, region, lane_off, t);
+        __builtin_amdgcn_sched_barrier(0);
+        fold_raw<T, ROBUST, U>(m, s, a);
+        if (t == trips - 1) {
+            fold_last<T, STRIDE, U>(m, s, c, l, count);
+            return;
+        }
+        ++t;
+        load_batch<STRIDE, U>(a, base, region, lane_off, t);
+        __builtin_amdgcn_sched_barrier(0);
+        fold_raw<T, ROBUST, U>(m, s, c);
+        if (t == trips - 1) {
+            fold_last<T, STRIDE, U>(m, s, a, l, count);
+            return;
+        }
+        ++t;
+    }
+}
+
+template <int64_t STEP>
+__device__ __forceinline__ int64_t batches(int64_t n) {
+    return n > 0 ? (n + STEP - 1) / STEP : 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -87,7 +205,7 @@ struct SelectOut {
 };
 
 // One block per row (grid-stride over rows).
-template <typename T, bool ROBUST, int THREADS, int U, typename OUT>
+template <typename T, bool ROBUST, int THREADS, int U, bool PIPE, typename OUT>
 __global__ __launch_bounds__(THREADS) void lse_fwd_block_rows(const T* __restrict__ x, OUT out, int64_t B,
                                                               int64_t N) {
     constexpr int VE = Elem<T>::kVec;
@@ -102,7 +220,11 @@ __global__ __launch_bounds__(THREADS) void lse_fwd_block_rows(const T* __restric
         float m = -kInf, s = 0.0f;
         if (tid < sp.head) fold_scalar<T, ROBUST>(m, s, p + tid);
         if (tid < sp.tail) fold_scalar<T, ROBUST>(m, s, p + sp.head + sp.nvec * VE + tid);
-        fold_body<T, ROBUST, THREADS, U>(m, s, p + sp.head, tid, sp.nvec);
+        if constexpr (PIPE)
+            fold_body<T, ROBUST, THREADS, U>(m, s, reinterpret_cast<const char*>(p + sp.head), sp.nvec * 16, tid * 16,
+                                             tid, sp.nvec, batches<(int64_t)U * THREADS>(sp.nvec));
+        else
+            fold_body_burst<T, ROBUST, THREADS, U>(m, s, p + sp.head, tid, sp.nvec);
         group_merge<64>(m, s);
         if ((tid & 63) == 0) {
             sh_m[tid >> 6] = m;
@@ -121,16 +243,24 @@ __global__ __launch_bounds__(THREADS) void lse_fwd_block_rows(const T* __restric
 
 // LPR lanes per row, 64/LPR rows per wave, WAVES waves per block
 // (grid-stride over row groups).
-template <typename T, bool ROBUST, int LPR, int U, typename OUT>
+template <typename T, bool ROBUST, int LPR, int U, bool PIPE, typename OUT>
 __global__ __launch_bounds__(256) void lse_fwd_group_rows(const T* __restrict__ x, OUT out, int64_t B, int64_t N) {
     constexpr int VE = Elem<T>::kVec;
     constexpr int RPW = 64 / LPR;
     constexpr int WAVES = 4;
+    constexpr int64_t E = (int64_t)sizeof(T);
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // The pipelined loop builds its buffer resource from the wave's first
+    // row, so it needs the wave index in a scalar register; the burst loop
+    // measured 2-3% faster (fp16, 256 vectors) with the plain index.
+    const int wave = PIPE ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : (int)(threadIdx.x >> 6);
     const int g = lane / LPR;
     const int j = lane % LPR;
     const int64_t step = (int64_t)gridDim.x * WAVES * RPW;
+    // Rows of one wave may differ in alignment by one body vector: N / VE
+    // bounds every row's count, and the masked last batch covers the
+    // difference.
+    const int64_t trips = batches<(int64_t)U * LPR>(N / VE);
     for (int64_t base = ((int64_t)blockIdx.x * WAVES + wave) * RPW; base < B; base += step) {
         const int64_t row = base + g;
         typename OUT::Row orow{};
@@ -142,7 +272,17 @@ __global__ __launch_bounds__(256) void lse_fwd_group_rows(const T* __restrict__ 
             for (int64_t h = j; h < sp.head; h += LPR) fold_scalar<T, ROBUST>(m, s, p + h);
             const T* tail = p + sp.head + sp.nvec * VE;
             for (int64_t t = j; t < sp.tail; t += LPR) fold_scalar<T, ROBUST>(m, s, tail + t);
-            fold_body<T, ROBUST, LPR, U>(m, s, p + sp.head, j, sp.nvec);
+            // The loads address the wave's rows [base, base + RPW) through one
+            // resource at row `base`; a lane's offset within them stays below
+            // RPW * N * E, which the launcher keeps under 2^31 (rows of at
+            // most 4096 vectors).
+            const int64_t rows = B - base < RPW ? B - base : RPW;
+            const int lane_off = (int)(((int64_t)g * N + sp.head) * E) + j * 16;
+            if constexpr (PIPE)
+                fold_body<T, ROBUST, LPR, U>(m, s, reinterpret_cast<const char*>(x + base * N), rows * N * E, lane_off,
+                                             j, sp.nvec, trips);
+            else
+                fold_body_burst<T, ROBUST, LPR, U>(m, s, p + sp.head, j, sp.nvec);
         }
         group_merge<LPR>(m, s);
         if (j == 0 && row < B) out.end(row, orow, lse_finish<ROBUST>(m, s));
@@ -180,7 +320,8 @@ __global__ __launch_bounds__(THREADS) void lse_fwd_split_partials(const T* __res
     }
     const int64_t v0 = (int64_t)k * seg;
     const int64_t v1 = v0 + seg < sp.nvec ? v0 + seg : sp.nvec;
-    fold_body<T, ROBUST, THREADS, U>(m, s, p + sp.head, v0 + tid, v1);
+    fold_body<T, ROBUST, THREADS, U>(m, s, reinterpret_cast<const char*>(p + sp.head + v0 * VE), (v1 - v0) * 16, tid * 16,
+                                     tid, v1 - v0, batches<(int64_t)U * THREADS>(v1 - v0));
     group_merge<64>(m, s);
     if ((tid & 63) == 0) {
         sh_m[tid >> 6] = m;
@@ -281,38 +422,87 @@ static int64_t pow2_ceil(int64_t v) {
     return p;
 }
 
+template <typename T, bool ROBUST, int LPR, int U, bool PIPE, typename OUT>
+static void launch_group(const T* x, OUT out, int64_t B, int64_t N, hipStream_t st) {
+    const int64_t rows_per_block = 4 * (64 / LPR);
+    int64_t grid = (B + rows_per_block - 1) / rows_per_block;
+    if (grid > (int64_t)1 << 30) grid = (int64_t)1 << 30;
+    lse_fwd_group_rows<T, ROBUST, LPR, U, PIPE, OUT><<<dim3((unsigned)grid), dim3(256), 0, st>>>(x, out, B, N);
+}
+
+template <typename T, bool ROBUST, int THREADS, int U, bool PIPE, typename OUT>
+static void launch_block(const T* x, OUT out, int64_t B, int64_t N, hipStream_t st) {
+    const int64_t grid = B < ((int64_t)1 << 30) ? B : ((int64_t)1 << 30);
+    lse_fwd_block_rows<T, ROBUST, THREADS, U, PIPE, OUT><<<dim3((unsigned)grid), dim3(THREADS), 0, st>>>(x, out, B, N);
+}
+
+// Geometry and loop per shape ("vectors" = 16-byte vectors per row), from
+// same-process sweeps of both loops over 256..1024-thread blocks and 4..64
+// lanes per row on MI355X.  The pipelined loop wins wherever a row is more
+// than a few hundred vectors long: for fp16 / bf16, whose fold costs twice
+// the ALU work per byte, by 3-10% on many rows and by up to 39% on few
+// mid-length rows.  Short rows keep the burst loop, 2-10% ahead there.
 template <typename T, bool ROBUST, typename OUT>
 static void launch_fwd(const T* x, OUT out, int64_t B, int64_t N, hipStream_t st) {
     constexpr int VE = Elem<T>::kVec;
+    constexpr bool kHalf = VE == 8;
     const int64_t vecs = (N + VE - 1) / VE;
     if (vecs > 4096) {
-        // one 512-thread block per row, two 16-byte loads per lane per fold:
-        // measured best at (512, 128256) among 256..1024 threads x 1..8 loads
-        int64_t grid = B < ((int64_t)1 << 30) ? B : ((int64_t)1 << 30);
-        lse_fwd_block_rows<T, ROBUST, 512, 2, OUT><<<dim3((unsigned)grid), dim3(512), 0, st>>>(x, out, B, N);
+        // Long rows, one block per row.  fp16/bf16: 512 threads x 4 loads per
+        // batch (1-1.5% ahead of x 2 at (2048, 128256)).  fp32: about 32 KB
+        // of loads in flight per CU streams best, so the block shrinks as
+        // more rows share a CU: 512 x 2 below 512 rows (22% ahead of the
+        // burst loop at 256 rows), 256 x 2 up to 2048 (0.8% ahead at
+        // (512, 128256)), 1024 x 1 above (1.6% ahead at (8184, 32000)).
+        if constexpr (kHalf)
+            launch_block<T, ROBUST, 512, 4, true, OUT>(x, out, B, N, st);
+        else if (B < 512)
+            launch_block<T, ROBUST, 512, 2, true, OUT>(x, out, B, N, st);
+        else if (B < 2048)
+            launch_block<T, ROBUST, 256, 2, true, OUT>(x, out, B, N, st);
+        else
+            launch_block<T, ROBUST, 1024, 1, true, OUT>(x, out, B, N, st);
         return;
     }
     if (vecs > 1024 && B <= 1024) {
-        // few mid-length rows: one wave per row leaves the GPU under-filled;
-        // a 256-thread block per row measured 13-37% faster for B <= 1024 and
-        // 1125..4000 vectors (fp16, N = 9000..32000), and within 2% above
-        const int64_t grid = B;
-        lse_fwd_block_rows<T, ROBUST, 256, 2, OUT><<<dim3((unsigned)grid), dim3(256), 0, st>>>(x, out, B, N);
+        // Few mid-length rows: a wave per row would leave the GPU
+        // under-filled, so one block per row; 128 threads for fp16/bf16 up
+        // to 2048 vectors (2-8% ahead of 256), 256 otherwise.
+        if (kHalf && vecs <= 2048)
+            launch_block<T, ROBUST, 128, 2, true, OUT>(x, out, B, N, st);
+        else
+            launch_block<T, ROBUST, 256, 2, true, OUT>(x, out, B, N, st);
         return;
     }
+    if (vecs > 512) {
+        // Many mid-length rows: fp32 takes a 256-thread block per row (4%
+        // ahead of a wave per row at 1024 vectors, 2% at 4000); fp16/bf16 a
+        // wave per row in batches of 4, or 32 lanes per row for 1025..2048
+        // vectors (3% ahead at 2000).
+        if constexpr (!kHalf)
+            launch_block<T, ROBUST, 256, 2, true, OUT>(x, out, B, N, st);
+        else if (vecs > 1024 && vecs <= 2048)
+            launch_group<T, ROBUST, 32, 4, true, OUT>(x, out, B, N, st);
+        else
+            launch_group<T, ROBUST, 64, 4, true, OUT>(x, out, B, N, st);
+        return;
+    }
+    if (vecs < 16) {
+        // a few vectors per row: 4 lanes per row, one masked batch of 2
+        // (22% ahead of the burst loop at 8 vectors)
+        launch_group<T, ROBUST, 4, 2, true, OUT>(x, out, B, N, st);
+        return;
+    }
+    // Short rows: LPR lanes per row, about 4 vectors per lane in one burst.
     int64_t lpr = pow2_ceil((vecs + 3) / 4);
     if (lpr < 4) lpr = 4;
     if (lpr > 64) lpr = 64;
-    const int64_t rows_per_block = 4 * (64 / lpr);
-    int64_t grid = (B + rows_per_block - 1) / rows_per_block;
-    if (grid > (int64_t)1 << 30) grid = (int64_t)1 << 30;
-    const dim3 g((unsigned)grid), blk(256);
     switch (lpr) {
-    case 4: lse_fwd_group_rows<T, ROBUST, 4, 4, OUT><<<g, blk, 0, st>>>(x, out, B, N); break;
-    case 8: lse_fwd_group_rows<T, ROBUST, 8, 4, OUT><<<g, blk, 0, st>>>(x, out, B, N); break;
-    case 16: lse_fwd_group_rows<T, ROBUST, 16, 4, OUT><<<g, blk, 0, st>>>(x, out, B, N); break;
-    case 32: lse_fwd_group_rows<T, ROBUST, 32, 4, OUT><<<g, blk, 0, st>>>(x, out, B, N); break;
-    default: lse_fwd_group_rows<T, ROBUST, 64, 4, OUT><<<g, blk, 0, st>>>(x, out, B, N); break;
+    case 4: launch_group<T, ROBUST, 4, 4, false, OUT>(x, out, B, N, st); break;
+    case 8: launch_group<T, ROBUST, 8, 4, false, OUT>(x, out, B, N, st); break;
+    case 16: launch_group<T, ROBUST, 16, 4, false, OUT>(x, out, B, N, st); break;
+    case 32: launch_group<T, ROBUST, 32, 4, false, OUT>(x, out, B, N, st); break;
+    default: launch_group<T, ROBUST, 64, 4, false, OUT>(x, out, B, N, st); break;
     }
 }
 

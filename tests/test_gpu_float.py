@@ -320,7 +320,7 @@ def test_fwd_half_robust_special_values(cuda, dtype, N):
 @pytest.mark.parametrize("B,N,off", [(3, 9000, 0), (1024, 16000, 0), (77, 32000, 3), (5, 8193, 1)])
 def test_fwd_mid_rows_block_geometry(cuda, dtype, B, N, off):
     """Few mid-length rows (1024 < vectors <= 4096, B <= 1024) take one
-    256-thread block per row; parity with fp64 at the tolerance of the dtype,
+    128- or 256-thread block per row; parity with fp64 at the tolerance of the dtype,
     robust and plain, aligned and offset rows."""
     print(f"case fwd_mid {dtype} B={B} N={N} off={off}", flush=True)
     rng = np.random.default_rng(B + N + off)
@@ -338,3 +338,64 @@ def test_fwd_mid_rows_block_geometry(cuda, dtype, B, N, off):
             got = fn(xd, robust=robust)
             tol = RTOL16
         _close(got.cpu().numpy(), want, tol, atol=1e-6)
+
+
+# (dtype, label, B, vectors per row, batch size in vectors or None for the
+# burst loop) for each branch of the forward launcher: long rows (fp16/bf16
+# 512 x 4; fp32 512 x 2 / 256 x 2 / 1024 x 1 by row count), few mid-length
+# rows (128- / 256-thread blocks), many mid-length rows (fp32 256-thread
+# blocks, fp16/bf16 32 or 64 lanes per row in batches of 4), rows of a few
+# vectors (4 lanes, one masked batch of 2), short rows (burst loop).
+_F32, _F16, _BF16 = torch.float32, torch.float16, torch.bfloat16
+GEOMETRIES = [
+    (_F32, "long-blk512x2", 300, 5120, 1024),
+    (_F32, "long-blk256x2", 600, 5120, 512),
+    (_F32, "long-blk1024x1", 2048, 4608, 1024),
+    (_F32, "mid-blk256x2", 33, 1536, 512),
+    (_F32, "many-blk256x2", 1100, 1025, 512),
+    (_F32, "tiny-grp4x2", 37, 8, 8),
+    (_F32, "short-burst", 37, 257, None),
+]
+for _h in (_F16, _BF16):
+    GEOMETRIES += [
+        (_h, "long-blk512x4", 9, 5120, 2048),
+        (_h, "mid-blk128x2", 33, 1536, 256),
+        (_h, "mid-blk256x2", 33, 4096, 512),
+        (_h, "many-grp32x4", 1100, 1536, 128),
+        (_h, "many-grp64x4", 1100, 1025, 256),
+        (_h, "tiny-grp4x2", 37, 8, 8),
+        (_h, "short-burst", 37, 257, None),
+    ]
+
+
+@pytest.mark.parametrize("dtype,label,B,vecs,step", GEOMETRIES)
+def test_fwd_pipelined_batch_boundaries(cuda, dtype, label, B, vecs, step):
+    """Rows that end exactly on, one vector short of, and past a batch
+    boundary of each geometry, with row lengths that are not a multiple of
+    the vector width (so rows of one wave start at different alignments and
+    the masked last batch holds 0 .. all of a lane's vectors), on aligned and
+    offset storage; robust and plain against fp64."""
+    ve = 16 // torch.empty((), dtype=dtype).element_size()
+    if step is None:
+        ns = [vecs * ve, vecs * ve - 1]
+    else:
+        k = max(1, vecs // step)
+        ns = sorted({vecs * ve, k * step * ve, k * step * ve - 1, (k * step + 1) * ve + 1, (k * step - 1) * ve + 3})
+    ext = _ext()
+    rng = np.random.default_rng(vecs + B)
+    for N in ns:
+        for off in (0, 1):
+            print(f"case fwd_batches {label} {dtype} B={B} N={N} off={off}", flush=True)
+            x32 = (rng.standard_normal((B, N)) * 2).astype(np.float32)
+            xt = torch.from_numpy(x32).to(dtype)
+            xd = _offset_view(xt, cuda, off)
+            want = O.lse_fp64(xt.double().numpy())
+            for robust in (False, True):
+                if dtype == torch.float32:
+                    got = (ext.onepass_lse_float_robust if robust else ext.onepass_lse_float)(xd)
+                    tol = RTOL32
+                else:
+                    fn = ext.batched_logsumexp_fp16 if dtype == torch.float16 else ext.batched_logsumexp_bf16
+                    got = fn(xd, robust=robust)
+                    tol = RTOL16
+                _close(got.cpu().numpy(), want, tol, atol=1e-6)
