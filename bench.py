@@ -499,7 +499,7 @@ def main():
         "roofline": {"bound": "hbm", "kernel": "lse_bwd_row_chunks<float, 1, LseGrad, true> (fused backward)",
                      "achieved": round(bwd_gbps, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                      "frac": round(bwd_gbps * 1e9 / HBM_PEAK, 4), "traffic": traffic},
-        "roofline_fwd": {"bound": "hbm", "kernel": "lse_fwd_block_rows<float, true, 512, 2, LseOut> (robust forward)",
+        "roofline_fwd": {"bound": "hbm", "kernel": "lse_fwd_block_rows<float, true, 256, 2, true, LseOut> (robust forward)",
                          "achieved": round(fwd_gbps, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                          "frac": round(fwd_gbps * 1e9 / HBM_PEAK, 4)},
         "cpu_baseline": cpu,

@@ -355,15 +355,20 @@ __global__ __launch_bounds__(256) void lse_fwd_split_merge(const float2* __restr
 }
 
 // The split is used for B < kSplitMaxRows and rows of more than 4096 body
-// vectors; S (<= 64) aims at kSplitBlocks blocks in all, with segments of at
-// least kSplitMinVecs vectors, rounded to whole folds of the block.  Measured
-// at N = 128256 fp32 (one-pass -> split): B=1 22.4 -> 6.4 us, B=64 24.8 ->
-// 10.1 us, B=256 28.3 -> 24.1 us; equal at B=384, one-pass ahead at B=511.
+// vectors, except for kOnePassRowsLo <= B <= kOnePassRowsHi: there
+// each CU holds at most one 512-thread block of the one-pass kernel, which
+// then streams without a partial second round of blocks and beats the split
+// plus its merge.  S (<= 64) aims at kSplitBlocks blocks in all, with
+// segments of at least kSplitMinVecs vectors, rounded to whole batches of the
+// block.  Measured at N = 128256 fp32 (one-pass / split, us): B=96 15.9 /
+// 11.9, 160 17.1 / 16.7, 192 18.1 / 19.1, 256 22.2 / 23.9, 288 30.4 / 27.0,
+// 320 31.1 / 31.1.
 constexpr int kSplitThreads = 256;
 constexpr int kSplitU = 2;
 constexpr int64_t kSplitMaxRows = 320;
 constexpr int64_t kSplitBlocks = 2048;
 constexpr int64_t kSplitMinVecs = 1024;
+constexpr int64_t kOnePassRowsLo = 192, kOnePassRowsHi = 256;
 
 struct SplitPlan {
     int64_t S, seg;
@@ -373,6 +378,7 @@ static SplitPlan split_plan(int64_t B, int64_t N, int64_t ve, int64_t max_rows, 
                             int64_t fold) {
     const int64_t vecs = (N + ve - 1) / ve;  // >= the body vectors of any alignment
     if (B <= 0 || B >= max_rows || B > 65535 || vecs <= 4096) return {1, 0};
+    if (B >= kOnePassRowsLo && B <= kOnePassRowsHi) return {1, 0};
     int64_t S = (blocks + B - 1) / B;
     if (S > 64) S = 64;
     if (S > vecs / min_vecs) S = vecs / min_vecs;
@@ -449,16 +455,16 @@ static void launch_fwd(const T* x, OUT out, int64_t B, int64_t N, hipStream_t st
     const int64_t vecs = (N + VE - 1) / VE;
     if (vecs > 4096) {
         // Long rows, one block per row.  fp16/bf16: 512 threads x 4 loads per
-        // batch (1-1.5% ahead of x 2 at (2048, 128256)).  fp32: about 32 KB
-        // of loads in flight per CU streams best, so the block shrinks as
-        // more rows share a CU: 512 x 2 below 512 rows (22% ahead of the
-        // burst loop at 256 rows), 256 x 2 up to 2048 (0.8% ahead at
-        // (512, 128256)), 1024 x 1 above (1.6% ahead at (8184, 32000)).
+        // batch (1-1.5% ahead of x 2 at (2048, 128256)).  fp32 by row count
+        // (N = 128256): 512 x 2 below 512 rows (22% ahead of the burst loop
+        // at 256), 256 x 2 below 768 (0.8% ahead at 512), 1024 x 1 from 768
+        // (best from 768 to 8184 rows, 1.5-4% ahead of 256 x 2 at 1024 and
+        // of the burst loop at (2046, 256128) and (8184, 50257)).
         if constexpr (kHalf)
             launch_block<T, ROBUST, 512, 4, true, OUT>(x, out, B, N, st);
         else if (B < 512)
             launch_block<T, ROBUST, 512, 2, true, OUT>(x, out, B, N, st);
-        else if (B < 2048)
+        else if (B < 768)
             launch_block<T, ROBUST, 256, 2, true, OUT>(x, out, B, N, st);
         else
             launch_block<T, ROBUST, 1024, 1, true, OUT>(x, out, B, N, st);

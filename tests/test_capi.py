@@ -64,6 +64,10 @@ def test_split_workspace_plan():
     assert ws(4096, 128256, 4) == 0
     assert ws(320, 128256, 4) == 0          # enough rows for one block per row
     assert ws(319, 128256, 4) > 0
+    assert ws(257, 128256, 4) > 0           # a partial second round of one-pass blocks
+    for B in (192, 200, 256):               # at most one one-pass block per CU
+        assert ws(B, 128256, 4) == 0, B
+    assert ws(191, 128256, 4) > 0
     assert ws(64, 16384, 4) == 0            # 4096 vectors: one-pass
     assert ws(64, 32768, 2) == 0            # 4096 half vectors
     assert ws(64, 128256, 3) == 0           # unsupported element size
