@@ -198,12 +198,50 @@ struct BlockLayout {
 // ---------------------------------------------------------------------------
 // Per-node reductions over one 256-column tile.
 // ---------------------------------------------------------------------------
+// The 16-byte column vectors of lane l (as Cols<true, PP>) from the row
+// segment starting at b0 (`row` points at it), through a buffer resource of
+// `rec` bytes: vectors past the range read as zeros, without a memory access,
+// and the load needs no branch.
+template <int PP>
+__device__ __forceinline__ void load_cols_buf(const float* row, int rec, int l, float (&v)[PP]) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(row), 0, rec, 0x00020000);
+#pragma unroll
+    for (int q = 0; q < PP / 4; ++q) {
+        const f32x4 t =
+            __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (256 * q + 4 * l) * 4, 0, kLoadStreamAux));
+        v[4 * q] = t.x;
+        v[4 * q + 1] = t.y;
+        v[4 * q + 2] = t.z;
+        v[4 * q + 3] = t.w;
+    }
+}
+
+// Bytes of a row from column b0 to the batch's end, clamped to a buffer range.
+__device__ __forceinline__ int cols_bytes(int64_t batch, int64_t b0) {
+    const int64_t left = (batch - b0) * 4;
+    return left > 0x7fffffff ? 0x7fffffff : (int)left;
+}
+
+// Loads the child rows of window edges j .. j + GS - 1 (edges at or past wn
+// are left for the fold to mask).  With VEC every load is issued: each edge's
+// row goes through a buffer resource built from its wave-uniform child id,
+// with an empty range for edges past wn and the range check covering the
+// batch's end, so no load sits behind a branch.  A load behind a branch left
+// the wait-count pass unable to count the loads in flight, and the fold of a
+// group then waited for the next group's loads as well.
 template <int GS, bool VEC, int PP>
 __device__ __forceinline__ void load_group(float (&v)[GS][PP], const EdgeMeta& ew, int j, int wn,
                                            const float* __restrict__ child, int64_t batch, int64_t b0, int l) {
+    if constexpr (VEC) {
+        const int rec = cols_bytes(batch, b0);
 #pragma unroll
-    for (int g = 0; g < GS; ++g)
-        if (j + g < wn) Cols<VEC, PP>::load(child + bcast64(ew.cid, j + g) * batch, b0, l, batch, v[g]);
+        for (int g = 0; g < GS; ++g)
+            load_cols_buf<PP>(child + bcast64(ew.cid, (j + g) & 63) * batch + b0, j + g < wn ? rec : 0, l, v[g]);
+    } else {
+#pragma unroll
+        for (int g = 0; g < GS; ++g)
+            if (j + g < wn) Cols<VEC, PP>::load(child + bcast64(ew.cid, j + g) * batch, b0, l, batch, v[g]);
+    }
 }
 
 template <int PP>
@@ -266,10 +304,12 @@ __device__ __forceinline__ void walk_edges(const LAYOUT& L, const DESC& d, const
         float va[GS][PP], vb[GS][PP];
         load_group<GS, VEC, PP>(va, ew, 0, wn, child, batch, b0, l);
         for (int gi = 0; gi < ng; gi += 2) {
-            if (gi + 1 < ng) load_group<GS, VEC, PP>(vb, ew, (gi + 1) * GS, wn, child, batch, b0, l);
+            // with VEC the prefetch is unconditional (a group past the window
+            // reads empty ranges), keeping every load outside a branch
+            if (VEC || gi + 1 < ng) load_group<GS, VEC, PP>(vb, ew, (gi + 1) * GS, wn, child, batch, b0, l);
             fold(va, gi * GS, wn, ew);
             if (gi + 1 >= ng) break;
-            if (gi + 2 < ng) load_group<GS, VEC, PP>(va, ew, (gi + 2) * GS, wn, child, batch, b0, l);
+            if (VEC || gi + 2 < ng) load_group<GS, VEC, PP>(va, ew, (gi + 2) * GS, wn, child, batch, b0, l);
             fold(vb, (gi + 1) * GS, wn, ew);
         }
     }
@@ -422,12 +462,24 @@ template <bool VEC>
 __device__ __forceinline__ void load_parents(float (&gv)[GB][PB], float (&ov)[GB][PB], const ParentMeta& pw, int j,
                                              int wn, const float* __restrict__ gout, const float* __restrict__ out,
                                              int64_t batch, int64_t b0, int l) {
+    if constexpr (VEC) {
+        // every load issued, as in load_group: parents past wn read empty ranges
+        const int rec = cols_bytes(batch, b0);
 #pragma unroll
-    for (int g = 0; g < GB; ++g) {
-        if (j + g < wn) {
-            const int64_t n = bcast64(pw.node, j + g);
-            Cols<VEC, PB>::load(gout + n * batch, b0, l, batch, gv[g]);
-            Cols<VEC, PB>::load(out + n * batch, b0, l, batch, ov[g]);
+        for (int g = 0; g < GB; ++g) {
+            const int64_t n = bcast64(pw.node, (j + g) & 63);
+            const int r = j + g < wn ? rec : 0;
+            load_cols_buf<PB>(gout + n * batch + b0, r, l, gv[g]);
+            load_cols_buf<PB>(out + n * batch + b0, r, l, ov[g]);
+        }
+    } else {
+#pragma unroll
+        for (int g = 0; g < GB; ++g) {
+            if (j + g < wn) {
+                const int64_t n = bcast64(pw.node, j + g);
+                Cols<VEC, PB>::load(gout + n * batch, b0, l, batch, gv[g]);
+                Cols<VEC, PB>::load(out + n * batch, b0, l, batch, ov[g]);
+            }
         }
     }
 }
@@ -450,7 +502,15 @@ __device__ __forceinline__ void flow_group(const float (&gv)[GB][PB], const floa
             }
             tsum = wave_sum(tsum);
             const int64_t e = bcast64(pw.edge, j + g);
-            if (l == 0) glogp[e] = first_tile ? tsum : glogp[e] + tsum;
+            // later tiles add without reading back, so no load sits in the
+            // edge loop; only this wave touches edge e, so the adds land in
+            // tile order and the result is deterministic
+            if (l == 0) {
+                if (first_tile)
+                    glogp[e] = tsum;
+                else
+                    __hip_atomic_fetch_add(glogp + e, tsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
     }
 }
@@ -470,7 +530,10 @@ __global__ __launch_bounds__(64 * WPB) void csr_bwd_kernel(const float* __restri
     const int64_t k = uniform64(csc_off[c + 1]) - p0;
     for (int64_t b0 = 0; b0 < batch; b0 += 64 * PB) {
         float cv[PB], acc[PB];
-        Cols<VEC, PB>::load(child + c * batch, b0, l, batch, cv);
+        if constexpr (VEC)
+            load_cols_buf<PB>(child + c * batch + b0, cols_bytes(batch, b0), l, cv);
+        else
+            Cols<VEC, PB>::load(child + c * batch, b0, l, batch, cv);
 #pragma unroll
         for (int i = 0; i < PB; ++i) acc[i] = 0.0f;
         for (int64_t w0 = 0; w0 < k; w0 += 64) {
@@ -487,7 +550,7 @@ __global__ __launch_bounds__(64 * WPB) void csr_bwd_kernel(const float* __restri
             for (; gi + 1 < ng; gi += 2) {
                 load_parents<VEC>(gb, ob, pw, (gi + 1) * GB, wn, gout, out, batch, b0, l);
                 flow_group<VEC>(ga, oa, pw, gi * GB, wn, cv, acc, b0 == 0, glogp, batch, b0, l);
-                if (gi + 2 < ng) load_parents<VEC>(ga, oa, pw, (gi + 2) * GB, wn, gout, out, batch, b0, l);
+                if (VEC || gi + 2 < ng) load_parents<VEC>(ga, oa, pw, (gi + 2) * GB, wn, gout, out, batch, b0, l);
                 flow_group<VEC>(gb, ob, pw, (gi + 1) * GB, wn, cv, acc, b0 == 0, glogp, batch, b0, l);
             }
             if (gi < ng) flow_group<VEC>(ga, oa, pw, gi * GB, wn, cv, acc, b0 == 0, glogp, batch, b0, l);

@@ -155,7 +155,7 @@ def _abs_terms(child, out, gout, off, cids, lp):
     return O.sparse_csr_bwd_fp64(child, out, np.abs(gout), off, cids, lp)
 
 
-@pytest.mark.parametrize("batch", [1, 7, 130, 512, 600])
+@pytest.mark.parametrize("batch", [1, 7, 130, 512, 600, 1100])
 @pytest.mark.parametrize("signed", [False, True])
 def test_csr_backward_matches_fp64(cuda, batch, signed):
     print(f"case csr_bwd batch={batch} signed={signed}", flush=True)
@@ -204,6 +204,16 @@ def test_csr_backward_deterministic_and_transpose(cuda):
     a = ext.sparse_csr_backward(ch, out, g, offd, cid, lpd, csc)
     for _ in range(3):
         b = ext.sparse_csr_backward(ch, out, g, offd, cid, lpd, csc)
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    # three 512-column tiles: the edge gradients of tiles 1 and 2 are added to
+    # tile 0's in tile order by the one wave that owns the edge
+    child3 = np.log(rng.random((500, 1100)) + 1e-12).astype(np.float32)
+    ch3 = torch.from_numpy(child3).to(cuda)
+    out3 = ext.sparse_csr_forward(ch3, offd, cid, lpd)
+    g3 = torch.rand(2000, 1100, device=cuda)
+    a = ext.sparse_csr_backward(ch3, out3, g3, offd, cid, lpd, csc)
+    for _ in range(3):
+        b = ext.sparse_csr_backward(ch3, out3, g3, offd, cid, lpd, csc)
         assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
 
 
