@@ -331,6 +331,75 @@ def sparse_forward_q16(node_mars, element_mars, params, nids, cids, pids, block_
     return _sparse_blocked(node_mars, element_mars, params, nids, cids, pids, block_size, True, params_are_log)
 
 
+def sparse_blocked_backward(node_flows, element_flows, node_mars, element_mars, params, param_flows, nids, cids, pids,
+                            block_size, params_are_log=False):
+    """Flows of the block-layout sum layer of sparse_forward_float (pyjuice's
+    layout, as the forward dispatcher passes it), in fp32, added in place:
+    for block j, position p < block_size and edge e, with n = nids[j] + p,
+    c = cids[j, e] and q = pids[j, e] + p,
+      term[b] = node_flows[n, b] * exp(lw_q + element_mars[c, b] - node_mars[n, b])
+    (lw_q = log max(params[q], 1e-45), or params[q] itself when
+    params_are_log; term = 0 where node_mars is -inf),
+      element_flows[c, b] += the terms of the edges into c,
+      param_flows[q]      += the terms of edge (j, p, e) summed over b.
+    node_mars must hold this layer's forward output.  The reference has no
+    sparse backward.  The layer is expanded to one CSR node per (block,
+    position) and run through fl_sparse_csr_bwd, whose transposed structure
+    names each edge's node_mars row directly, so node_mars and node_flows are
+    read in place.  param_flows is accumulated with index_add_, whose order is
+    not fixed where several edges share a parameter.  Returns None."""
+    _check(node_flows.is_cuda and element_flows.is_cuda and param_flows.is_cuda, "flows must be CUDA tensors")
+    for t, nm in ((node_flows, "node_flows"), (element_flows, "element_flows"), (param_flows, "param_flows")):
+        _check(t.dtype == torch.float32 and t.is_contiguous(), f"{nm} must be contiguous float32")
+    _check(tuple(node_flows.shape) == tuple(node_mars.shape), "node_flows must have node_mars's shape")
+    _check(tuple(element_flows.shape) == tuple(element_mars.shape), "element_flows must have element_mars's shape")
+    _check(param_flows.numel() == params.numel(), "param_flows must have params's size")
+    # the forward's layout checks
+    _check(node_mars.is_cuda and element_mars.is_cuda and params.is_cuda, "node_mars, element_mars, params must be CUDA")
+    _check(node_mars.dtype == torch.float32 and element_mars.dtype == torch.float32 and params.dtype == torch.float32,
+           "node_mars, element_mars and params must be float32")
+    _check(node_mars.dim() == 2 and element_mars.dim() == 2 and node_mars.size(1) == element_mars.size(1),
+           "node_mars and element_mars must be 2-D [nodes, batch] with the same batch")
+    _check(node_mars.is_contiguous() and element_mars.is_contiguous() and params.is_contiguous(),
+           "node_mars, element_mars and params must be contiguous")
+    for name, t in (("nids", nids), ("cids", cids), ("pids", pids)):
+        _check(t.is_cuda and t.dtype == torch.int64 and t.is_contiguous(), f"{name} must be a contiguous CUDA int64 tensor")
+    _check(cids.dim() == 2 and pids.shape == cids.shape and nids.dim() == 1 and nids.size(0) == cids.size(0),
+           "nids [nblocks], cids and pids [nblocks, num_edges] shapes disagree")
+    nb, ne = cids.shape
+    bs = int(block_size)
+    num_el, batch = element_mars.shape
+    nnz = nb * bs * ne
+    if nnz == 0 or batch == 0:
+        return None
+    _check(nnz < 2 ** 31 and num_el < 2 ** 31 and node_mars.size(0) < 2 ** 31,
+           "edges, element rows and node rows must each be < 2^31")
+    dev = cids.device
+    pos = torch.arange(bs, device=dev)
+    node_rows = (nids[:, None] + pos[None, :]).reshape(-1)                      # [nb * bs]
+    child_ids = cids[:, None, :].expand(nb, bs, ne).reshape(-1)                 # [nnz], edge (j, p, e)
+    q = (pids[:, None, :] + pos[None, :, None]).reshape(-1)                     # [nnz]
+    w = params.reshape(-1)[q]
+    logp = w if params_are_log else torch.log(torch.clamp_min(w, 1e-45))
+    logp = logp.contiguous()
+    order = torch.sort(child_ids, stable=True).indices
+    counts = torch.bincount(child_ids, minlength=num_el)
+    _check(counts.numel() == num_el, "cids hold ids >= element_mars rows")
+    csc_off = torch.zeros(num_el + 1, dtype=torch.int64, device=dev)
+    torch.cumsum(counts, 0, out=csc_off[1:])
+    csc_edge = order.to(torch.int32)
+    csc_node = node_rows[order // ne].to(torch.int32)
+    grad_el = torch.empty_like(element_mars)
+    grad_lp = torch.empty_like(logp)
+    with _on_device(element_mars):
+        _lib.call("fl_sparse_csr_bwd", element_mars.data_ptr(), node_mars.data_ptr(), node_flows.data_ptr(),
+                  logp.data_ptr(), csc_off.data_ptr(), csc_edge.data_ptr(), csc_node.data_ptr(), grad_el.data_ptr(),
+                  grad_lp.data_ptr(), num_el, batch, _stream(element_mars))
+    element_flows.add_(grad_el)
+    param_flows.view(-1).index_add_(0, q, grad_lp)
+    return None
+
+
 def sparse_csr_forward(child, offsets, child_ids, logparams, q16=False, out=None):
     """CSR sum layer: out[n, b] = LSE_{e in [offsets[n], offsets[n+1])}
     (logparams[e] + child[child_ids[e], b]); -inf for a node without edges.

@@ -198,6 +198,38 @@ def sparse_blocked_fp64(element_mars, params, nids, cids, pids, block_size, clam
     return np.array(rows, np.int64), np.array(vals)
 
 
+def sparse_blocked_bwd_fp64(node_flows, node_mars, element_mars, params, nids, cids, pids, block_size, clamp=1e-45,
+                            params_are_log=False):
+    """Flows of the block-layout sum layer in float64, by loops over blocks,
+    positions and edges: for block j, position p, edge e with n = nids[j]+p,
+    c = cids[j,e], q = pids[j,e]+p and lw = log max(params[q], clamp) (params[q]
+    when params_are_log): term[b] = node_flows[n,b] * exp(lw + em[c,b] -
+    node_mars[n,b]) (0 where node_mars is -inf).  Returns the increments
+    (element_flows [nelem, batch], param_flows [nparams]).  The reference has no
+    sparse backward; this is the derivative of its block-layout forward
+    (sparse_float_kernel.cu:40-105, pyjuice's element and parameter flows)."""
+    nf = np.asarray(node_flows, np.float64)
+    nm = np.asarray(node_mars, np.float64)
+    em = np.asarray(element_mars, np.float64)
+    params = np.asarray(params, np.float64).reshape(-1)
+    nb, ne = cids.shape
+    def_el = np.zeros_like(em)
+    def_par = np.zeros_like(params)
+    for j in range(nb):
+        for p in range(block_size):
+            n = int(nids[j]) + p
+            live = ~np.isneginf(nm[n])
+            for e in range(ne):
+                c = int(cids[j, e])
+                q = int(pids[j, e]) + p
+                lw = params[q] if params_are_log else np.log(max(params[q], clamp))
+                with np.errstate(invalid="ignore", over="ignore"):
+                    t = np.where(live, nf[n] * np.exp(lw + em[c] - np.where(live, nm[n], 0.0)), 0.0)
+                def_el[c] += t
+                def_par[q] += t.sum()
+    return def_el, def_par
+
+
 def sparse_csr_fp64(child, offsets, cids, logparam):
     """CSR gather-LSE in fp64: out[n, b] = LSE_{e in node n}(logparam[e] + child[cid[e], b])."""
     child = np.asarray(child, np.float64)

@@ -249,3 +249,65 @@ def test_csr_layer_autograd(cuda):
     np.testing.assert_allclose(y.detach().cpu().numpy(), yt.detach().numpy(), rtol=1e-5, atol=1e-5)
     for got, want in ((xd.grad, xt.grad), (l1d.grad, l1t.grad), (l2d.grad, l2t.grad)):
         np.testing.assert_allclose(got.cpu().numpy(), want.numpy(), rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("ne,bs,batch", [(5, 4, 32), (12, 2, 130), (30, 3, 512), (70, 1, 64), (9, 2, 600)])
+def test_blocked_backward_matches_fp64(cuda, ne, bs, batch):
+    """ext.sparse_blocked_backward: the flows of the block-layout layer added
+    into existing element and parameter flows, against the fp64 loops of the
+    oracle; also with params given as log-weights."""
+    print(f"case blocked_bwd ne={ne} bs={bs} batch={batch}", flush=True)
+    rng = np.random.default_rng(ne * bs + batch + 1)
+    nb, nelem, nparams = 7, 40, 600
+    nids, cids, pids, params, em = _blocked(rng, nb, ne, bs, batch, nelem, nparams)
+    cids[0, : min(3, ne)] = 2                    # a child repeated within a block
+    em[5, :] = -np.inf                           # a child of probability 0
+    ext = _ext()
+    for log_params in (False, True):
+        p_in = np.log(params).astype(np.float32) if log_params else params
+        nm = torch.zeros(nb * bs, batch, device=cuda)
+        d = {k: torch.from_numpy(v).to(cuda) for k, v in (("em", em), ("p", p_in), ("nids", nids), ("cids", cids),
+                                                          ("pids", pids))}
+        ext.sparse_forward_float(nm, d["em"], d["p"], d["nids"], d["cids"], d["pids"], bs, params_are_log=log_params)
+        nf = rng.standard_normal((nb * bs, batch)).astype(np.float32)
+        ef0 = rng.standard_normal((nelem, batch)).astype(np.float32)
+        pf0 = rng.standard_normal(nparams).astype(np.float32)
+        ef, pf = torch.from_numpy(ef0).to(cuda), torch.from_numpy(pf0).to(cuda)
+        ext.sparse_blocked_backward(torch.from_numpy(nf).to(cuda), ef, nm, d["em"], d["p"], pf, d["nids"], d["cids"],
+                                    d["pids"], bs, params_are_log=log_params)
+        nm64 = nm.cpu().numpy()
+        de, dp = O.sparse_blocked_bwd_fp64(nf, nm64, em, p_in, nids, cids, pids, bs, params_are_log=log_params)
+        ae, ap = O.sparse_blocked_bwd_fp64(np.abs(nf), nm64, em, p_in, nids, cids, pids, bs,
+                                           params_are_log=log_params)
+        got_e, got_p = ef.cpu().numpy(), pf.cpu().numpy()
+        # fp32 terms within 1e-5 of their magnitudes, plus the rounding of the final add
+        assert (np.abs(got_e - (ef0 + de)) <= 1e-5 * ae + 2e-7 * np.abs(ef0 + de) + 1e-30).all()
+        assert (np.abs(got_p - (pf0 + dp)) <= 1e-5 * ap + 2e-7 * np.abs(pf0 + dp) + 1e-30).all()
+        assert (got_e[5] == ef0[5]).all()        # no flow into a child of probability 0
+
+
+def test_blocked_backward_subset_of_blocks(cuda):
+    """The backward over a subset of node blocks (as the dispatcher selects
+    with local_ids) touches only those blocks' children and parameters."""
+    print("case blocked_bwd subset", flush=True)
+    rng = np.random.default_rng(77)
+    nb, ne, bs, batch, nelem, nparams = 6, 5, 2, 16, 30, 200
+    nids, cids, pids, params, em = _blocked(rng, nb, ne, bs, batch, nelem, nparams)
+    sel = np.array([1, 4])
+    ext = _ext()
+    nm = torch.zeros(nb * bs, batch, device=cuda)
+    d = {k: torch.from_numpy(v).to(cuda) for k, v in (("em", em), ("p", params), ("nids", nids[sel]),
+                                                      ("cids", cids[sel]), ("pids", pids[sel]))}
+    ext.sparse_forward_float(nm, d["em"], d["p"], d["nids"], d["cids"], d["pids"], bs)
+    nf = rng.standard_normal((nb * bs, batch)).astype(np.float32)
+    ef = torch.zeros(nelem, batch, device=cuda)
+    pf = torch.zeros(nparams, device=cuda)
+    ext.sparse_blocked_backward(torch.from_numpy(nf).to(cuda), ef, nm, d["em"], d["p"], pf, d["nids"], d["cids"],
+                                d["pids"], bs)
+    de, dp = O.sparse_blocked_bwd_fp64(nf, nm.cpu().numpy(), em, params, nids[sel], cids[sel], pids[sel], bs)
+    ae, ap = O.sparse_blocked_bwd_fp64(np.abs(nf), nm.cpu().numpy(), em, params, nids[sel], cids[sel], pids[sel], bs)
+    got_e, got_p = ef.cpu().numpy(), pf.cpu().numpy()
+    assert (np.abs(got_e - de) <= 1e-5 * ae + 1e-30).all()
+    assert (np.abs(got_p - dp) <= 1e-5 * ap + 1e-30).all()
+    untouched = np.setdiff1d(np.arange(nelem), cids[sel].reshape(-1))
+    assert (got_e[untouched] == 0).all()

@@ -615,3 +615,49 @@ def test_cpu_torch_wrapper_dispatch():
     torch.testing.assert_close(O.logsumexp_intlse_torch(x, 0), torch.logsumexp(x, 0))
     torch.testing.assert_close(O.logsumexp_intlse_torch(x[:, :1], -1), torch.logsumexp(x[:, :1], -1))
     assert isinstance(O.logsumexp_intlse_torch(torch.randn(30), -1), torch.Tensor)
+
+
+def test_sparse_blocked_bwd_fp64_against_csr_expansion_and_autograd():
+    """The block-layout flows equal the CSR flows of the layer expanded to one
+    node per (block, position), and torch fp64 autograd of the block-layout
+    forward written with gather + logsumexp."""
+    import torch
+
+    rng = np.random.default_rng(41)
+    nb, ne, bs, batch, nel, npar = 3, 4, 2, 5, 6, 20
+    nids = np.array([0, 2, 4], np.int64)
+    cids = rng.integers(0, nel, (nb, ne)).astype(np.int64)
+    cids[0, :2] = 1                                  # repeated child in one block
+    pids = rng.integers(0, npar - bs, (nb, ne)).astype(np.int64)
+    params = rng.random(npar) + 1e-3
+    em = np.log(rng.random((nel, batch)))
+    em[2, 1] = -np.inf
+    rows, vals = O.sparse_blocked_fp64(em, params, nids, cids, pids, bs)
+    nm = np.zeros((nb * bs, batch))
+    nm[rows] = vals
+    nf = rng.standard_normal(nm.shape)
+    de, dp = O.sparse_blocked_bwd_fp64(nf, nm, em, params, nids, cids, pids, bs)
+    # CSR expansion: node (j, p) -> row nids[j] + p, edges e in order
+    off = np.arange(nb * bs + 1, dtype=np.int64) * ne
+    cid = np.repeat(cids[:, None, :], bs, axis=1).reshape(-1)
+    q = (pids[:, None, :] + np.arange(bs)[None, :, None]).reshape(-1)
+    lw = np.log(np.maximum(params[q], 1e-45))
+    order_rows = (nids[:, None] + np.arange(bs)[None, :]).reshape(-1)
+    gc, gl = O.sparse_csr_bwd_fp64(em, nm[order_rows], nf[order_rows], off, cid, lw)
+    np.testing.assert_allclose(de, gc, rtol=1e-12, atol=1e-14)
+    want_p = np.zeros(npar)
+    np.add.at(want_p, q, gl)
+    np.testing.assert_allclose(dp, want_p, rtol=1e-12, atol=1e-14)
+    # torch autograd of the forward: d(sum nf * out) / d em and d / d params
+    et = torch.from_numpy(np.where(np.isneginf(em), -1e300, em)).requires_grad_(True)
+    pt = torch.from_numpy(params).requires_grad_(True)
+    loss = 0.0
+    for j in range(nb):
+        for p in range(bs):
+            lwt = torch.log(pt[torch.from_numpy(pids[j] + p)])
+            y = torch.logsumexp(lwt[:, None] + et[torch.from_numpy(cids[j])], dim=0)
+            loss = loss + (y * torch.from_numpy(nf[nids[j] + p])).sum()
+    loss.backward()
+    np.testing.assert_allclose(de, et.grad.numpy(), rtol=1e-12, atol=1e-14)
+    # param flows are d loss / d log w = w * d loss / d w
+    np.testing.assert_allclose(dp, params * pt.grad.numpy(), rtol=1e-12, atol=1e-14)
