@@ -55,8 +55,12 @@ def cpu_baseline(max_rows=512):
     """FuseLSE-CPU forward (sequential expf/log1pf pair chain per row, rows over
     OpenMP) plus the backward formula, the repo's C port, on the host cores:
     median of 5 timed calls after 2 warm-ups (the reference's CPU protocol,
-    benchmark.py:36-44).  Also times torch.logsumexp fwd+bwd on CPU and, when
-    it was built, the reference's own AVX2 IntLSE (single thread, 32 rows)."""
+    benchmark.py:36-44), at all cores.  Also reports: the port and
+    torch.logsumexp fwd+bwd at 1 thread (64-row sample, scaled); the C1 shapes
+    (32, 256) and (200, 1000) forward at 1 thread and all cores; torch's
+    fwd+bwd at all cores; when it was built, the reference's own AVX2 IntLSE
+    (single thread as in the reference, 32 rows, also scaled to B); the
+    affinity core count and the CPU model."""
     import numpy as np
     import torch
 
@@ -84,7 +88,42 @@ def cpu_baseline(max_rows=512):
 
     cores = O.omp_threads()
     port_ms = med(fb) * (B / rows)
-    extra = {}
+    extra = {"affinity_cores": len(os.sched_getaffinity(0))}
+    # 1 thread (the reference's README protocol) on a 64-row sample, scaled
+    xs, gs = x[:64], g[:64]
+    O.set_omp_threads(1)
+    try:
+        extra["fuselse_port_1thread_fwd_bwd_ms"] = round(
+            med(lambda: O.lse_backward_rows(gs, xs, O.fuselse_cpu_rows(xs))) * (B / 64), 3)
+        # C1 (32, 256) and (200, 1000), N(0, 1): forward per call, 1 thread and all cores
+        c1 = {}
+        for cb, cn in ((32, 256), (200, 1000)):
+            xc = np.random.default_rng(0).standard_normal((cb, cn), dtype=np.float32)
+            reps = 20
+
+            def port_c1():
+                for _ in range(reps):
+                    O.fuselse_cpu_rows(xc)
+
+            O.set_omp_threads(1)
+            one = med(port_c1) * 1e3 / reps
+            O.set_omp_threads(cores)
+            allc = med(port_c1) * 1e3 / reps
+            tc = torch.from_numpy(xc)
+
+            def torch_c1():
+                for _ in range(reps):
+                    torch.logsumexp(tc, -1)
+
+            torch.set_num_threads(1)
+            t_one = med(torch_c1) * 1e3 / reps
+            torch.set_num_threads(cores)
+            t_all = med(torch_c1) * 1e3 / reps
+            c1[f"{cb}x{cn}"] = {"port_1thread_us": round(one, 2), f"port_{cores}threads_us": round(allc, 2),
+                                "torch_1thread_us": round(t_one, 2), f"torch_{cores}threads_us": round(t_all, 2)}
+        extra["c1_fwd"] = c1
+    finally:
+        O.set_omp_threads(cores)
     try:
         torch.set_num_threads(cores)
         xt = torch.from_numpy(x).requires_grad_(True)
@@ -95,11 +134,23 @@ def cpu_baseline(max_rows=512):
             torch.logsumexp(xt, -1).backward(gt)
 
         extra["torch_cpu_fwd_bwd_ms"] = round(med(tfb, 1, 3) * (B / rows), 3)
+        torch.set_num_threads(1)
+        xt1 = torch.from_numpy(xs).requires_grad_(True)
+        gt1 = torch.from_numpy(gs)
+
+        def tfb1():
+            xt1.grad = None
+            torch.logsumexp(xt1, -1).backward(gt1)
+
+        extra["torch_cpu_1thread_fwd_bwd_ms"] = round(med(tfb1, 1, 3) * (B / 64), 3)
+        torch.set_num_threads(cores)
     except Exception as e:  # pragma: no cover - reported, not fatal
         extra["torch_cpu_error"] = repr(e)
     if O.ref_available():
-        xs = np.ascontiguousarray(x[:32])
-        extra["intlse_avx2_ref_fwd_ms_1thread_32rows"] = round(med(lambda: O.ref_intlse_cpu_rows(xs, True), 1, 3), 3)
+        x32 = np.ascontiguousarray(x[:32])
+        t32 = med(lambda: O.ref_intlse_cpu_rows(x32, True), 1, 3)
+        extra["intlse_avx2_ref_fwd_ms_1thread_32rows"] = round(t32, 3)
+        extra["intlse_avx2_ref_fwd_ms_1thread_scaled_to_B"] = round(t32 * B / 32, 3)
     cpu = ""
     try:
         for ln in open("/proc/cpuinfo"):

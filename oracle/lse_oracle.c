@@ -456,6 +456,15 @@ void or_lse_backward_rows(const float* g, const float* x, const float* lse, int6
         for (int64_t i = 0; i < N; i++) gx[b * N + i] = g[b] * expf(x[b * N + i] - lse[b]);
 }
 
+void or_omp_set_threads(int n) {
+#ifdef _OPENMP
+    extern void omp_set_num_threads(int);
+    omp_set_num_threads(n > 0 ? n : 1);
+#else
+    (void)n;
+#endif
+}
+
 int or_omp_max_threads(void) {
 #ifdef _OPENMP
     extern int omp_get_max_threads(void);

@@ -76,6 +76,8 @@ def lib():
         L.or_fuselse_cpu_rows.argtypes = [_f32p, _i64, _i64, _f32p]
         L.or_lse_backward_rows.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _f32p]
         L.or_omp_max_threads.restype = ctypes.c_int
+        L.or_omp_set_threads.argtypes = [ctypes.c_int]
+        L.or_omp_set_threads.restype = None
         _lib = L
     return _lib
 
@@ -391,6 +393,11 @@ def lse_backward_rows(g, x, lse):
 
 def omp_threads() -> int:
     return lib().or_omp_max_threads()
+
+
+def set_omp_threads(n: int) -> None:
+    """Threads of the C port's OpenMP loops (the CPU baseline's 1-thread runs)."""
+    lib().or_omp_set_threads(int(n))
 
 
 # ----------------------------------------------------------------------------
