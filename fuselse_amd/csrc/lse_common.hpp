@@ -120,15 +120,31 @@ __device__ __forceinline__ float lse_finish(float m, float s) {
 }
 
 // Merge (m, s) across aligned groups of W lanes; every lane of a group ends
-// with the group result.
+// with the group result.  Two phases: a butterfly max, one rescale of each
+// lane's sum to the group max, a butterfly sum.  This equals the tree of
+// pairwise lse_merge steps up to rounding (the rescale factors compose, and
+// lse_rescale keeps -inf partials at 0 and base(+inf) = 0 as each pairwise
+// step would), with a dependent chain of cheap max and add steps and one
+// exponential instead of two exponentials per level; the end-of-row merge is
+// on the critical path of every block.
 template <int W>
 __device__ __forceinline__ void group_merge(float& m, float& s) {
-    if constexpr (W >= 2) { lse_merge(m, s, reduce_partner<1>(m), reduce_partner<1>(s)); }
-    if constexpr (W >= 4) { lse_merge(m, s, reduce_partner<2>(m), reduce_partner<2>(s)); }
-    if constexpr (W >= 8) { lse_merge(m, s, reduce_partner<4>(m), reduce_partner<4>(s)); }
-    if constexpr (W >= 16) { lse_merge(m, s, reduce_partner<8>(m), reduce_partner<8>(s)); }
-    if constexpr (W >= 32) { lse_merge(m, s, reduce_partner<16>(m), reduce_partner<16>(s)); }
-    if constexpr (W >= 64) { lse_merge(m, s, reduce_partner<32>(m), reduce_partner<32>(s)); }
+    float mm = m;
+    if constexpr (W >= 2) mm = fmaxf(mm, reduce_partner<1>(mm));
+    if constexpr (W >= 4) mm = fmaxf(mm, reduce_partner<2>(mm));
+    if constexpr (W >= 8) mm = fmaxf(mm, reduce_partner<4>(mm));
+    if constexpr (W >= 16) mm = fmaxf(mm, reduce_partner<8>(mm));
+    if constexpr (W >= 32) mm = fmaxf(mm, reduce_partner<16>(mm));
+    if constexpr (W >= 64) mm = fmaxf(mm, reduce_partner<32>(mm));
+    float ss = s * lse_rescale(m, mm);
+    if constexpr (W >= 2) ss += reduce_partner<1>(ss);
+    if constexpr (W >= 4) ss += reduce_partner<2>(ss);
+    if constexpr (W >= 8) ss += reduce_partner<4>(ss);
+    if constexpr (W >= 16) ss += reduce_partner<8>(ss);
+    if constexpr (W >= 32) ss += reduce_partner<16>(ss);
+    if constexpr (W >= 64) ss += reduce_partner<32>(ss);
+    m = mm;
+    s = ss;
 }
 
 // ---------------------------------------------------------------------------
