@@ -2,12 +2,16 @@
 // robust) and the fused fp32 backward.
 //
 // Forward: a single pass over HBM.  Each lane keeps an online (max, scaled
-// sum) pair and folds one 16-byte vector group at a time with a single
-// rescale, so the steady state costs one v_exp_f32 per element.  Lanes merge
-// through DPP / swizzle exchanges and waves through LDS.  Three geometries:
+// sum) pair and folds a batch of 16-byte vectors at a time with a single
+// rescale, so the steady state costs one v_exp_f32 per element.  Two loops:
+// a software-pipelined one (the next batch's loads in flight while a batch
+// folds; masked last batch) and a burst one (short rows).  Lanes merge
+// through DPP / swizzle exchanges and waves through LDS.  Three geometries
+// (launch_fwd picks geometry and loop per shape):
 //   * group rows  : LPR lanes per row (4..64), 64/LPR rows per wave, for rows
-//                   of up to a few thousand vectors;
-//   * block rows  : one 256..1024-thread block per row for long rows;
+//                   of up to 4096 vectors;
+//   * block rows  : one 128..1024-thread block per row for longer rows and
+//                   for few mid-length rows;
 //   * split rows  : S blocks per row for few long rows, then a merge kernel
 //                   (partials in a caller workspace);
 // Backward: grad * exp2((x - lse) * log2 e), 16-byte loads and stores (fp32,
