@@ -81,11 +81,17 @@ def load():
     return lib
 
 
+_bound = {}
+
+
 def call(name: str, *args) -> None:
     """Call entry point `name`; a nonzero status raises RuntimeError with the
-    library's message."""
-    lib = load()
-    rc = getattr(lib, name)(*args)
+    library's message.  Entry points are looked up once and kept, since the
+    Python side of a call is the floor of small launches."""
+    fn = _bound.get(name)
+    if fn is None:
+        fn = _bound[name] = getattr(load(), name)
+    rc = fn(*args)
     if rc != 0:
-        msg = lib.fl_last_error().decode(errors="replace")
+        msg = load().fl_last_error().decode(errors="replace")
         raise RuntimeError(msg or f"{name} failed with status {rc}")

@@ -9,8 +9,6 @@ reference's drop-in (fuselse/gpu/autograd.py:6-61).
 
 from __future__ import annotations
 
-import contextlib
-
 import torch
 
 from . import _lib
@@ -21,7 +19,16 @@ def _check(cond: bool, msg: str) -> None:
         raise RuntimeError(msg)
 
 
+# torch's raw current-stream query (what its own compiled kernels use) costs
+# a fraction of building a torch.cuda.Stream object; the public form is the
+# fallback.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(t: torch.Tensor):
+    if _raw_stream is not None:
+        idx = t.device.index
+        return _raw_stream(torch.cuda.current_device() if idx is None else idx)
     return ctypes_stream(torch.cuda.current_stream(t.device))
 
 
@@ -29,14 +36,25 @@ def ctypes_stream(s) -> int:
     return s.cuda_stream
 
 
-@contextlib.contextmanager
+class _Same:
+    """The no-op device guard (the tensor is on the current device)."""
+
+    def __enter__(self):
+        return None
+
+    def __exit__(self, *exc):
+        return False
+
+
+_SAME = _Same()
+
+
 def _on_device(t: torch.Tensor):
+    """A guard that makes t's device current for the enclosed launch."""
     idx = t.device.index
     if idx is None or idx == torch.cuda.current_device():
-        yield
-    else:
-        with torch.cuda.device(idx):
-            yield
+        return _SAME
+    return torch.cuda.device(idx)
 
 
 def _launch_fwd(entry: str, x: torch.Tensor, out: torch.Tensor, elem_bytes: int, robust: bool) -> None:
