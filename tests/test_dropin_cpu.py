@@ -263,3 +263,23 @@ def test_sparse_dispatcher_local_ids_and_fallback():
     assert fb == ["MPE"] and len(calls) == 2
     with pytest.raises(NotImplementedError):
         make_sparse_dispatcher(ext_call)(Layer(), None, None, None, nids, cids, pids, propagation_alg="GeneralLL")
+
+
+def test_reference_edge_cases_of_the_dispatch():
+    """The reference's dispatch (autograd.py:37-43) evaluates dim >= 0 first and
+    shape[-1] last, so: a tuple dim raises TypeError on any input, a 0-d CUDA
+    fp32 tensor raises IndexError at shape[-1], a 0-d CPU tensor falls back to
+    torch, and dim defaults to the last axis."""
+    ext = FakeExt()
+    lse = make_fuselse_logsumexp(ext)
+    with pytest.raises(TypeError):
+        lse(fake(torch.randn(3, 4)), dim=(0, 1))
+    with pytest.raises(TypeError):
+        lse(torch.randn(3, 4), dim=(0, 1))
+    with pytest.raises(IndexError):
+        lse(fake(torch.tensor(1.5)))
+    y = lse(torch.tensor(1.5))
+    torch.testing.assert_close(y, torch.logsumexp(torch.tensor(1.5), dim=-1))
+    out = lse(fake(torch.randn(3, 4)))
+    assert ext.calls and ext.calls[-1][0] == "fwd_robust" and tuple(out.shape) == (3,)
+    assert not hasattr(lse, "out")
