@@ -363,7 +363,47 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
                          1, max(5, iters // 5))
         bbytes = 2 * nnz * batch * 4 + nnz * (4 + 4 + 4 + 4) + (nodes + 1) * 8 + 2 * nodes * batch * 4
         rec("C5_sparse_csr_bwd_fp32_1M_nodes_b512", ms, bbytes, nnz=nnz, alpha=2.0)
-        del child, out, gout
+        del child, out, gout, csc
+    if want("C5"):
+        # pyjuice's block layout (the reference's own sparse entry points,
+        # experiment_pyjuice/sparse_float_kernel.cu:110-167): 8192 node blocks
+        # of 32 nodes, 32 edges per block (a latent-32 HCLT-like sum layer),
+        # 262144 element rows, batch 512.  Bytes counted: each block's 32 child
+        # rows read once (its 32 nodes share them), every node row written once,
+        # the edge metadata.
+        nbk, bs, ne, nel, batch = 8192, 32, 32, 262144, 512
+        em = torch.log(torch.rand(nel, batch, device=dev, generator=gen).clamp_min_(1e-30))
+        nids = torch.arange(nbk, device=dev, dtype=torch.int64) * bs
+        cids = torch.randint(0, nel, (nbk, ne), device=dev, generator=gen, dtype=torch.int64)
+        pids = (torch.arange(nbk * ne, device=dev, dtype=torch.int64) * bs).reshape(nbk, ne)
+        params = torch.rand(nbk * ne * bs, device=dev, generator=gen) + 1e-3
+        nm = torch.empty(nbk * bs, batch, device=dev)
+        fbytes = nbk * ne * batch * 4 + nbk * bs * batch * 4 + nbk * ne * 16 + nbk * ne * bs * 4
+        for fn, tag in [(ext.sparse_forward_float, "fp32"), (ext.sparse_forward_q16, "q16")]:
+            ms = _time_calls(torch, stream, lambda i: fn(nm, em, params, nids, cids, pids, bs), 1, max(5, iters // 5))
+            rec(f"C5_blocked_{tag}_8192x32_e32_b512", ms, fbytes, nnz=nbk * bs * ne)
+        ext.sparse_forward_float(nm, em, params, nids, cids, pids, bs)
+        nf = torch.rand(nbk * bs, batch, device=dev, generator=gen)
+        ef = torch.zeros(nel, batch, device=dev)
+        pf = torch.zeros(params.numel(), device=dev)
+        plan = ext.sparse_blocked_transpose(nids, cids, pids, bs, nel)
+        t0 = time.perf_counter()
+        for _ in range(3):
+            ext.sparse_blocked_transpose(nids, cids, pids, bs, nel)
+        torch.cuda.synchronize()
+        plan_ms = (time.perf_counter() - t0) / 3 * 1e3
+        ms = _time_calls(torch, stream, lambda i: ext.sparse_blocked_backward(nf, ef, nm, em, params, pf, nids, cids,
+                                                                              pids, bs, plan=plan), 1, max(5, iters // 5))
+        ms_np = _time_calls(torch, stream, lambda i: ext.sparse_blocked_backward(nf, ef, nm, em, params, pf, nids, cids,
+                                                                                 pids, bs), 1, max(5, iters // 5))
+        # bytes of the flows kernel alone (the call adds the log-weight gather
+        # before it and element_flows.add_ / index_add_ after it): per expanded
+        # edge the parent's flow and mar rows and 16 B of edge data, per
+        # element row one read of element_mars and one write of its gradient
+        bbytes = 2 * nbk * bs * ne * batch * 4 + 2 * nel * batch * 4 + nbk * bs * ne * 16
+        rec("C5_blocked_bwd_fp32_8192x32_e32_b512", ms, bbytes, nnz=nbk * bs * ne,
+            without_plan_us=round(ms_np * 1e3, 1), plan_build_ms=round(plan_ms, 2))
+        del em, nm, nf, ef, pf, plan
     return res
 
 

@@ -31,6 +31,7 @@
 
 #include "../../include/fuselse_amd.h"
 #include "fl_status.hpp"
+#include "lse_blocked.hpp"
 #include "lse_common.hpp"
 
 namespace fl {
@@ -616,6 +617,11 @@ extern "C" int fl_sparse_blocked_fwd(float* node_mars, const float* element_mars
     FL_CHECK(node_mars && element_mars && params && nids && (num_edges == 0 || (cids && pids)),
              "%s: NULL pointer argument", name);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (!q16 && sparse::blocked_mfma_eligible(num_edges, block_size)) {
+        sparse::launch_blocked_mfma(node_mars, element_mars, params, nids, cids, pids, num_nblocks, num_edges,
+                                    block_size, batch, params_are_log != 0, st);
+        return launch_status(name);
+    }
     const int64_t items = num_nblocks * block_size;
     if (params_are_log) {
         const sparse::BlockLayout<true> L{node_mars, params, nids, cids, pids, num_edges, block_size, batch};

@@ -349,8 +349,40 @@ def sparse_forward_q16(node_mars, element_mars, params, nids, cids, pids, block_
     return _sparse_blocked(node_mars, element_mars, params, nids, cids, pids, block_size, True, params_are_log)
 
 
+def sparse_blocked_transpose(nids, cids, pids, block_size, num_elements):
+    """The transposed structure fl_sparse_csr_bwd walks for a block-layout sum
+    layer (the forward dispatcher's nids [nblocks], cids and pids [nblocks,
+    num_edges], int64): the layer expanded to one edge per (block j, position
+    p < block_size, edge e) in that order, and returned as (csc_offsets int64
+    [num_elements + 1], csc_edges int32 [nnz] with the expanded edges into
+    each element row in increasing order, csc_nodes int32 [nnz] with each of
+    those edges' node_mars row nids[j] + p, param_ids int64 [nnz] with each
+    expanded edge's parameter pids[j, e] + p).  Built with torch's sort on
+    the device; it depends on the layer only, so a caller that runs the layer
+    many times builds it once and passes it to sparse_blocked_backward."""
+    for name, t in (("nids", nids), ("cids", cids), ("pids", pids)):
+        _check(t.is_cuda and t.dtype == torch.int64 and t.is_contiguous(), f"{name} must be a contiguous CUDA int64 tensor")
+    _check(cids.dim() == 2 and pids.shape == cids.shape and nids.dim() == 1 and nids.size(0) == cids.size(0),
+           "nids [nblocks], cids and pids [nblocks, num_edges] shapes disagree")
+    nb, ne = cids.shape
+    bs = int(block_size)
+    nnz = nb * bs * ne
+    _check(nnz < 2 ** 31 and num_elements < 2 ** 31, "edges and element rows must each be < 2^31")
+    dev = cids.device
+    pos = torch.arange(bs, device=dev)
+    node_rows = (nids[:, None] + pos[None, :]).reshape(-1)                      # [nb * bs]
+    child_ids = cids[:, None, :].expand(nb, bs, ne).reshape(-1)                 # [nnz], edge (j, p, e)
+    param_ids = (pids[:, None, :] + pos[None, :, None]).reshape(-1)             # [nnz]
+    order = torch.sort(child_ids, stable=True).indices
+    counts = torch.bincount(child_ids, minlength=num_elements)
+    _check(counts.numel() == num_elements, "cids hold ids >= element_mars rows")
+    csc_off = torch.zeros(num_elements + 1, dtype=torch.int64, device=dev)
+    torch.cumsum(counts, 0, out=csc_off[1:])
+    return csc_off, order.to(torch.int32), node_rows[order // ne].to(torch.int32), param_ids
+
+
 def sparse_blocked_backward(node_flows, element_flows, node_mars, element_mars, params, param_flows, nids, cids, pids,
-                            block_size, params_are_log=False):
+                            block_size, params_are_log=False, plan=None):
     """Flows of the block-layout sum layer of sparse_forward_float (pyjuice's
     layout, as the forward dispatcher passes it), in fp32, added in place:
     for block j, position p < block_size and edge e, with n = nids[j] + p,
@@ -361,10 +393,11 @@ def sparse_blocked_backward(node_flows, element_flows, node_mars, element_mars, 
       element_flows[c, b] += the terms of the edges into c,
       param_flows[q]      += the terms of edge (j, p, e) summed over b.
     node_mars must hold this layer's forward output.  The reference has no
-    sparse backward.  The layer is expanded to one CSR node per (block,
-    position) and run through fl_sparse_csr_bwd, whose transposed structure
-    names each edge's node_mars row directly, so node_mars and node_flows are
-    read in place.  param_flows is accumulated with index_add_, whose order is
+    sparse backward.  The layer runs as one CSR node per (block, position)
+    through fl_sparse_csr_bwd, whose transposed structure names each edge's
+    node_mars row directly, so node_mars and node_flows are read in place.
+    plan: the result of sparse_blocked_transpose for this layer (built here
+    when None).  param_flows is accumulated with index_add_, whose order is
     not fixed where several edges share a parameter.  Returns None."""
     _check(node_flows.is_cuda and element_flows.is_cuda and param_flows.is_cuda, "flows must be CUDA tensors")
     for t, nm in ((node_flows, "node_flows"), (element_flows, "element_flows"), (param_flows, "param_flows")):
@@ -385,28 +418,21 @@ def sparse_blocked_backward(node_flows, element_flows, node_mars, element_mars, 
     _check(cids.dim() == 2 and pids.shape == cids.shape and nids.dim() == 1 and nids.size(0) == cids.size(0),
            "nids [nblocks], cids and pids [nblocks, num_edges] shapes disagree")
     nb, ne = cids.shape
-    bs = int(block_size)
+    nnz = nb * int(block_size) * ne
     num_el, batch = element_mars.shape
-    nnz = nb * bs * ne
     if nnz == 0 or batch == 0:
         return None
     _check(nnz < 2 ** 31 and num_el < 2 ** 31 and node_mars.size(0) < 2 ** 31,
            "edges, element rows and node rows must each be < 2^31")
-    dev = cids.device
-    pos = torch.arange(bs, device=dev)
-    node_rows = (nids[:, None] + pos[None, :]).reshape(-1)                      # [nb * bs]
-    child_ids = cids[:, None, :].expand(nb, bs, ne).reshape(-1)                 # [nnz], edge (j, p, e)
-    q = (pids[:, None, :] + pos[None, :, None]).reshape(-1)                     # [nnz]
+    if plan is None:
+        plan = sparse_blocked_transpose(nids, cids, pids, block_size, num_el)
+    csc_off, csc_edge, csc_node, q = plan
+    _check(csc_off.dtype == torch.int64 and csc_off.numel() == num_el + 1 and csc_edge.dtype == torch.int32
+           and csc_node.dtype == torch.int32 and q.dtype == torch.int64 and csc_edge.numel() == nnz
+           and csc_node.numel() == nnz and q.numel() == nnz, "plan does not fit this layer")
     w = params.reshape(-1)[q]
     logp = w if params_are_log else torch.log(torch.clamp_min(w, 1e-45))
     logp = logp.contiguous()
-    order = torch.sort(child_ids, stable=True).indices
-    counts = torch.bincount(child_ids, minlength=num_el)
-    _check(counts.numel() == num_el, "cids hold ids >= element_mars rows")
-    csc_off = torch.zeros(num_el + 1, dtype=torch.int64, device=dev)
-    torch.cumsum(counts, 0, out=csc_off[1:])
-    csc_edge = order.to(torch.int32)
-    csc_node = node_rows[order // ne].to(torch.int32)
     grad_el = torch.empty_like(element_mars)
     grad_lp = torch.empty_like(logp)
     with _on_device(element_mars):

@@ -311,3 +311,128 @@ def test_blocked_backward_subset_of_blocks(cuda):
     assert (np.abs(got_p - dp) <= 1e-5 * ap + 1e-30).all()
     untouched = np.setdiff1d(np.arange(nelem), cids[sel].reshape(-1))
     assert (got_e[untouched] == 0).all()
+
+
+def test_blocked_backward_with_a_reused_plan(cuda):
+    """sparse_blocked_transpose built once and passed to several backward
+    calls gives the same bits as the backward that builds it itself; a plan
+    of another layer is refused."""
+    print("case blocked_bwd plan reuse", flush=True)
+    rng = np.random.default_rng(91)
+    nb, ne, bs, batch, nelem, nparams = 9, 11, 3, 96, 50, 400
+    nids, cids, _, params, em = _blocked(rng, nb, ne, bs, batch, nelem, nparams)
+    pids = (np.arange(nb * ne, dtype=np.int64) * bs).reshape(nb, ne)     # one parameter per expanded edge
+    ext = _ext()
+    d = {k: torch.from_numpy(v).to(cuda) for k, v in (("em", em), ("p", params), ("nids", nids), ("cids", cids),
+                                                      ("pids", pids))}
+    nm = torch.zeros(nb * bs, batch, device=cuda)
+    ext.sparse_forward_float(nm, d["em"], d["p"], d["nids"], d["cids"], d["pids"], bs)
+    plan = ext.sparse_blocked_transpose(d["nids"], d["cids"], d["pids"], bs, nelem)
+    for rep in range(3):
+        nf = torch.from_numpy(rng.standard_normal((nb * bs, batch)).astype(np.float32)).to(cuda)
+        ef_a, pf_a = torch.zeros(nelem, batch, device=cuda), torch.zeros(nparams, device=cuda)
+        ef_b, pf_b = torch.zeros_like(ef_a), torch.zeros_like(pf_a)
+        ext.sparse_blocked_backward(nf, ef_a, nm, d["em"], d["p"], pf_a, d["nids"], d["cids"], d["pids"], bs)
+        ext.sparse_blocked_backward(nf, ef_b, nm, d["em"], d["p"], pf_b, d["nids"], d["cids"], d["pids"], bs,
+                                    plan=plan)
+        assert torch.equal(ef_a, ef_b)
+        assert torch.equal(pf_a, pf_b)
+    other = ext.sparse_blocked_transpose(d["nids"][:4], d["cids"][:4], d["pids"][:4], bs, nelem)
+    with pytest.raises(RuntimeError, match="plan does not fit"):
+        ext.sparse_blocked_backward(nf, ef_a, nm, d["em"], d["p"], pf_a, d["nids"], d["cids"], d["pids"], bs,
+                                    plan=other)
+
+
+# ---------------------------------------------------------------------------
+# Block layout, fp32, block_size >= 8: the product form on the matrix cores
+# (node_mars = log W_p + m_b + log sum_e w'[p, e] exp(x[e, b] - m_b)), against
+# the fp64 loops of the oracle.  The weight floor is the fp32 value of 1e-45
+# (the smallest subnormal), which the kernels apply before the log.
+# ---------------------------------------------------------------------------
+F32_FLOOR = float(np.float32(1e-45))
+
+PRODUCT_CASES = [(8, 5, 64), (16, 32, 130), (24, 33, 512), (32, 32, 512), (48, 7, 96), (64, 100, 260),
+                 (128, 16, 64), (32, 1, 3), (9, 70, 600), (16, 64, 1)]
+
+
+@pytest.mark.parametrize("bs,ne,batch", PRODUCT_CASES)
+@pytest.mark.parametrize("log_params", [False, True])
+def test_blocked_product_form_matches_fp64(cuda, bs, ne, batch, log_params):
+    print(f"case blocked product bs={bs} ne={ne} batch={batch} log={log_params}", flush=True)
+    rng = np.random.default_rng(bs * 1000 + ne * 10 + batch)
+    nb, nelem = 5, 90
+    nparams = nb * ne * bs + 40
+    nids = (np.arange(nb) * (bs + 2) + 1).astype(np.int64)     # gaps between blocks stay untouched
+    cids = rng.integers(0, nelem, (nb, ne)).astype(np.int64)
+    pids = rng.integers(0, nparams - bs + 1, (nb, ne)).astype(np.int64)
+    params = (rng.random(nparams) + 1e-3).astype(np.float32)
+    em = (np.log(rng.random((nelem, batch)) + 1e-12) * rng.choice([1.0, 5.0], (nelem, 1))).astype(np.float32)
+    p_in = np.log(params).astype(np.float32) if log_params else params
+    nm0 = np.full((int(nids[-1]) + bs + 3, batch), 7.0, np.float32)
+    nm = torch.from_numpy(nm0.copy()).to(cuda)
+    d = _to(cuda, em, p_in, nids, cids, pids)
+    _ext().sparse_forward_float(nm, d[0], d[1], d[2], d[3], d[4], bs, params_are_log=log_params)
+    got = nm.cpu().numpy()
+    if log_params:
+        rows, vals = O.sparse_blocked_fp64(em, np.exp(p_in.astype(np.float64)), nids, cids, pids, bs, clamp=0.0)
+    else:
+        rows, vals = O.sparse_blocked_fp64(em, params, nids, cids, pids, bs, clamp=F32_FLOOR)
+    np.testing.assert_allclose(got[rows], vals, rtol=1e-5, atol=1e-6)
+    untouched = np.setdiff1d(np.arange(nm0.shape[0]), rows)
+    assert (got[untouched] == 7.0).all()
+
+
+def test_blocked_product_form_special_values_and_fallback(cuda):
+    """Entries the product cannot resolve take the exact fold: -inf children,
+    columns of -inf, +inf and NaN children, zero weights, a parent whose only
+    large weights meet children ~200 nats below the column maximum."""
+    print("case blocked product special values", flush=True)
+    rng = np.random.default_rng(5)
+    nb, ne, bs, batch, nelem = 3, 40, 16, 68, 60
+    nids = (np.arange(nb) * bs).astype(np.int64)
+    cids = np.stack([rng.permutation(nelem)[:ne] for _ in range(nb)]).astype(np.int64)
+    pids = (np.arange(nb * ne, dtype=np.int64) * bs).reshape(nb, ne)
+    params = (rng.random(nb * ne * bs) + 1e-3).astype(np.float32)
+    em = np.log(rng.random((nelem, batch)) + 1e-9).astype(np.float32)
+    em[cids[0, 3], :] = -np.inf                  # a child of probability 0
+    em[:, 5] = -np.inf                           # a column where every child is -inf
+    em[cids[1, 0], 7] = np.inf                   # +inf wins
+    em[cids[2, 1], 9] = np.nan                   # NaN wins
+    params[pids[0, :] + 2] = 0.0                 # parent 2 of block 0: every weight zero
+    params[pids[1, 5] + 4] = 0.0                 # one zero weight
+    # block 2, parent 6: weight ~1 only on edge 0, whose child sits 200 below
+    # the column maximum held by edge 1, whose weight is zero
+    params[pids[2, :] + 6] = 1e-36
+    params[pids[2, 0] + 6] = 1.0
+    params[pids[2, 1] + 6] = 0.0
+    em[cids[2, 0], 20:30] = -200.0
+    em[cids[2, 1], 20:30] = 0.0
+    nm = torch.zeros(nb * bs, batch, device=cuda)
+    d = _to(cuda, em, params, nids, cids, pids)
+    _ext().sparse_forward_float(nm, d[0], d[1], d[2], d[3], d[4], bs)
+    got = nm.cpu().numpy()
+    rows, vals = O.sparse_blocked_fp64(em, params, nids, cids, pids, bs, clamp=F32_FLOOR)
+    want = np.empty_like(got, dtype=np.float64)
+    want[rows] = vals
+    assert np.isneginf(got[:, 5]).all()
+    assert np.isnan(got[bs * 2:, 9]).all() and np.isposinf(got[bs:2 * bs, 7]).all()
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6, equal_nan=True)
+    assert (np.abs(got[2 * bs + 6, 20:30] - want[2 * bs + 6, 20:30]) < 1e-3).all()
+
+
+@pytest.mark.parametrize("offset", [1, 3])
+def test_blocked_product_form_unaligned_rows(cuda, offset):
+    """Rows that are not 16-byte aligned take the scalar-column loads."""
+    print(f"case blocked product unaligned off={offset}", flush=True)
+    rng = np.random.default_rng(offset)
+    nb, ne, bs, batch, nelem = 4, 12, 16, 36, 30
+    nids, cids, pids, params, em = _blocked(rng, nb, ne, bs, batch, nelem, 600)
+    buf = torch.zeros(nelem * batch + offset, device=cuda)
+    emd = buf[offset:].view(nelem, batch)
+    emd.copy_(torch.from_numpy(em).to(cuda))
+    obuf = torch.zeros(nb * bs * batch + offset, device=cuda)
+    nm = obuf[offset:].view(nb * bs, batch)
+    d = _to(cuda, params, nids, cids, pids)
+    _ext().sparse_forward_float(nm, emd, d[0], d[1], d[2], d[3], bs)
+    rows, vals = O.sparse_blocked_fp64(em, params, nids, cids, pids, bs, clamp=F32_FLOOR)
+    np.testing.assert_allclose(nm.cpu().numpy()[rows], vals, rtol=1e-5, atol=1e-6)
