@@ -14,15 +14,18 @@
 // value is loaded and exponentiated once per block and the product runs on
 // v_mfma_f32_16x16x4_f32.
 //
-// Mapping: one wave per (node block, group of 16*MT parents, 64-column tile).
-// In each 16x16x4 product lane l supplies A[l%16][l/16] (parent row) and
-// B[l/16][l%16] (edge row, column) and holds D[4*(l/16) + r][l%16], r < 4.
-// Column j of N-tile t is batch column b0 + 4*j + t, so lane l loads one
-// 16-byte vector (columns b0 + 4*(l%16) .. +3) of the child row of edge
-// 4*ks + l/16 and that vector is its B operand for the four N-tiles t; the
+// Mapping: one wave per (node block, group of 16*MT parents, tile of 16*NT
+// batch columns).  In each 16x16x4 product lane l supplies A[l%16][l/16]
+// (parent row) and B[l/16][l%16] (edge row, column) and holds
+// D[4*(l/16) + r][l%16], r < 4.  Column j of N-tile t = 4*q + u is batch
+// column b0 + 64*q + 4*j + u, so lane l loads one 16-byte vector (columns
+// b0 + 64*q + 4*(l%16) .. +3) of the child row of edge 4*ks + l/16 per q and
+// that vector is its B operand for the four N-tiles 4*q .. 4*q + 3; the
 // results of row p come back as the same four consecutive columns, one
-// 16-byte store.  Edges are taken 32 at a time (8 K-steps); the column
-// maximum is kept online across chunks, rescaling the accumulators.
+// 16-byte store.  Edges are taken up to 32 at a time (2, 4 or 8 K-steps of
+// 4); the row maxima of the weights and the column maxima of the child values
+// are kept online across chunks, rescaling the accumulators, so every weight
+// and child value is loaded once.
 //
 // Accuracy: every term is >= 0, so S carries only rounding of fp32 products
 // and sums.  Terms below 2^-126 may flush to zero, losing at most
@@ -41,11 +44,14 @@ namespace sparse {
 
 namespace {
 
-constexpr int KC = 32;      // edges per chunk
-constexpr int KS = KC / 4;  // K-steps per chunk
+constexpr int KSMAX = 8;        // K-steps of 4 edges per chunk, at most
+constexpr int KCMAX = 4 * KSMAX;  // edges per chunk, at most
 
 __device__ __forceinline__ float xor16(float v) { return exact_xor<16>(v); }
 __device__ __forceinline__ float xor32(float v) { return exact_xor<32>(v); }
+__device__ __forceinline__ float lane_read(float v, int src) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src * 4, __builtin_bit_cast(int, v)));
+}
 
 // The weight entering the linear product: the reference floors linear weights
 // at 1e-45 before its log (sparse_float_kernel.cu:76).
@@ -55,29 +61,34 @@ __device__ __forceinline__ float weight_term(float w) {
 }
 
 // Child values of chunk edges c0 + 4*ks + kq at the lane's four columns;
-// edges past ne read -inf, columns past the batch read 0 (never stored).
-template <bool VEC>
-__device__ __forceinline__ void load_chunk(float (&x)[KS][4], const float* __restrict__ child,
+// edges past ne read -inf (their addresses clamped to edge ne - 1), columns
+// past the batch read 0 (never stored).
+template <int NK, int NT, bool VEC>
+__device__ __forceinline__ void load_chunk(float (&x)[NK][NT], const float* __restrict__ child,
                                            const int64_t* __restrict__ cids, int64_t ebase, int64_t ne, int64_t c0,
                                            int kq, int64_t col, int64_t batch) {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
+    for (int ks = 0; ks < NK; ++ks) {
         const int64_t e = c0 + 4 * ks + kq;
         const bool ev = e < ne;
         const float* row = child + cids[ebase + (ev ? e : ne - 1)] * batch;
-        if constexpr (VEC) {
-            const bool cv = col < batch;
-            const f32x4 v = *reinterpret_cast<const f32x4*>(row + (cv ? col : 0));
-            x[ks][0] = ev ? (cv ? v.x : 0.0f) : -kInf;
-            x[ks][1] = ev ? (cv ? v.y : 0.0f) : -kInf;
-            x[ks][2] = ev ? (cv ? v.z : 0.0f) : -kInf;
-            x[ks][3] = ev ? (cv ? v.w : 0.0f) : -kInf;
-        } else {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const bool cv = col + t < batch;
-                const float v = row[cv ? col + t : 0];
-                x[ks][t] = ev ? (cv ? v : 0.0f) : -kInf;
+        for (int q = 0; q < NT / 4; ++q) {
+            const int64_t cq = col + 64 * q;
+            if constexpr (VEC) {
+                const bool cv = cq < batch;
+                const f32x4 v = *reinterpret_cast<const f32x4*>(row + (cv ? cq : 0));
+                x[ks][4 * q] = ev ? (cv ? v.x : 0.0f) : -kInf;
+                x[ks][4 * q + 1] = ev ? (cv ? v.y : 0.0f) : -kInf;
+                x[ks][4 * q + 2] = ev ? (cv ? v.z : 0.0f) : -kInf;
+                x[ks][4 * q + 3] = ev ? (cv ? v.w : 0.0f) : -kInf;
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const bool cv = cq + t < batch;
+                    const float v = row[cv ? cq + t : 0];
+                    x[ks][4 * q + t] = ev ? (cv ? v : 0.0f) : -kInf;
+                }
             }
         }
     }
@@ -86,12 +97,12 @@ __device__ __forceinline__ void load_chunk(float (&x)[KS][4], const float* __res
 // Raw weights of chunk edges c0 + 4*ks + kq for parents p0 + 16*mt + jc
 // (the lane's A-layout entries); invalid entries read as -inf (log weights)
 // or 0 (linear weights), the identity of the row maximum.
-template <int MT, bool LOGP>
-__device__ __forceinline__ void load_weights(float (&w)[MT][KS], const float* __restrict__ params,
+template <int MT, int NK, bool LOGP>
+__device__ __forceinline__ void load_weights(float (&w)[MT][NK], const float* __restrict__ params,
                                              const int64_t* __restrict__ pids, int64_t ebase, int64_t ne, int64_t bs,
                                              int64_t c0, int64_t p0, int kq, int jc) {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
+    for (int ks = 0; ks < NK; ++ks) {
         const int64_t e = c0 + 4 * ks + kq;
         const bool ev = e < ne;
         const int64_t q = pids[ebase + (ev ? e : ne - 1)];
@@ -105,14 +116,78 @@ __device__ __forceinline__ void load_weights(float (&w)[MT][KS], const float* __
     }
 }
 
+// Folds one chunk into the accumulators: online row maxima of the weights
+// (A layout, wm) and column maxima of the child values (m), the accumulators
+// rescaled to both (FIRST: nothing accumulated yet), then
+// acc += (w / wm) x exp(x - m) on the matrix cores.
+template <int MT, int NK, int NT, bool LOGP, bool FIRST>
+__device__ __forceinline__ void fold_chunk(f32x4 (&acc)[MT][NT], float (&wm)[MT], float (&m)[NT],
+                                           float (&x)[NK][NT], const float (&w)[MT][NK], int kq) {
+    float a[MT][NK];
+    float beta[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        float cw = w[mt][0];
+#pragma unroll
+        for (int ks = 1; ks < NK; ++ks) cw = fmaxf(cw, w[mt][ks]);
+        cw = fmaxf(cw, xor16(cw));
+        cw = fmaxf(cw, xor32(cw));
+        const float nw = fmaxf(wm[mt], cw);
+        if constexpr (LOGP) {
+            beta[mt] = wm[mt] == -kInf ? 0.0f : fexp2((wm[mt] - nw) * kLog2e);
+#pragma unroll
+            for (int ks = 0; ks < NK; ++ks) a[mt][ks] = nw == -kInf ? 0.0f : fexp2((w[mt][ks] - nw) * kLog2e);
+        } else {
+            const float rinv = 1.0f / nw;
+            beta[mt] = wm[mt] * rinv;
+#pragma unroll
+            for (int ks = 0; ks < NK; ++ks) a[mt][ks] = w[mt][ks] * rinv;
+        }
+        wm[mt] = nw;
+    }
+    float alpha[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        float cm = x[0][t];
+#pragma unroll
+        for (int ks = 1; ks < NK; ++ks) cm = fmaxf(cm, x[ks][t]);
+        cm = fmaxf(cm, xor16(cm));
+        cm = fmaxf(cm, xor32(cm));
+        const float mn = fmaxf(m[t], cm);
+        alpha[t] = m[t] == -kInf ? 0.0f : fexp2((m[t] - mn) * kLog2e);
+        m[t] = mn;
+#pragma unroll
+        for (int ks = 0; ks < NK; ++ks) x[ks][t] = mn == -kInf ? 0.0f : fexp2((x[ks][t] - mn) * kLog2e);
+    }
+    if constexpr (!FIRST) {
+        // D-layout row 16*mt + 4*kq + r takes the row factor of A-layout lane 4*kq + r
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float br = lane_read(beta[mt], 4 * kq + r);
+#pragma unroll
+                for (int t = 0; t < NT; ++t) acc[mt][t][r] *= br * alpha[t];
+            }
+    }
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[mt][ks], x[ks][t], acc[mt][t], 0, 0, 0);
+}
+
 }  // namespace
 
 // One wave per (node block j, parent group g, column tile ct); logical ids
 // run ct fastest, then g, then j, and are dealt to the XCDs in contiguous
 // ranges (physical workgroup w runs on XCD w % 8), so the column tiles and
 // parent groups of one node block share an L2 for the block's weights and
-// child rows.
-template <int MT, bool VEC, bool LOGP, bool ONE>
+// child rows.  NK: K-steps per chunk (ne <= 4*NK takes one chunk); MULTI:
+// chunks of 32 edges, the next chunk's loads in flight while one folds.
+template <int MT, int NK, int NT, bool MULTI, bool VEC, bool LOGP>
 __global__ __launch_bounds__(64) void blocked_mfma_kernel(float* __restrict__ node_mars,
                                                           const float* __restrict__ child,
                                                           const float* __restrict__ params,
@@ -131,107 +206,80 @@ __global__ __launch_bounds__(64) void blocked_mfma_kernel(float* __restrict__ no
     const int l = lane_id();
     const int kq = l >> 4;
     const int jc = l & 15;
-    const int64_t col = ct * 64 + 4 * jc;
+    const int64_t col = ct * 16 * NT + 4 * jc;  // N-tile t: column col + 64*(t/4) + t%4
     const int64_t ebase = j * ne;
     const int64_t p0 = g * 16 * MT;
+    constexpr int KC = 4 * NK;
 
-    // Weights, A layout (row p0 + 16*mt + jc, edge c0 + 4*ks + kq), and their
-    // row maxima over all edges.  With a single chunk (ONE) they are loaded
-    // once; otherwise a first pass takes the maxima and each chunk reloads.
-    float wr[MT][KS];
-    float wmax[MT];
+    float m[NT], wm[MT];
+    f32x4 acc[MT][NT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) wmax[mt] = LOGP ? -kInf : 0.0f;
-    for (int64_t c0 = 0; c0 < (ONE ? 1 : ne); c0 += KC) {
-        load_weights<MT, LOGP>(wr, params, pids, ebase, ne, bs, c0, p0, kq, jc);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) wmax[mt] = fmaxf(wmax[mt], wr[mt][ks]);
-    }
-    float rinv[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        wmax[mt] = fmaxf(wmax[mt], xor16(wmax[mt]));
-        wmax[mt] = fmaxf(wmax[mt], xor32(wmax[mt]));
-        rinv[mt] = LOGP ? 0.0f : 1.0f / wmax[mt];
-    }
-
-    float m[4];
-    f32x4 acc[MT][4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < NT; ++t) {
         m[t] = -kInf;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[mt][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) wm[mt] = LOGP ? -kInf : 0.0f;
 
-    for (int64_t c0 = 0; c0 < ne; c0 += KC) {
-        float x[KS][4];
-        load_chunk<VEC>(x, child, cids, ebase, ne, c0, kq, col, batch);
-        if (!ONE) load_weights<MT, LOGP>(wr, params, pids, ebase, ne, bs, c0, p0, kq, jc);
-        float a[MT][KS];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const bool valid = c0 + 4 * ks + kq < ne && p0 + 16 * mt + jc < bs;
-                const float wn = LOGP ? fexp2((wr[mt][ks] - wmax[mt]) * kLog2e) : wr[mt][ks] * rinv[mt];
-                a[mt][ks] = valid ? wn : 0.0f;
-            }
-        // online column maximum; lanes l, l^16, l^32, l^48 share columns
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            float cm = x[0][t];
-#pragma unroll
-            for (int ks = 1; ks < KS; ++ks) cm = fmaxf(cm, x[ks][t]);
-            cm = fmaxf(cm, xor16(cm));
-            cm = fmaxf(cm, xor32(cm));
-            const float mn = fmaxf(m[t], cm);
-            const float alpha = m[t] == -kInf ? 0.0f : fexp2((m[t] - mn) * kLog2e);
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) acc[mt][t] *= alpha;
-            m[t] = mn;
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) x[ks][t] = mn == -kInf ? 0.0f : fexp2((x[ks][t] - mn) * kLog2e);
+    float xa[NK][NT], wa[MT][NK];
+    load_chunk<NK, NT, VEC>(xa, child, cids, ebase, ne, 0, kq, col, batch);
+    load_weights<MT, NK, LOGP>(wa, params, pids, ebase, ne, bs, 0, p0, kq, jc);
+    if constexpr (!MULTI) {
+        fold_chunk<MT, NK, NT, LOGP, true>(acc, wm, m, xa, wa, kq);
+    } else {
+        // chunks past the end load clamped addresses and fold nothing
+        float xb[NK][NT], wb[MT][NK];
+        load_chunk<NK, NT, VEC>(xb, child, cids, ebase, ne, KC, kq, col, batch);
+        load_weights<MT, NK, LOGP>(wb, params, pids, ebase, ne, bs, KC, p0, kq, jc);
+        __builtin_amdgcn_sched_barrier(0);
+        fold_chunk<MT, NK, NT, LOGP, true>(acc, wm, m, xa, wa, kq);
+        for (int64_t c0 = KC; c0 < ne; c0 += 2 * KC) {
+            load_chunk<NK, NT, VEC>(xa, child, cids, ebase, ne, c0 + KC, kq, col, batch);
+            load_weights<MT, NK, LOGP>(wa, params, pids, ebase, ne, bs, c0 + KC, p0, kq, jc);
+            __builtin_amdgcn_sched_barrier(0);
+            fold_chunk<MT, NK, NT, LOGP, false>(acc, wm, m, xb, wb, kq);
+            if (c0 + KC >= ne) break;
+            load_chunk<NK, NT, VEC>(xb, child, cids, ebase, ne, c0 + 2 * KC, kq, col, batch);
+            load_weights<MT, NK, LOGP>(wb, params, pids, ebase, ne, bs, c0 + 2 * KC, p0, kq, jc);
+            __builtin_amdgcn_sched_barrier(0);
+            fold_chunk<MT, NK, NT, LOGP, false>(acc, wm, m, xa, wa, kq);
         }
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int t = 0; t < 4; ++t)
-                    acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[mt][ks], x[ks][t], acc[mt][t], 0, 0, 0);
     }
 
     // D layout: lane l holds rows p0 + 16*mt + 4*kq + r.  Their weight maxima
     // live in A-layout lane 4*kq + r.
     const float thr = (float)ne * 0x1p-102f;
     const int64_t nrow0 = nids[j];
-    uint64_t redo = 0;  // bit 16*mt + 4*r + t: entry left to the exact fold
+    static_assert(MT * 4 * NT <= 64, "one bit per held entry");
+    uint64_t redo = 0;  // bit (4*mt + r)*NT + t: entry left to the exact fold
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-        const float lwm = LOGP ? wmax[mt] : logf(wmax[mt]);
+        const float lwm = LOGP ? wm[mt] : logf(wm[mt]);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float lwr = __builtin_bit_cast(
-                float, __builtin_amdgcn_ds_bpermute((4 * kq + r) * 4, __builtin_bit_cast(int, lwm)));
+            const float lwr = lane_read(lwm, 4 * kq + r);
             const int64_t p = p0 + 16 * mt + 4 * kq + r;
             if (p >= bs) continue;
-            float res[4];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const float s = acc[mt][t][r];
-                res[t] = lwr + m[t] + flog2(s) * kLn2;
-                if (!(s >= thr && s <= 0x1p100f) && col + t < batch) redo |= (uint64_t)1 << (16 * mt + 4 * r + t);
-            }
             float* orow = node_mars + (nrow0 + p) * batch;
-            if constexpr (VEC) {
-                if (col < batch) *reinterpret_cast<f32x4*>(orow + col) = f32x4{res[0], res[1], res[2], res[3]};
-            } else {
 #pragma unroll
-                for (int t = 0; t < 4; ++t)
-                    if (col + t < batch) orow[col + t] = res[t];
+            for (int q = 0; q < NT / 4; ++q) {
+                const int64_t cq = col + 64 * q;
+                float res[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const float s = acc[mt][4 * q + u][r];
+                    res[u] = lwr + m[4 * q + u] + flog2(s) * kLn2;
+                    if (!(s >= thr && s <= 0x1p100f) && cq + u < batch)
+                        redo |= (uint64_t)1 << ((4 * mt + r) * NT + 4 * q + u);
+                }
+                if constexpr (VEC) {
+                    if (cq < batch) *reinterpret_cast<f32x4*>(orow + cq) = f32x4{res[0], res[1], res[2], res[3]};
+                } else {
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        if (cq + u < batch) orow[cq + u] = res[u];
+                }
             }
         }
     }
@@ -241,8 +289,9 @@ __global__ __launch_bounds__(64) void blocked_mfma_kernel(float* __restrict__ no
     while (redo) {
         const int bit = __builtin_ctzll(redo);
         redo &= redo - 1;
-        const int64_t p = p0 + 16 * (bit >> 4) + 4 * kq + ((bit >> 2) & 3);
-        const int64_t c = col + (bit & 3);
+        const int mr = bit / NT, t = bit % NT;
+        const int64_t p = p0 + 16 * (mr >> 2) + 4 * kq + (mr & 3);
+        const int64_t c = col + 64 * (t >> 2) + (t & 3);
         float mm = -kInf, ss = 0.0f;
         for (int64_t e = 0; e < ne; ++e) {
             const float w = params[pids[ebase + e] + p];
@@ -257,24 +306,41 @@ __global__ __launch_bounds__(64) void blocked_mfma_kernel(float* __restrict__ no
 // Parents per product row group: 16, 32 or 64.
 static int blocked_mt(int64_t bs) { return bs <= 16 ? 1 : bs <= 32 ? 2 : 4; }
 
-template <int MT, bool VEC, bool LOGP>
-static void launch_mt(float* node_mars, const float* child, const float* params, const int64_t* nids,
-                      const int64_t* cids, const int64_t* pids, int64_t nblocks, int64_t ne, int64_t bs,
-                      int64_t batch, hipStream_t st) {
-    const int64_t ctiles = (batch + 63) / 64;
+template <int MT, int NK, int NT, bool MULTI, bool VEC, bool LOGP>
+static void launch_k(float* node_mars, const float* child, const float* params, const int64_t* nids,
+                     const int64_t* cids, const int64_t* pids, int64_t nblocks, int64_t ne, int64_t bs,
+                     int64_t batch, hipStream_t st) {
+    const int64_t ctiles = (batch + 16 * NT - 1) / (16 * NT);
     const int64_t pgroups = (bs + 16 * MT - 1) / (16 * MT);
     const int64_t items = nblocks * pgroups * ctiles;
     constexpr int64_t kMax = (int64_t)1 << 30;  // workgroups per launch, a multiple of 8
     for (int64_t id0 = 0; id0 < items; id0 += kMax) {
         const int64_t n = items - id0 < kMax ? items - id0 : kMax;
         const unsigned grid = (unsigned)((n + 7) / 8 * 8);
-        if (ne <= KC)
-            blocked_mfma_kernel<MT, VEC, LOGP, true><<<dim3(grid), dim3(64), 0, st>>>(
-                node_mars, child, params, nids, cids, pids, ne, bs, batch, ctiles, pgroups, items, id0);
-        else
-            blocked_mfma_kernel<MT, VEC, LOGP, false><<<dim3(grid), dim3(64), 0, st>>>(
-                node_mars, child, params, nids, cids, pids, ne, bs, batch, ctiles, pgroups, items, id0);
+        blocked_mfma_kernel<MT, NK, NT, MULTI, VEC, LOGP><<<dim3(grid), dim3(64), 0, st>>>(
+            node_mars, child, params, nids, cids, pids, ne, bs, batch, ctiles, pgroups, items, id0);
     }
+}
+
+template <int MT, bool VEC, bool LOGP>
+static void launch_mt(float* node_mars, const float* child, const float* params, const int64_t* nids,
+                      const int64_t* cids, const int64_t* pids, int64_t nblocks, int64_t ne, int64_t bs,
+                      int64_t batch, hipStream_t st) {
+    // 16x16 N-tiles per wave (16 * NT batch columns).  One parent group of 16
+    // takes 128 columns (more bytes in flight per wave: bs = 16, ne = 32 at
+    // batch 512, 337 -> 291 us); with 32 or 64 parents the larger accumulator
+    // set cost occupancy and time (256 -> 388 us at bs = 32), so they take 64.
+    constexpr int NT = MT == 1 ? 8 : 4;
+    if (ne <= 8)
+        launch_k<MT, 2, NT, false, VEC, LOGP>(node_mars, child, params, nids, cids, pids, nblocks, ne, bs, batch, st);
+    else if (ne <= 16)
+        launch_k<MT, 4, NT, false, VEC, LOGP>(node_mars, child, params, nids, cids, pids, nblocks, ne, bs, batch, st);
+    else if (ne <= KCMAX)
+        launch_k<MT, KSMAX, NT, false, VEC, LOGP>(node_mars, child, params, nids, cids, pids, nblocks, ne, bs, batch,
+                                                  st);
+    else
+        launch_k<MT, KSMAX, NT, true, VEC, LOGP>(node_mars, child, params, nids, cids, pids, nblocks, ne, bs, batch,
+                                                 st);
 }
 
 template <bool VEC, bool LOGP>

@@ -8,8 +8,10 @@
 namespace fl {
 namespace sparse {
 
-// Smallest block_size that takes the product form.
-constexpr int64_t kBlockedMfmaMinBs = 8;
+// Smallest block_size that takes the product form.  Measured at batch 512,
+// 32 edges per block: block_size 2, 1528 -> 823 us; 4, 1567 -> 422 us against
+// the per-parent gather.  block_size 1 keeps the per-parent kernel.
+constexpr int64_t kBlockedMfmaMinBs = 2;
 
 bool blocked_mfma_eligible(int64_t num_edges, int64_t block_size);
 

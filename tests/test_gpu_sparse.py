@@ -344,7 +344,7 @@ def test_blocked_backward_with_a_reused_plan(cuda):
 
 
 # ---------------------------------------------------------------------------
-# Block layout, fp32, block_size >= 8: the product form on the matrix cores
+# Block layout, fp32, block_size >= 2: the product form on the matrix cores
 # (node_mars = log W_p + m_b + log sum_e w'[p, e] exp(x[e, b] - m_b)), against
 # the fp64 loops of the oracle.  The weight floor is the fp32 value of 1e-45
 # (the smallest subnormal), which the kernels apply before the log.
@@ -352,7 +352,7 @@ def test_blocked_backward_with_a_reused_plan(cuda):
 F32_FLOOR = float(np.float32(1e-45))
 
 PRODUCT_CASES = [(8, 5, 64), (16, 32, 130), (24, 33, 512), (32, 32, 512), (48, 7, 96), (64, 100, 260),
-                 (128, 16, 64), (32, 1, 3), (9, 70, 600), (16, 64, 1)]
+                 (128, 16, 64), (32, 1, 3), (9, 70, 600), (16, 64, 1), (2, 40, 200), (5, 16, 129), (3, 9, 8)]
 
 
 @pytest.mark.parametrize("bs,ne,batch", PRODUCT_CASES)
@@ -436,3 +436,29 @@ def test_blocked_product_form_unaligned_rows(cuda, offset):
     _ext().sparse_forward_float(nm, emd, d[0], d[1], d[2], d[3], bs)
     rows, vals = O.sparse_blocked_fp64(em, params, nids, cids, pids, bs, clamp=F32_FLOOR)
     np.testing.assert_allclose(nm.cpu().numpy()[rows], vals, rtol=1e-5, atol=1e-6)
+
+
+def test_blocked_product_form_log_weights_empty_first_chunk(cuda):
+    """Log-weights of -inf (structural zeros): a parent whose first 32 edges
+    are all -inf and whose later edges are finite (the online row maximum
+    starts from nothing), and a parent with every weight -inf (-> -inf)."""
+    print("case blocked product log-weights -inf", flush=True)
+    rng = np.random.default_rng(17)
+    nb, ne, bs, batch, nelem = 2, 70, 32, 64, 100
+    nids = (np.arange(nb) * bs).astype(np.int64)
+    cids = rng.integers(0, nelem, (nb, ne)).astype(np.int64)
+    pids = (np.arange(nb * ne, dtype=np.int64) * bs).reshape(nb, ne)
+    lw = np.log(rng.random(nb * ne * bs) + 1e-3).astype(np.float32)
+    lw[pids[0, :32] + 5] = -np.inf
+    lw[pids[1, :] + 9] = -np.inf
+    em = np.log(rng.random((nelem, batch)) + 1e-9).astype(np.float32)
+    nm = torch.zeros(nb * bs, batch, device=cuda)
+    d = _to(cuda, em, lw, nids, cids, pids)
+    _ext().sparse_forward_float(nm, d[0], d[1], d[2], d[3], d[4], bs, params_are_log=True)
+    got = nm.cpu().numpy()
+    with np.errstate(divide="ignore"):
+        rows, vals = O.sparse_blocked_fp64(em, np.exp(lw.astype(np.float64)), nids, cids, pids, bs, clamp=0.0)
+    want = np.empty_like(got, dtype=np.float64)
+    want[rows] = vals
+    assert np.isneginf(got[bs + 9]).all()
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
