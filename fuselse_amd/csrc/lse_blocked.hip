@@ -122,8 +122,7 @@ __device__ __forceinline__ void load_weights(float (&w)[MT][NK], const float* __
 // acc += (w / wm) x exp(x - m) on the matrix cores.
 template <int MT, int NK, int NT, bool LOGP, bool FIRST>
 __device__ __forceinline__ void fold_chunk(f32x4 (&acc)[MT][NT], float (&wm)[MT], float (&m)[NT],
-                                           float (&x)[NK][NT], const float (&w)[MT][NK], int kq) {
-    float a[MT][NK];
+                                           float (&x)[NK][NT], float (&w)[MT][NK], int kq) {
     float beta[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -135,15 +134,18 @@ __device__ __forceinline__ void fold_chunk(f32x4 (&acc)[MT][NT], float (&wm)[MT]
         const float nw = fmaxf(wm[mt], cw);
         if constexpr (LOGP) {
             beta[mt] = wm[mt] == -kInf ? 0.0f : fexp2((wm[mt] - nw) * kLog2e);
-#pragma unroll
-            for (int ks = 0; ks < NK; ++ks) a[mt][ks] = nw == -kInf ? 0.0f : fexp2((w[mt][ks] - nw) * kLog2e);
         } else {
-            const float rinv = 1.0f / nw;
-            beta[mt] = wm[mt] * rinv;
-#pragma unroll
-            for (int ks = 0; ks < NK; ++ks) a[mt][ks] = w[mt][ks] * rinv;
+            beta[mt] = wm[mt] / nw;
         }
         wm[mt] = nw;
+    }
+    // normalised weights, in place: w / wm (linear) or exp(w - wm) (log)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const float rinv = LOGP ? 0.0f : 1.0f / wm[mt];
+#pragma unroll
+        for (int ks = 0; ks < NK; ++ks)
+            w[mt][ks] = LOGP ? (wm[mt] == -kInf ? 0.0f : fexp2((w[mt][ks] - wm[mt]) * kLog2e)) : w[mt][ks] * rinv;
     }
     float alpha[NT];
 #pragma unroll
@@ -176,7 +178,20 @@ __device__ __forceinline__ void fold_chunk(f32x4 (&acc)[MT][NT], float (&wm)[MT]
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int t = 0; t < NT; ++t)
-                acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[mt][ks], x[ks][t], acc[mt][t], 0, 0, 0);
+                acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(w[mt][ks], x[ks][t], acc[mt][t], 0, 0, 0);
+}
+
+// Loads and folds the NK K-steps of edges from c0.
+template <int MT, int NK, int NT, bool VEC, bool LOGP, bool FIRST>
+__device__ __forceinline__ void load_fold(f32x4 (&acc)[MT][NT], float (&wm)[MT], float (&m)[NT],
+                                          const float* __restrict__ child, const float* __restrict__ params,
+                                          const int64_t* __restrict__ cids, const int64_t* __restrict__ pids,
+                                          int64_t ebase, int64_t ne, int64_t bs, int64_t c0, int64_t p0, int kq,
+                                          int jc, int64_t col, int64_t batch) {
+    float x[NK][NT], w[MT][NK];
+    load_chunk<NK, NT, VEC>(x, child, cids, ebase, ne, c0, kq, col, batch);
+    load_weights<MT, NK, LOGP>(w, params, pids, ebase, ne, bs, c0, p0, kq, jc);
+    fold_chunk<MT, NK, NT, LOGP, FIRST>(acc, wm, m, x, w, kq);
 }
 
 }  // namespace
@@ -185,8 +200,8 @@ __device__ __forceinline__ void fold_chunk(f32x4 (&acc)[MT][NT], float (&wm)[MT]
 // run ct fastest, then g, then j, and are dealt to the XCDs in contiguous
 // ranges (physical workgroup w runs on XCD w % 8), so the column tiles and
 // parent groups of one node block share an L2 for the block's weights and
-// child rows.  NK: K-steps per chunk (ne <= 4*NK takes one chunk); MULTI:
-// chunks of 32 edges, the next chunk's loads in flight while one folds.
+// child rows.  NK: K-steps of the single chunk when ne <= 4*NK; MULTI: any
+// ne, in chunks of 32 edges and a tail of 8, 16 or 32.
 template <int MT, int NK, int NT, bool MULTI, bool VEC, bool LOGP>
 __global__ __launch_bounds__(64) void blocked_mfma_kernel(float* __restrict__ node_mars,
                                                           const float* __restrict__ child,
@@ -209,7 +224,6 @@ __global__ __launch_bounds__(64) void blocked_mfma_kernel(float* __restrict__ no
     const int64_t col = ct * 16 * NT + 4 * jc;  // N-tile t: column col + 64*(t/4) + t%4
     const int64_t ebase = j * ne;
     const int64_t p0 = g * 16 * MT;
-    constexpr int KC = 4 * NK;
 
     float m[NT], wm[MT];
     f32x4 acc[MT][NT];
@@ -222,29 +236,29 @@ __global__ __launch_bounds__(64) void blocked_mfma_kernel(float* __restrict__ no
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) wm[mt] = LOGP ? -kInf : 0.0f;
 
-    float xa[NK][NT], wa[MT][NK];
-    load_chunk<NK, NT, VEC>(xa, child, cids, ebase, ne, 0, kq, col, batch);
-    load_weights<MT, NK, LOGP>(wa, params, pids, ebase, ne, bs, 0, p0, kq, jc);
     if constexpr (!MULTI) {
-        fold_chunk<MT, NK, NT, LOGP, true>(acc, wm, m, xa, wa, kq);
+        load_fold<MT, NK, NT, VEC, LOGP, true>(acc, wm, m, child, params, cids, pids, ebase, ne, bs, 0, p0, kq, jc,
+                                               col, batch);
     } else {
-        // chunks past the end load clamped addresses and fold nothing
-        float xb[NK][NT], wb[MT][NK];
-        load_chunk<NK, NT, VEC>(xb, child, cids, ebase, ne, KC, kq, col, batch);
-        load_weights<MT, NK, LOGP>(wb, params, pids, ebase, ne, bs, KC, p0, kq, jc);
-        __builtin_amdgcn_sched_barrier(0);
-        fold_chunk<MT, NK, NT, LOGP, true>(acc, wm, m, xa, wa, kq);
-        for (int64_t c0 = KC; c0 < ne; c0 += 2 * KC) {
-            load_chunk<NK, NT, VEC>(xa, child, cids, ebase, ne, c0 + KC, kq, col, batch);
-            load_weights<MT, NK, LOGP>(wa, params, pids, ebase, ne, bs, c0 + KC, p0, kq, jc);
-            __builtin_amdgcn_sched_barrier(0);
-            fold_chunk<MT, NK, NT, LOGP, false>(acc, wm, m, xb, wb, kq);
-            if (c0 + KC >= ne) break;
-            load_chunk<NK, NT, VEC>(xb, child, cids, ebase, ne, c0 + 2 * KC, kq, col, batch);
-            load_weights<MT, NK, LOGP>(wb, params, pids, ebase, ne, bs, c0 + 2 * KC, p0, kq, jc);
-            __builtin_amdgcn_sched_barrier(0);
-            fold_chunk<MT, NK, NT, LOGP, false>(acc, wm, m, xa, wa, kq);
-        }
+        // full chunks of KCMAX edges, one at a time (a second buffer in flight
+        // cost more in occupancy than it hid), then the rest in the smallest
+        // chunk that holds it
+        load_fold<MT, KSMAX, NT, VEC, LOGP, true>(acc, wm, m, child, params, cids, pids, ebase, ne, bs, 0, p0, kq,
+                                                  jc, col, batch);
+        int64_t c0 = KCMAX;
+        for (; c0 + KCMAX <= ne; c0 += KCMAX)
+            load_fold<MT, KSMAX, NT, VEC, LOGP, false>(acc, wm, m, child, params, cids, pids, ebase, ne, bs, c0, p0,
+                                                       kq, jc, col, batch);
+        const int64_t rest = ne - c0;
+        if (rest > 16)
+            load_fold<MT, KSMAX, NT, VEC, LOGP, false>(acc, wm, m, child, params, cids, pids, ebase, ne, bs, c0, p0,
+                                                       kq, jc, col, batch);
+        else if (rest > 8)
+            load_fold<MT, 4, NT, VEC, LOGP, false>(acc, wm, m, child, params, cids, pids, ebase, ne, bs, c0, p0, kq,
+                                                   jc, col, batch);
+        else if (rest > 0)
+            load_fold<MT, 2, NT, VEC, LOGP, false>(acc, wm, m, child, params, cids, pids, ebase, ne, bs, c0, p0, kq,
+                                                   jc, col, batch);
     }
 
     // D layout: lane l holds rows p0 + 16*mt + 4*kq + r.  Their weight maxima
@@ -303,8 +317,11 @@ __global__ __launch_bounds__(64) void blocked_mfma_kernel(float* __restrict__ no
     }
 }
 
-// Parents per product row group: 16, 32 or 64.
-static int blocked_mt(int64_t bs) { return bs <= 16 ? 1 : bs <= 32 ? 2 : 4; }
+// Parents per product row group: 16, 32 or 64.  Groups of 64 suit one chunk
+// of edges (bs = 64, ne = 32: 197 us against 211 with two groups of 32); with
+// several chunks their larger register set costs occupancy (bs = 64, ne = 64:
+// 475 us against 401), so those take groups of 32.
+static int blocked_mt(int64_t bs, int64_t ne) { return bs <= 16 ? 1 : bs <= 32 || ne > KCMAX ? 2 : 4; }
 
 template <int MT, int NK, int NT, bool MULTI, bool VEC, bool LOGP>
 static void launch_k(float* node_mars, const float* child, const float* params, const int64_t* nids,
@@ -347,7 +364,7 @@ template <bool VEC, bool LOGP>
 static void launch_vec_log(float* node_mars, const float* child, const float* params, const int64_t* nids,
                            const int64_t* cids, const int64_t* pids, int64_t nblocks, int64_t ne, int64_t bs,
                            int64_t batch, hipStream_t st) {
-    switch (blocked_mt(bs)) {
+    switch (blocked_mt(bs, ne)) {
         case 1: launch_mt<1, VEC, LOGP>(node_mars, child, params, nids, cids, pids, nblocks, ne, bs, batch, st); break;
         case 2: launch_mt<2, VEC, LOGP>(node_mars, child, params, nids, cids, pids, nblocks, ne, bs, batch, st); break;
         default: launch_mt<4, VEC, LOGP>(node_mars, child, params, nids, cids, pids, nblocks, ne, bs, batch, st); break;
