@@ -379,9 +379,24 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
         params = torch.rand(nbk * ne * bs, device=dev, generator=gen) + 1e-3
         nm = torch.empty(nbk * bs, batch, device=dev)
         fbytes = nbk * ne * batch * 4 + nbk * bs * batch * 4 + nbk * ne * 16 + nbk * ne * bs * 4
+        # fp32 runs as a matrix product on MFMA; Q16 keeps the reference's
+        # per-parent edge-thread tree (bit-exact).  per_parent_us: the same fp32
+        # layer expanded to one CSR node per parent, through the per-parent
+        # gather kernel (the reference's computation shape).
+        pos = torch.arange(bs, device=dev)
+        x_cid = cids[:, None, :].expand(nbk, bs, ne).reshape(-1).to(torch.int32).contiguous()
+        x_lp = torch.log(params[(pids[:, None, :] + pos[None, :, None]).reshape(-1)]).contiguous()
+        x_off = torch.arange(0, nbk * bs * ne + 1, ne, device=dev, dtype=torch.int64)
+        x_out = torch.empty(nbk * bs, batch, device=dev)
+        ms_pp = _time_calls(torch, stream, lambda i: ext.sparse_csr_forward(em, x_off, x_cid, x_lp, out=x_out), 1,
+                            max(5, iters // 5))
         for fn, tag in [(ext.sparse_forward_float, "fp32"), (ext.sparse_forward_q16, "q16")]:
             ms = _time_calls(torch, stream, lambda i: fn(nm, em, params, nids, cids, pids, bs), 1, max(5, iters // 5))
-            rec(f"C5_blocked_{tag}_8192x32_e32_b512", ms, fbytes, nnz=nbk * bs * ne)
+            extra = {"per_parent_us": round(ms_pp * 1e3, 1)} if tag == "fp32" else {}
+            rec(f"C5_blocked_{tag}_8192x32_e32_b512", ms, fbytes, nnz=nbk * bs * ne, **extra)
+        ext.sparse_forward_float(nm, em, params, nids, cids, pids, bs)
+        assert torch.allclose(nm, x_out, rtol=1e-5, atol=1e-5), "block-layout product form mismatch"
+        del x_cid, x_lp, x_out
         ext.sparse_forward_float(nm, em, params, nids, cids, pids, bs)
         nf = torch.rand(nbk * bs, batch, device=dev, generator=gen)
         ef = torch.zeros(nel, batch, device=dev)
