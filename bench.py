@@ -411,11 +411,12 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
                                                                               pids, bs, plan=plan), 1, max(5, iters // 5))
         ms_np = _time_calls(torch, stream, lambda i: ext.sparse_blocked_backward(nf, ef, nm, em, params, pf, nids, cids,
                                                                                  pids, bs), 1, max(5, iters // 5))
-        # bytes of the flows kernel alone (the call adds the log-weight gather
-        # before it and element_flows.add_ / index_add_ after it): per expanded
-        # edge the parent's flow and mar rows and 16 B of edge data, per
-        # element row one read of element_mars and one write of its gradient
-        bbytes = 2 * nbk * bs * ne * batch * 4 + 2 * nel * batch * 4 + nbk * bs * ne * 16
+        # algorithmic bytes of the whole call: node_flows and node_mars once,
+        # each block's child rows once, element_flows read and written, the
+        # weights read and param_flows read and written, the edge metadata
+        # (the edge-flow workspace's round trip is the kernels' own traffic)
+        bbytes = (2 * nbk * bs * batch * 4 + nbk * ne * batch * 4 + 2 * nel * batch * 4 + 3 * nbk * ne * bs * 4
+                  + nbk * ne * 16)
         rec("C5_blocked_bwd_fp32_8192x32_e32_b512", ms, bbytes, nnz=nbk * bs * ne,
             without_plan_us=round(ms_np * 1e3, 1), plan_build_ms=round(plan_ms, 2))
         del em, nm, nf, ef, pf, plan

@@ -1,0 +1,649 @@
+// Backward ("flows") of the pyjuice block-layout fp32 sum layer, as products
+// on the matrix cores (gfx950).  The reference has no sparse backward; this
+// is the derivative of its block-layout forward (experiment_pyjuice/
+// sparse_float_kernel.cu:40-105).  For node block j, parent p (node
+// n = nids[j] + p), edge e (child c = cids[j, e], weight
+// w[p, e] = params[pids[j, e] + p], floored at 1e-45 or given as a log) and
+// batch column b, with g = node_flows, o = node_mars (the forward's output)
+// and x = element_mars:
+//     T[p, e, b] = g[n, b] * w[p, e] * exp(x[c, b] - o[n, b])   (0 where o = -inf)
+//     edge flow   F[j, e, b] = sum over p of T
+//     param flow  P[p, e]    = sum over b of T,  param_flows[pids[j, e] + p] += P
+//     element_flows[c, b]   += sum of F[j, e, b] over the block edges (j, e) into c.
+// For any per-column reference m_b and per-row reference W_p,
+//     T = A[p, e] * X[e, b] * R[p, b],  A = w / W,  X = exp(x - m),
+//     R = g * exp(log W + m - o),
+// so F = X .* (A^T R) is a product over parents and P = A .* (R X^T) a
+// product over the batch.  Each kernel takes m and W as the maxima over the
+// 32-edge chunk it works on, so A, X <= 1, and R <= 2^24 |g| wherever
+// log W + m - o <= 16.6.  Pairs (p, b) past that bound (a parent far below the
+// scale of its heavy children, or non-finite values) are left out of the
+// product and their terms computed one by one as T = g * exp(lw + x - o).
+// A term lost to fp32 underflow in the product is below 2^-102 |g|.
+//
+// Three kernels: edge flows (one wave per block, edge chunk and 64-column
+// tile, the parents as the product's K), parameter flows (one wave per block,
+// edge chunk and parent group, the batch as K, the sums added to param_flows
+// once per (p, e)), and element flows (one wave per element row, its block
+// edges summed in a fixed order through the transposed structure): the result
+// does not depend on scheduling, except that parameters shared by several
+// (block, parent, edge) triples receive their sums in any order.
+#include <math.h>
+#include <stdint.h>
+
+#include "../../include/fuselse_amd.h"
+#include "fl_status.hpp"
+#include "lse_common.hpp"
+
+namespace fl {
+namespace sparse {
+
+namespace {
+
+constexpr int CE = 32;          // edges per chunk
+constexpr float kRMax = 16.6f;  // largest log W + m - o taken by the product
+
+__device__ __forceinline__ float xor16(float v) { return exact_xor<16>(v); }
+__device__ __forceinline__ float xor32(float v) { return exact_xor<32>(v); }
+__device__ __forceinline__ float lane_read(float v, int src) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src * 4, __builtin_bit_cast(int, v)));
+}
+// maximum over the 16 lanes of a row (lanes 16*i .. 16*i + 15)
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, reduce_partner<1>(v));
+    v = fmaxf(v, reduce_partner<2>(v));
+    v = fmaxf(v, reduce_partner<4>(v));
+    return fmaxf(v, reduce_partner<8>(v));
+}
+
+template <bool LOGP>
+__device__ __forceinline__ float weight_term(float w) {
+    return LOGP ? w : fmaxf(w, 1e-45f);
+}
+template <bool LOGP>
+__device__ __forceinline__ float log_weight(float w) {
+    return LOGP ? w : logf(fmaxf(w, 1e-45f));
+}
+
+// Four consecutive columns col .. col + 3 of a row; columns past the batch
+// read `fill`.  With VEC, col is a multiple of 4 and rows are 16-byte aligned.
+template <bool VEC>
+__device__ __forceinline__ void ld4(const float* __restrict__ row, int64_t col, int64_t batch, float fill,
+                                    float (&v)[4]) {
+    if constexpr (VEC) {
+        const bool cv = col < batch;
+        const f32x4 t = *reinterpret_cast<const f32x4*>(row + (cv ? col : 0));
+        v[0] = cv ? t.x : fill;
+        v[1] = cv ? t.y : fill;
+        v[2] = cv ? t.z : fill;
+        v[3] = cv ? t.w : fill;
+    } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const bool cv = col + u < batch;
+            const float t = row[cv ? col + u : 0];
+            v[u] = cv ? t : fill;
+        }
+    }
+}
+
+// R = g * exp(lw + m - o) for one (p, b); `left` when the pair must take the
+// one-by-one terms, 0 when the pair contributes nothing (o = -inf, padding).
+__device__ __forceinline__ float r_factor(float lw, float m, float o, float g, bool valid, bool& left) {
+    const float ex = lw + m - o;
+    const float r = g * fexp2(ex * kLog2e);
+    const bool dead = !valid || o == -kInf;
+    const bool ok = ex <= kRMax && __builtin_isfinite(r);
+    left = !dead && !ok;
+    return dead || !ok ? 0.0f : r;
+}
+
+// XCD-contiguous logical id (physical workgroup w runs on XCD w % 8).
+__device__ __forceinline__ int64_t logical_id(int64_t id0) {
+    const int64_t per_xcd = gridDim.x / 8;
+    return id0 + (int64_t)(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+}
+
+}  // namespace
+
+// Edge flows F[j, e, b] for edges c0 .. c0 + 16*ET - 1 and columns b0 .. b0 + 63.
+// Product Z[e, b] = sum_p A[p, e] R[p, b]: lane l supplies A[e = c0 + 16*et + l%16]
+// [p = pc0 + 4*ks + l/16] and R[p][b = b0 + 4*(l%16) + u] (N-tile u) and holds
+// Z[e = c0 + 16*et + 4*(l/16) + r][b0 + 4*(l%16) + u], the same cells as its
+// 16-byte vectors of x, so F = X .* Z needs no exchange.  KP: K-steps per
+// parent chunk.
+template <int ET, int KP, bool VEC, bool LOGP>
+__global__ __launch_bounds__(64) void blocked_bwd_edges(float* __restrict__ edge_flows, const float* __restrict__ gf,
+                                                        const float* __restrict__ om, const float* __restrict__ xm,
+                                                        const float* __restrict__ params,
+                                                        const int64_t* __restrict__ nids,
+                                                        const int64_t* __restrict__ cids,
+                                                        const int64_t* __restrict__ pids, int64_t ne, int64_t bs,
+                                                        int64_t batch, int64_t ctiles, int64_t chunks, int64_t items,
+                                                        int64_t id0) {
+    __shared__ float ex[16 * ET][64];  // one-by-one terms: [edge - c0][column - b0]
+    const int64_t id = logical_id(id0);
+    if (id >= items) return;
+    const int64_t ct = id % ctiles;
+    const int64_t jc_ = id / ctiles;
+    const int64_t c = jc_ % chunks;
+    const int64_t j = jc_ / chunks;
+    const int l = lane_id();
+    const int kq = l >> 4;
+    const int jc = l & 15;
+    const int64_t b0 = ct * 64;
+    const int64_t col = b0 + 4 * jc;
+    const int64_t c0 = c * CE;
+    const int64_t ebase = j * ne;
+    const int64_t nrow0 = nids[j];
+
+    // x at the lane's output cells; edges past ne read -inf, columns past the batch 0
+    float xv[ET][4][4];
+#pragma unroll
+    for (int et = 0; et < ET; ++et)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t e = c0 + 16 * et + 4 * kq + r;
+            const bool ev = e < ne;
+            float v[4];
+            ld4<VEC>(xm + cids[ebase + (ev ? e : ne - 1)] * batch, col, batch, 0.0f, v);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) xv[et][r][u] = ev ? v[u] : -kInf;
+        }
+    float m[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        float mu = xv[0][0][u];
+#pragma unroll
+        for (int et = 0; et < ET; ++et)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mu = fmaxf(mu, xv[et][r][u]);
+        mu = fmaxf(mu, xor16(mu));
+        m[u] = fmaxf(mu, xor32(mu));
+    }
+#pragma unroll
+    for (int et = 0; et < ET; ++et)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                xv[et][r][u] = __builtin_isfinite(m[u]) ? fexp2((xv[et][r][u] - m[u]) * kLog2e) : 0.0f;
+
+    // the A operand's edges c0 + 16*et + jc
+    int64_t qa[ET];
+    bool eva[ET];
+#pragma unroll
+    for (int et = 0; et < ET; ++et) {
+        const int64_t e = c0 + 16 * et + jc;
+        eva[et] = e < ne;
+        qa[et] = pids[ebase + (eva[et] ? e : ne - 1)];
+    }
+
+    f32x4 z[ET][4];
+#pragma unroll
+    for (int et = 0; et < ET; ++et)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) z[et][u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    bool any_left = false;
+
+    for (int64_t pc0 = 0; pc0 < bs; pc0 += 4 * KP) {
+        float a[KP][ET], rr[KP][4];
+        uint32_t left = 0;  // bit 4*ks + u
+#pragma unroll
+        for (int ks = 0; ks < KP; ++ks) {
+            const int64_t p = pc0 + 4 * ks + kq;
+            const bool pv = p < bs;
+            const int64_t pcl = pv ? p : bs - 1;
+            float wv[ET];
+#pragma unroll
+            for (int et = 0; et < ET; ++et) {
+                const float w = weight_term<LOGP>(params[qa[et] + pcl]);
+                wv[et] = eva[et] && pv ? w : (LOGP ? -kInf : 0.0f);
+            }
+            float wm = wv[0];
+#pragma unroll
+            for (int et = 1; et < ET; ++et) wm = fmaxf(wm, wv[et]);
+            wm = row16_max(wm);  // over the chunk's edges
+#pragma unroll
+            for (int et = 0; et < ET; ++et)
+                a[ks][et] = !pv ? 0.0f
+                            : LOGP ? (wm == -kInf ? 0.0f : fexp2((wv[et] - wm) * kLog2e))
+                                   : wv[et] / wm;
+            const float lwm = LOGP ? wm : logf(wm);
+            float ov[4], gv[4];
+            ld4<VEC>(om + (nrow0 + pcl) * batch, col, batch, -kInf, ov);
+            ld4<VEC>(gf + (nrow0 + pcl) * batch, col, batch, 0.0f, gv);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                bool lf;
+                rr[ks][u] = r_factor(lwm, m[u], ov[u], gv[u], pv, lf);
+                left |= (uint32_t)lf << (4 * ks + u);
+            }
+        }
+#pragma unroll
+        for (int ks = 0; ks < KP; ++ks)
+#pragma unroll
+            for (int et = 0; et < ET; ++et)
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    z[et][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[ks][et], rr[ks][u], z[et][u], 0, 0, 0);
+
+        if (__ballot(left != 0)) {
+            if (!any_left) {
+#pragma unroll
+                for (int et = 0; et < ET; ++et)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) ex[16 * et + 4 * kq + r][4 * jc + u] = 0.0f;
+                any_left = true;
+                // one wave: its LDS operations complete in order
+                __builtin_amdgcn_wave_barrier();
+            }
+            // One parent row of each quad at a time, so the lanes writing
+            // ex hold different columns; a lane takes its pairs in order.
+            for (int kk = 0; kk < 4; ++kk) {
+                if (kq == kk) {
+                    uint32_t lf = left;
+                    while (lf) {
+                        const int bit = __builtin_ctz(lf);
+                        lf &= lf - 1;
+                        const int64_t p = pc0 + 4 * (bit >> 2) + kk;
+                        const int cu = 4 * jc + (bit & 3);
+                        const int64_t n = nrow0 + p;
+                        const float gg = gf[n * batch + b0 + cu];
+                        const float oo = om[n * batch + b0 + cu];
+                        for (int ee = 0; ee < 16 * ET && c0 + ee < ne; ++ee) {
+                            const int64_t e = c0 + ee;
+                            const float lw = log_weight<LOGP>(params[pids[ebase + e] + p]);
+                            const float xx = xm[cids[ebase + e] * batch + b0 + cu];
+                            ex[ee][cu] += gg * fexp2((lw + xx - oo) * kLog2e);
+                        }
+                    }
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+
+    // F = X .* Z (+ one-by-one terms) at rows c0 + 16*et + 4*kq + r
+#pragma unroll
+    for (int et = 0; et < ET; ++et)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t e = c0 + 16 * et + 4 * kq + r;
+            if (e >= ne) continue;
+            float res[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float zz = z[et][u][r];
+                res[u] = zz == 0.0f ? 0.0f : xv[et][r][u] * zz;
+                if (any_left) res[u] += ex[16 * et + 4 * kq + r][4 * jc + u];
+            }
+            float* orow = edge_flows + (ebase + e) * batch;
+            if constexpr (VEC) {
+                if (col < batch) *reinterpret_cast<f32x4*>(orow + col) = f32x4{res[0], res[1], res[2], res[3]};
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (col + u < batch) orow[col + u] = res[u];
+            }
+        }
+}
+
+// Parameter flows for parents p0 .. p0 + 16*MT - 1 and edges c0 .. c0 + 16*ET - 1.
+// Product G[p, e] = sum_b R[p, b] X[e, b] over the whole batch, 4*CW columns
+// per pass: lane l supplies R[p = p0 + 16*pt + l%16][b = b0 + CW*(l/16) + ks]
+// and X[e = c0 + 16*et + l%16][same b] (its CW columns are CW/4 vectors of
+// one row) and holds G[p0 + 16*pt + 4*(l/16) + r][c0 + 16*et + l%16].
+template <int MT, int ET, int CW, bool VEC, bool LOGP>
+__global__ __launch_bounds__(64) void blocked_bwd_params(float* __restrict__ param_flows, const float* __restrict__ gf,
+                                                         const float* __restrict__ om, const float* __restrict__ xm,
+                                                         const float* __restrict__ params,
+                                                         const int64_t* __restrict__ nids,
+                                                         const int64_t* __restrict__ cids,
+                                                         const int64_t* __restrict__ pids, int64_t ne, int64_t bs,
+                                                         int64_t batch, int64_t pgroups, int64_t chunks, int64_t items,
+                                                         int64_t id0) {
+    __shared__ float ex[16 * MT][16 * ET];  // one-by-one terms: [parent - p0][edge - c0]
+    const int64_t id = logical_id(id0);
+    if (id >= items) return;
+    const int64_t g = id % pgroups;
+    const int64_t jc_ = id / pgroups;
+    const int64_t c = jc_ % chunks;
+    const int64_t j = jc_ / chunks;
+    const int l = lane_id();
+    const int kq = l >> 4;
+    const int jc = l & 15;
+    const int64_t p0 = g * 16 * MT;
+    const int64_t c0 = c * CE;
+    const int64_t ebase = j * ne;
+    const int64_t nrow0 = nids[j];
+
+    // row maxima of the weights over the chunk's edges, for rows p0 + 16*pt + jc
+    float wmx[MT], lwm[MT];
+#pragma unroll
+    for (int pt = 0; pt < MT; ++pt) {
+        const int64_t p = p0 + 16 * pt + jc;
+        const bool pv = p < bs;
+        const int64_t pcl = pv ? p : bs - 1;
+        float wm = LOGP ? -kInf : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4 * ET; ++i) {
+            const int64_t e = c0 + kq + 4 * i;
+            const bool ev = e < ne;
+            const float w = weight_term<LOGP>(params[pids[ebase + (ev ? e : ne - 1)] + pcl]);
+            wm = ev ? fmaxf(wm, w) : wm;
+        }
+        wm = fmaxf(wm, xor16(wm));
+        wmx[pt] = fmaxf(wm, xor32(wm));
+        lwm[pt] = LOGP ? wmx[pt] : logf(wmx[pt]);
+    }
+    const float* xrow[ET];
+    bool evb[ET];
+#pragma unroll
+    for (int et = 0; et < ET; ++et) {
+        const int64_t e = c0 + 16 * et + jc;
+        evb[et] = e < ne;
+        xrow[et] = xm + cids[ebase + (evb[et] ? e : ne - 1)] * batch;
+    }
+    const float* orow[MT];
+    const float* grow[MT];
+    bool pvr[MT];
+#pragma unroll
+    for (int pt = 0; pt < MT; ++pt) {
+        const int64_t p = p0 + 16 * pt + jc;
+        pvr[pt] = p < bs;
+        const int64_t n = nrow0 + (pvr[pt] ? p : bs - 1);
+        orow[pt] = om + n * batch;
+        grow[pt] = gf + n * batch;
+    }
+
+    f32x4 acc[MT][ET];
+#pragma unroll
+    for (int pt = 0; pt < MT; ++pt)
+#pragma unroll
+        for (int et = 0; et < ET; ++et) acc[pt][et] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    bool any_left = false;
+
+    for (int64_t b0 = 0; b0 < batch; b0 += 4 * CW) {
+        const int64_t cb = b0 + CW * kq;  // K-step ks takes column cb + ks
+        float xv[ET][CW];
+#pragma unroll
+        for (int et = 0; et < ET; ++et)
+#pragma unroll
+            for (int q = 0; q < CW / 4; ++q) {
+                float v[4];
+                ld4<VEC>(xrow[et], cb + 4 * q, batch, 0.0f, v);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) xv[et][4 * q + u] = evb[et] ? v[u] : -kInf;
+            }
+        float m[CW];
+#pragma unroll
+        for (int i = 0; i < CW; ++i) {
+            float mi = xv[0][i];
+#pragma unroll
+            for (int et = 1; et < ET; ++et) mi = fmaxf(mi, xv[et][i]);
+            m[i] = row16_max(mi);  // over the chunk's edges
+        }
+#pragma unroll
+        for (int et = 0; et < ET; ++et)
+#pragma unroll
+            for (int i = 0; i < CW; ++i)
+                xv[et][i] = __builtin_isfinite(m[i]) ? fexp2((xv[et][i] - m[i]) * kLog2e) : 0.0f;
+        float rr[MT][CW];
+        uint32_t left[MT];  // bit i: column cb + i
+#pragma unroll
+        for (int pt = 0; pt < MT; ++pt) {
+            left[pt] = 0;
+#pragma unroll
+            for (int q = 0; q < CW / 4; ++q) {
+                float ov[4], gv[4];
+                ld4<VEC>(orow[pt], cb + 4 * q, batch, -kInf, ov);
+                ld4<VEC>(grow[pt], cb + 4 * q, batch, 0.0f, gv);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    bool lf;
+                    rr[pt][4 * q + u] = r_factor(lwm[pt], m[4 * q + u], ov[u], gv[u], pvr[pt], lf);
+                    left[pt] |= (uint32_t)lf << (4 * q + u);
+                }
+            }
+        }
+#pragma unroll
+        for (int ks = 0; ks < CW; ++ks)
+#pragma unroll
+            for (int pt = 0; pt < MT; ++pt)
+#pragma unroll
+                for (int et = 0; et < ET; ++et)
+                    acc[pt][et] = __builtin_amdgcn_mfma_f32_16x16x4f32(rr[pt][ks], xv[et][ks], acc[pt][et], 0, 0, 0);
+
+        bool anyl = false;
+#pragma unroll
+        for (int pt = 0; pt < MT; ++pt) anyl = anyl || left[pt] != 0;
+        if (__ballot(anyl)) {
+            if (!any_left) {
+#pragma unroll
+                for (int pt = 0; pt < MT; ++pt)
+#pragma unroll
+                    for (int et = 0; et < ET; ++et)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) ex[16 * pt + 4 * kq + r][16 * et + jc] = 0.0f;
+                any_left = true;
+                __builtin_amdgcn_wave_barrier();
+            }
+            // One column quarter at a time, so the lanes writing ex hold
+            // different parent rows; a lane takes its pairs in order.
+            for (int kk = 0; kk < 4; ++kk) {
+                if (kq == kk) {
+#pragma unroll
+                    for (int pt = 0; pt < MT; ++pt) {
+                        uint32_t lf = left[pt];
+                        while (lf) {
+                            const int i = __builtin_ctz(lf);
+                            lf &= lf - 1;
+                            const int64_t p = p0 + 16 * pt + jc;
+                            const int64_t b = cb + i;
+                            const int64_t n = nrow0 + p;
+                            const float gg = gf[n * batch + b];
+                            const float oo = om[n * batch + b];
+                            for (int ee = 0; ee < 16 * ET && c0 + ee < ne; ++ee) {
+                                const int64_t e = c0 + ee;
+                                const float lw = log_weight<LOGP>(params[pids[ebase + e] + p]);
+                                const float xx = xm[cids[ebase + e] * batch + b];
+                                ex[16 * pt + jc][ee] += gg * fexp2((lw + xx - oo) * kLog2e);
+                            }
+                        }
+                    }
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+
+    // param_flows[pids[j, e] + p] += (w / W) G + one-by-one terms, rows p0 + 16*pt + 4*kq + r
+#pragma unroll
+    for (int pt = 0; pt < MT; ++pt) {
+        float wr[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) wr[r] = lane_read(wmx[pt], 4 * kq + r);
+#pragma unroll
+        for (int et = 0; et < ET; ++et) {
+            const int64_t e = c0 + 16 * et + jc;
+            if (e >= ne) continue;
+            const int64_t q = pids[ebase + e];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t p = p0 + 16 * pt + 4 * kq + r;
+                if (p >= bs) continue;
+                const float w = weight_term<LOGP>(params[q + p]);
+                const float aw = LOGP ? (wr[r] == -kInf ? 0.0f : fexp2((w - wr[r]) * kLog2e)) : w / wr[r];
+                const float gsum = acc[pt][et][r];
+                float v = gsum == 0.0f ? 0.0f : aw * gsum;
+                if (any_left) v += ex[16 * pt + 4 * kq + r][16 * et + jc];
+                if (v != 0.0f)
+                    __hip_atomic_fetch_add(param_flows + q + p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    }
+}
+
+// element_flows[c, b] += sum of edge_flows rows csc_edges[csc_offsets[c] ..
+// csc_offsets[c + 1]) in that order: one wave per element row, 256 columns
+// per pass.
+template <bool VEC>
+__global__ __launch_bounds__(256) void blocked_bwd_elements(float* __restrict__ element_flows,
+                                                            const float* __restrict__ edge_flows,
+                                                            const int64_t* __restrict__ csc_offsets,
+                                                            const int32_t* __restrict__ csc_edges, int64_t nel,
+                                                            int64_t batch) {
+    const int64_t c = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (c >= nel) return;
+    const int64_t k0 = csc_offsets[c];
+    const int64_t k1 = csc_offsets[c + 1];
+    if (k0 >= k1) return;
+    const int l = lane_id();
+    float* er = element_flows + c * batch;
+    for (int64_t b0 = 0; b0 < batch; b0 += 256) {
+        const int64_t col = b0 + 4 * l;
+        float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int64_t k = k0; k < k1; ++k) {
+            float v[4];
+            ld4<VEC>(edge_flows + (int64_t)csc_edges[k] * batch, col, batch, 0.0f, v);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) s[u] += v[u];
+        }
+        float cur[4];
+        ld4<VEC>(er, col, batch, 0.0f, cur);
+        if constexpr (VEC) {
+            if (col < batch) *reinterpret_cast<f32x4*>(er + col) = f32x4{cur[0] + s[0], cur[1] + s[1], cur[2] + s[2], cur[3] + s[3]};
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (col + u < batch) er[col + u] = cur[u] + s[u];
+        }
+    }
+}
+
+namespace {
+
+constexpr int64_t kMaxGroups = (int64_t)1 << 30;  // workgroups per launch, a multiple of 8
+// Columns per lane per pass of the parameter-flow product, and parent K-steps
+// per chunk of the edge-flow product (at most).  Measured at 8192 blocks of
+// 32 parents, 32 edges, batch 512: 16 columns and 8 K-steps 1280 us; 8 and 4
+// 1084 us (4 waves per SIMD instead of 2 in both kernels); 4 columns 1191 us;
+// 2 K-steps as 4.
+constexpr int kParamCW = 8;
+constexpr int kEdgeKPMax = 4;
+
+template <int ET, int KP, bool VEC, bool LOGP>
+void launch_edges(float* edge_flows, const float* gf, const float* om, const float* xm, const float* params,
+                  const int64_t* nids, const int64_t* cids, const int64_t* pids, int64_t nb, int64_t ne, int64_t bs,
+                  int64_t batch, hipStream_t st) {
+    const int64_t ctiles = (batch + 63) / 64;
+    const int64_t chunks = (ne + CE - 1) / CE;
+    const int64_t items = nb * chunks * ctiles;
+    for (int64_t id0 = 0; id0 < items; id0 += kMaxGroups) {
+        const int64_t n = items - id0 < kMaxGroups ? items - id0 : kMaxGroups;
+        blocked_bwd_edges<ET, KP, VEC, LOGP><<<dim3((unsigned)((n + 7) / 8 * 8)), dim3(64), 0, st>>>(
+            edge_flows, gf, om, xm, params, nids, cids, pids, ne, bs, batch, ctiles, chunks, items, id0);
+    }
+}
+
+template <int MT, int ET, bool VEC, bool LOGP>
+void launch_params(float* param_flows, const float* gf, const float* om, const float* xm, const float* params,
+                   const int64_t* nids, const int64_t* cids, const int64_t* pids, int64_t nb, int64_t ne, int64_t bs,
+                   int64_t batch, hipStream_t st) {
+    const int64_t pgroups = (bs + 16 * MT - 1) / (16 * MT);
+    const int64_t chunks = (ne + CE - 1) / CE;
+    const int64_t items = nb * chunks * pgroups;
+    for (int64_t id0 = 0; id0 < items; id0 += kMaxGroups) {
+        const int64_t n = items - id0 < kMaxGroups ? items - id0 : kMaxGroups;
+        blocked_bwd_params<MT, ET, kParamCW, VEC, LOGP><<<dim3((unsigned)((n + 7) / 8 * 8)), dim3(64), 0, st>>>(
+            param_flows, gf, om, xm, params, nids, cids, pids, ne, bs, batch, pgroups, chunks, items, id0);
+    }
+}
+
+template <int ET, bool VEC, bool LOGP>
+void launch_et(float* edge_flows, float* param_flows, const float* gf, const float* om, const float* xm,
+               const float* params, const int64_t* nids, const int64_t* cids, const int64_t* pids, int64_t nb,
+               int64_t ne, int64_t bs, int64_t batch, hipStream_t st) {
+    // parents per K chunk of the edge-flow product: 4 * KP
+    if (bs <= 4)
+        launch_edges<ET, 1, VEC, LOGP>(edge_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, st);
+    else if (bs <= 8)
+        launch_edges<ET, 2, VEC, LOGP>(edge_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, st);
+    else if (bs <= 16)
+        launch_edges<ET, 4, VEC, LOGP>(edge_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, st);
+    else
+        launch_edges<ET, kEdgeKPMax, VEC, LOGP>(edge_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch,
+                                                st);
+    // parents per group of the parameter-flow product: 16 * MT
+    if (bs <= 16)
+        launch_params<1, ET, VEC, LOGP>(param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, st);
+    else
+        launch_params<2, ET, VEC, LOGP>(param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, st);
+}
+
+template <bool VEC, bool LOGP>
+void launch_all(float* edge_flows, float* param_flows, const float* gf, const float* om, const float* xm,
+                const float* params, const int64_t* nids, const int64_t* cids, const int64_t* pids, int64_t nb,
+                int64_t ne, int64_t bs, int64_t batch, hipStream_t st) {
+    if (ne <= 16)
+        launch_et<1, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, st);
+    else
+        launch_et<2, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, st);
+}
+
+}  // namespace
+
+}  // namespace sparse
+}  // namespace fl
+
+using namespace fl;
+
+extern "C" int fl_sparse_blocked_bwd(const float* node_flows, const float* node_mars, const float* element_mars,
+                                     const float* params, const int64_t* nids, const int64_t* cids,
+                                     const int64_t* pids, int64_t num_nblocks, int64_t num_edges, int64_t block_size,
+                                     int64_t batch, int params_are_log, const int64_t* csc_offsets,
+                                     const int32_t* csc_edges, int64_t num_elements, float* edge_flows,
+                                     float* element_flows, float* param_flows, void* stream) {
+    const char* name = "fl_sparse_blocked_bwd";
+    FL_CHECK(num_nblocks >= 0 && num_edges >= 0 && block_size >= 0 && batch >= 0 && num_elements >= 0,
+             "%s: negative size", name);
+    if (num_nblocks == 0 || num_edges == 0 || block_size == 0 || batch == 0) return ok();
+    FL_CHECK(node_flows && node_mars && element_mars && params && nids && cids && pids && csc_offsets && csc_edges &&
+                 edge_flows && element_flows && param_flows,
+             "%s: NULL pointer argument", name);
+    FL_CHECK(num_nblocks * num_edges < ((int64_t)1 << 31), "%s: block edges must be < 2^31", name);
+    const bool vec = (batch % 4 == 0) &&
+                     ((reinterpret_cast<uintptr_t>(node_flows) | reinterpret_cast<uintptr_t>(node_mars) |
+                       reinterpret_cast<uintptr_t>(element_mars) | reinterpret_cast<uintptr_t>(edge_flows) |
+                       reinterpret_cast<uintptr_t>(element_flows)) & 15) == 0;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const int64_t nb = num_nblocks, ne = num_edges, bs = block_size;
+    if (vec) {
+        if (params_are_log)
+            sparse::launch_all<true, true>(edge_flows, param_flows, node_flows, node_mars, element_mars, params, nids,
+                                           cids, pids, nb, ne, bs, batch, st);
+        else
+            sparse::launch_all<true, false>(edge_flows, param_flows, node_flows, node_mars, element_mars, params,
+                                            nids, cids, pids, nb, ne, bs, batch, st);
+    } else {
+        if (params_are_log)
+            sparse::launch_all<false, true>(edge_flows, param_flows, node_flows, node_mars, element_mars, params,
+                                            nids, cids, pids, nb, ne, bs, batch, st);
+        else
+            sparse::launch_all<false, false>(edge_flows, param_flows, node_flows, node_mars, element_mars, params,
+                                             nids, cids, pids, nb, ne, bs, batch, st);
+    }
+    if (num_elements > 0) {
+        const dim3 grid((unsigned)((num_elements + 3) / 4));
+        if (vec)
+            sparse::blocked_bwd_elements<true><<<grid, dim3(256), 0, st>>>(element_flows, edge_flows, csc_offsets,
+                                                                          csc_edges, num_elements, batch);
+        else
+            sparse::blocked_bwd_elements<false><<<grid, dim3(256), 0, st>>>(element_flows, edge_flows, csc_offsets,
+                                                                           csc_edges, num_elements, batch);
+    }
+    return launch_status(name);
+}

@@ -9,6 +9,8 @@ reference's drop-in (fuselse/gpu/autograd.py:6-61).
 
 from __future__ import annotations
 
+from typing import NamedTuple, Optional
+
 import torch
 
 from . import _lib
@@ -349,36 +351,45 @@ def sparse_forward_q16(node_mars, element_mars, params, nids, cids, pids, block_
     return _sparse_blocked(node_mars, element_mars, params, nids, cids, pids, block_size, True, params_are_log)
 
 
+class BlockedPlan(NamedTuple):
+    """The transposed structure of a block-layout sum layer (see
+    sparse_blocked_transpose)."""
+    csc_offsets: torch.Tensor   # int64 [num_elements + 1]
+    csc_edges: torch.Tensor     # int32 [nblocks * num_edges]: block edges j * num_edges + e, by child
+    csc_nodes: Optional[torch.Tensor]  # int32, block_size 1 only: node_mars row of each listed edge
+    param_ids: Optional[torch.Tensor]  # int64 [nblocks * num_edges], block_size 1 only: pids flattened
+
+
 def sparse_blocked_transpose(nids, cids, pids, block_size, num_elements):
-    """The transposed structure fl_sparse_csr_bwd walks for a block-layout sum
-    layer (the forward dispatcher's nids [nblocks], cids and pids [nblocks,
-    num_edges], int64): the layer expanded to one edge per (block j, position
-    p < block_size, edge e) in that order, and returned as (csc_offsets int64
-    [num_elements + 1], csc_edges int32 [nnz] with the expanded edges into
-    each element row in increasing order, csc_nodes int32 [nnz] with each of
-    those edges' node_mars row nids[j] + p, param_ids int64 [nnz] with each
-    expanded edge's parameter pids[j, e] + p).  Built with torch's sort on
-    the device; it depends on the layer only, so a caller that runs the layer
-    many times builds it once and passes it to sparse_blocked_backward."""
+    """The transposed structure sparse_blocked_backward walks for a block-layout
+    sum layer (the forward dispatcher's nids [nblocks], cids and pids
+    [nblocks, num_edges], int64): for each element row c, the block edges
+    j * num_edges + e with cids[j, e] = c, in increasing order.  Built with
+    torch's sort on the device; it depends on the layer only, so a caller that
+    runs the layer many times builds it once and passes it to
+    sparse_blocked_backward."""
     for name, t in (("nids", nids), ("cids", cids), ("pids", pids)):
         _check(t.is_cuda and t.dtype == torch.int64 and t.is_contiguous(), f"{name} must be a contiguous CUDA int64 tensor")
     _check(cids.dim() == 2 and pids.shape == cids.shape and nids.dim() == 1 and nids.size(0) == cids.size(0),
            "nids [nblocks], cids and pids [nblocks, num_edges] shapes disagree")
     nb, ne = cids.shape
     bs = int(block_size)
-    nnz = nb * bs * ne
-    _check(nnz < 2 ** 31 and num_elements < 2 ** 31, "edges and element rows must each be < 2^31")
+    _check(nb * ne < 2 ** 31 and nb * bs * ne < 2 ** 31 and num_elements < 2 ** 31,
+           "edges and element rows must each be < 2^31")
     dev = cids.device
-    pos = torch.arange(bs, device=dev)
-    node_rows = (nids[:, None] + pos[None, :]).reshape(-1)                      # [nb * bs]
-    child_ids = cids[:, None, :].expand(nb, bs, ne).reshape(-1)                 # [nnz], edge (j, p, e)
-    param_ids = (pids[:, None, :] + pos[None, :, None]).reshape(-1)             # [nnz]
+    child_ids = cids.reshape(-1)
     order = torch.sort(child_ids, stable=True).indices
     counts = torch.bincount(child_ids, minlength=num_elements)
     _check(counts.numel() == num_elements, "cids hold ids >= element_mars rows")
     csc_off = torch.zeros(num_elements + 1, dtype=torch.int64, device=dev)
     torch.cumsum(counts, 0, out=csc_off[1:])
-    return csc_off, order.to(torch.int32), node_rows[order // ne].to(torch.int32), param_ids
+    nodes = qids = None
+    if bs == 1:
+        # one parent per block: the block edges are the layer's edges, walked by
+        # the CSR flows kernel, which names each edge's node_mars row
+        nodes = nids[order // ne].to(torch.int32)
+        qids = pids.reshape(-1)
+    return BlockedPlan(csc_off, order.to(torch.int32), nodes, qids)
 
 
 def sparse_blocked_backward(node_flows, element_flows, node_mars, element_mars, params, param_flows, nids, cids, pids,
@@ -393,12 +404,12 @@ def sparse_blocked_backward(node_flows, element_flows, node_mars, element_mars, 
       element_flows[c, b] += the terms of the edges into c,
       param_flows[q]      += the terms of edge (j, p, e) summed over b.
     node_mars must hold this layer's forward output.  The reference has no
-    sparse backward.  The layer runs as one CSR node per (block, position)
-    through fl_sparse_csr_bwd, whose transposed structure names each edge's
-    node_mars row directly, so node_mars and node_flows are read in place.
-    plan: the result of sparse_blocked_transpose for this layer (built here
-    when None).  param_flows is accumulated with index_add_, whose order is
-    not fixed where several edges share a parameter.  Returns None."""
+    sparse backward.  block_size >= 2 runs fl_sparse_blocked_bwd (products on
+    the matrix cores, a workspace of nblocks * num_edges rows); block_size 1
+    runs the CSR flows kernel fl_sparse_csr_bwd over the same edges.  plan:
+    the result of sparse_blocked_transpose for this layer (built here when
+    None).  param_flows receives one add per (block, parent, edge), in any
+    order where several of them share a parameter.  Returns None."""
     _check(node_flows.is_cuda and element_flows.is_cuda and param_flows.is_cuda, "flows must be CUDA tensors")
     for t, nm in ((node_flows, "node_flows"), (element_flows, "element_flows"), (param_flows, "param_flows")):
         _check(t.dtype == torch.float32 and t.is_contiguous(), f"{nm} must be contiguous float32")
@@ -418,29 +429,37 @@ def sparse_blocked_backward(node_flows, element_flows, node_mars, element_mars, 
     _check(cids.dim() == 2 and pids.shape == cids.shape and nids.dim() == 1 and nids.size(0) == cids.size(0),
            "nids [nblocks], cids and pids [nblocks, num_edges] shapes disagree")
     nb, ne = cids.shape
-    nnz = nb * int(block_size) * ne
+    bs = int(block_size)
     num_el, batch = element_mars.shape
-    if nnz == 0 or batch == 0:
+    if nb * ne * bs == 0 or batch == 0:
         return None
-    _check(nnz < 2 ** 31 and num_el < 2 ** 31 and node_mars.size(0) < 2 ** 31,
+    _check(nb * bs * ne < 2 ** 31 and num_el < 2 ** 31 and node_mars.size(0) < 2 ** 31,
            "edges, element rows and node rows must each be < 2^31")
     if plan is None:
-        plan = sparse_blocked_transpose(nids, cids, pids, block_size, num_el)
+        plan = sparse_blocked_transpose(nids, cids, pids, bs, num_el)
     csc_off, csc_edge, csc_node, q = plan
     _check(csc_off.dtype == torch.int64 and csc_off.numel() == num_el + 1 and csc_edge.dtype == torch.int32
-           and csc_node.dtype == torch.int32 and q.dtype == torch.int64 and csc_edge.numel() == nnz
-           and csc_node.numel() == nnz and q.numel() == nnz, "plan does not fit this layer")
-    w = params.reshape(-1)[q]
-    logp = w if params_are_log else torch.log(torch.clamp_min(w, 1e-45))
-    logp = logp.contiguous()
-    grad_el = torch.empty_like(element_mars)
-    grad_lp = torch.empty_like(logp)
+           and csc_edge.numel() == nb * ne and (bs != 1 or (csc_node is not None and q is not None
+                                                             and csc_node.numel() == nb * ne and q.numel() == nb * ne)),
+           "plan does not fit this layer")
+    if bs == 1:
+        w = params.reshape(-1)[q]
+        logp = (w if params_are_log else torch.log(torch.clamp_min(w, 1e-45))).contiguous()
+        grad_el = torch.empty_like(element_mars)
+        grad_lp = torch.empty_like(logp)
+        with _on_device(element_mars):
+            _lib.call("fl_sparse_csr_bwd", element_mars.data_ptr(), node_mars.data_ptr(), node_flows.data_ptr(),
+                      logp.data_ptr(), csc_off.data_ptr(), csc_edge.data_ptr(), csc_node.data_ptr(), grad_el.data_ptr(),
+                      grad_lp.data_ptr(), num_el, batch, _stream(element_mars))
+        element_flows.add_(grad_el)
+        param_flows.view(-1).index_add_(0, q, grad_lp)
+        return None
+    edge_flows = torch.empty(nb * ne, batch, dtype=torch.float32, device=element_mars.device)
     with _on_device(element_mars):
-        _lib.call("fl_sparse_csr_bwd", element_mars.data_ptr(), node_mars.data_ptr(), node_flows.data_ptr(),
-                  logp.data_ptr(), csc_off.data_ptr(), csc_edge.data_ptr(), csc_node.data_ptr(), grad_el.data_ptr(),
-                  grad_lp.data_ptr(), num_el, batch, _stream(element_mars))
-    element_flows.add_(grad_el)
-    param_flows.view(-1).index_add_(0, q, grad_lp)
+        _lib.call("fl_sparse_blocked_bwd", node_flows.data_ptr(), node_mars.data_ptr(), element_mars.data_ptr(),
+                  params.data_ptr(), nids.data_ptr(), cids.data_ptr(), pids.data_ptr(), nb, ne, bs, batch,
+                  int(params_are_log), csc_off.data_ptr(), csc_edge.data_ptr(), num_el, edge_flows.data_ptr(),
+                  element_flows.data_ptr(), param_flows.data_ptr(), _stream(element_mars))
     return None
 
 

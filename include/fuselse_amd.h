@@ -179,6 +179,34 @@ int fl_sparse_csr_bwd(const float* child, const float* out, const float* grad_ou
                       const int64_t* csc_offsets, const int32_t* csc_edges, const int32_t* csc_nodes,
                       float* grad_child, float* grad_logparams, int64_t num_children, int64_t batch, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Block-layout backward ("flows") of fl_sparse_blocked_fwd in fp32 (the
+ * reference has no backward; this differentiates its block-layout forward,
+ * experiment_pyjuice/sparse_float_kernel.cu:40-105).  With node_mars the
+ * forward's output and node_flows the upstream flows, for block j, parent p
+ * (node n = nids[j] + p), edge e (child c = cids[j, e], parameter
+ * q = pids[j, e] + p) and column b:
+ *   term = node_flows[n, b] * w_q * exp(element_mars[c, b] - node_mars[n, b])
+ * (w_q = max(params[q], 1e-45), or exp(params[q]) with params_are_log; term
+ * = 0 where node_mars is -inf), and
+ *   edge_flows[j * num_edges + e, b] = sum over p of term   (written)
+ *   element_flows[c, b]            += sum of edge_flows rows into c
+ *   param_flows[q]                 += sum over b of term.
+ * edge_flows is a caller workspace of num_nblocks * num_edges rows of batch
+ * floats.  csc_offsets int64 [num_elements + 1] and csc_edges int32
+ * [num_nblocks * num_edges] list, for each element row, the block edges
+ * j * num_edges + e with cids[j, e] = c in increasing order.  Element flows
+ * are summed in that order; param_flows takes one atomic add per
+ * (block, parent, edge), so its order is free only where parameters are
+ * shared.
+ * ------------------------------------------------------------------------- */
+int fl_sparse_blocked_bwd(const float* node_flows, const float* node_mars, const float* element_mars,
+                          const float* params, const int64_t* nids, const int64_t* cids, const int64_t* pids,
+                          int64_t num_nblocks, int64_t num_edges, int64_t block_size, int64_t batch,
+                          int params_are_log, const int64_t* csc_offsets, const int32_t* csc_edges,
+                          int64_t num_elements, float* edge_flows, float* element_flows, float* param_flows,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -462,3 +462,127 @@ def test_blocked_product_form_log_weights_empty_first_chunk(cuda):
     want[rows] = vals
     assert np.isneginf(got[bs + 9]).all()
     np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# Block layout backward, block_size >= 2: fl_sparse_blocked_bwd (edge flows
+# and parameter flows as products on the matrix cores, element flows summed
+# in a fixed order), against the fp64 loops of the oracle with the node_mars
+# of the kernels' own forward.  Bound: 1e-5 of the sum of |terms| of each
+# entry plus fp32 rounding of the final add.
+# ---------------------------------------------------------------------------
+PRODUCT_BWD_CASES = [(2, 5, 64), (16, 16, 130), (32, 32, 512), (24, 33, 96), (48, 70, 64), (64, 7, 260),
+                     (9, 40, 1), (32, 3, 3), (128, 20, 64)]
+
+
+def _blocked_bwd_case(cuda, rng, nb, ne, bs, batch, nelem, log_params, special=False):
+    nids = (np.arange(nb) * (bs + 1)).astype(np.int64)
+    cids = rng.integers(0, nelem, (nb, ne)).astype(np.int64)
+    pids = (np.arange(nb * ne, dtype=np.int64) * bs).reshape(nb, ne)
+    params = (rng.random(nb * ne * bs) + 1e-3).astype(np.float32)
+    em = np.log(rng.random((nelem, batch)) + 1e-9).astype(np.float32)
+    return nids, cids, pids, params, em
+
+
+def _check_blocked_bwd(cuda, nids, cids, pids, params, em, bs, batch, log_params, nf=None, clamp=F32_FLOOR):
+    rng = np.random.default_rng(1)
+    nb, ne = cids.shape
+    nelem = em.shape[0]
+    nrows = int(nids.max()) + bs + 2
+    p_in = np.log(params).astype(np.float32) if log_params else params
+    d = {k: torch.from_numpy(v).to(cuda) for k, v in (("em", em), ("p", p_in), ("nids", nids), ("cids", cids),
+                                                      ("pids", pids))}
+    nm = torch.full((nrows, batch), -np.inf, device=cuda)
+    ext = _ext()
+    ext.sparse_forward_float(nm, d["em"], d["p"], d["nids"], d["cids"], d["pids"], bs, params_are_log=log_params)
+    if nf is None:
+        nf = rng.standard_normal((nrows, batch)).astype(np.float32)
+    ef0 = rng.standard_normal((nelem, batch)).astype(np.float32)
+    pf0 = rng.standard_normal(params.size).astype(np.float32)
+    ef, pf = torch.from_numpy(ef0).to(cuda), torch.from_numpy(pf0).to(cuda)
+    ext.sparse_blocked_backward(torch.from_numpy(nf).to(cuda), ef, nm, d["em"], d["p"], pf, d["nids"], d["cids"],
+                                d["pids"], bs, params_are_log=log_params)
+    nm64 = nm.cpu().numpy()
+    p_or = np.exp(p_in.astype(np.float64)) if log_params else params
+    kw = dict(clamp=0.0) if log_params else dict(clamp=clamp)
+    with np.errstate(divide="ignore"):
+        de, dp = O.sparse_blocked_bwd_fp64(nf, nm64, em, p_in if log_params else p_or, nids, cids, pids, bs,
+                                           params_are_log=log_params, **kw)
+        ae, ap = O.sparse_blocked_bwd_fp64(np.abs(nf), nm64, em, p_in if log_params else p_or, nids, cids, pids, bs,
+                                           params_are_log=log_params, **kw)
+    got_e, got_p = ef.cpu().numpy(), pf.cpu().numpy()
+    want_e, want_p = ef0 + de, pf0 + dp
+    bad_e = ~(np.abs(got_e - want_e) <= 1e-5 * ae + 2e-7 * np.abs(want_e) + 1e-30)
+    bad_p = ~(np.abs(got_p - want_p) <= 1e-5 * ap + 2e-7 * np.abs(want_p) + 1e-30)
+    assert not bad_e.any(), (np.argwhere(bad_e)[:5], got_e[bad_e][:5], want_e[bad_e][:5])
+    assert not bad_p.any(), (np.argwhere(bad_p)[:5], got_p[bad_p][:5], want_p[bad_p][:5])
+    return got_e, got_p
+
+
+@pytest.mark.parametrize("bs,ne,batch", PRODUCT_BWD_CASES)
+@pytest.mark.parametrize("log_params", [False, True])
+def test_blocked_backward_product_form_matches_fp64(cuda, bs, ne, batch, log_params):
+    print(f"case blocked bwd product bs={bs} ne={ne} batch={batch} log={log_params}", flush=True)
+    rng = np.random.default_rng(bs * 100 + ne + batch)
+    nb, nelem = 5, 60
+    nids, cids, pids, params, em = _blocked_bwd_case(cuda, rng, nb, ne, bs, batch, nelem, log_params)
+    cids[0, : min(3, ne)] = 2                    # a child repeated within a block
+    em[5, :] = -np.inf                           # a child of probability 0
+    _check_blocked_bwd(cuda, nids, cids, pids, params, em, bs, batch, log_params)
+
+
+def test_blocked_backward_product_form_pairs_left_out(cuda):
+    """Pairs (parent, column) whose scale factor would pass 2^24 take the
+    one-by-one terms: a parent whose only large weight meets a child ~200
+    below the column maximum (held by a child of weight zero); a column where
+    every child is -inf (parents of probability 0, no flow); +inf and NaN
+    upstream flows."""
+    print("case blocked bwd product left-out pairs", flush=True)
+    rng = np.random.default_rng(23)
+    nb, ne, bs, batch, nelem = 3, 40, 16, 68, 90
+    nids = (np.arange(nb) * bs).astype(np.int64)
+    cids = np.stack([rng.permutation(nelem)[:ne] for _ in range(nb)]).astype(np.int64)
+    pids = (np.arange(nb * ne, dtype=np.int64) * bs).reshape(nb, ne)
+    params = (rng.random(nb * ne * bs) + 1e-3).astype(np.float32)
+    em = np.log(rng.random((nelem, batch)) + 1e-9).astype(np.float32)
+    params[pids[2, :] + 6] = 1e-36
+    params[pids[2, 0] + 6] = 1.0
+    params[pids[2, 1] + 6] = 0.0
+    em[cids[2, 0], 20:30] = -200.0
+    em[cids[2, 1], 20:30] = 0.0
+    em[:, 40] = -np.inf
+    nf = rng.standard_normal((nb * bs + 2, batch)).astype(np.float32)
+    got_e, got_p = _check_blocked_bwd(cuda, nids, cids, pids, params, em, bs, batch, False, nf=nf)
+    # the left-out parent's parameter flows carry its whole flow
+    assert np.isfinite(got_p).all()
+
+
+@pytest.mark.parametrize("offset", [1, 3])
+def test_blocked_backward_product_form_unaligned(cuda, offset):
+    """Odd batch and rows off the 16-byte grid take the scalar-column loads."""
+    print(f"case blocked bwd product unaligned off={offset}", flush=True)
+    rng = np.random.default_rng(40 + offset)
+    nb, ne, bs, batch, nelem = 4, 20, 8, 37, 30
+    nids, cids, pids, params, em = _blocked_bwd_case(cuda, rng, nb, ne, bs, batch, nelem, False)
+    _check_blocked_bwd(cuda, nids, cids, pids, params, em, bs, batch, False)
+
+
+def test_blocked_backward_product_form_deterministic(cuda):
+    """Element and parameter flows are the same bits on every call."""
+    print("case blocked bwd product determinism", flush=True)
+    rng = np.random.default_rng(8)
+    nb, ne, bs, batch, nelem = 40, 33, 32, 300, 20        # few elements: many block edges per element
+    nids, cids, pids, params, em = _blocked_bwd_case(cuda, rng, nb, ne, bs, batch, nelem, False)
+    d = _to(cuda, em, params, nids, cids, pids)
+    nm = torch.zeros(nb * (bs + 1), batch, device=cuda)
+    ext = _ext()
+    ext.sparse_forward_float(nm, d[0], d[1], d[2], d[3], d[4], bs)
+    nf = torch.from_numpy(rng.standard_normal((nb * (bs + 1), batch)).astype(np.float32)).to(cuda)
+    outs = []
+    for _ in range(3):
+        ef = torch.zeros(nelem, batch, device=cuda)
+        pf = torch.zeros(params.size, device=cuda)
+        ext.sparse_blocked_backward(nf, ef, nm, d[0], d[1], pf, d[2], d[3], d[4], bs)
+        outs.append((ef, pf))
+    for ef, pf in outs[1:]:
+        assert torch.equal(ef, outs[0][0]) and torch.equal(pf, outs[0][1])
