@@ -21,13 +21,14 @@
 // product and their terms computed one by one as T = g * exp(lw + x - o).
 // A term lost to fp32 underflow in the product is below 2^-102 |g|.
 //
-// Three kernels: edge flows (one wave per block, edge chunk and 64-column
-// tile, the parents as the product's K), parameter flows (one wave per block,
-// edge chunk and parent group, the batch as K, the sums added to param_flows
-// once per (p, e)), and element flows (one wave per element row, its block
-// edges summed in a fixed order through the transposed structure): the result
-// does not depend on scheduling, except that parameters shared by several
-// (block, parent, edge) triples receive their sums in any order.
+// Kernels: edge flows (one wave per block, edge chunk and 64-column tile, the
+// parents as the product's K), parameter flows (one wave per block, edge
+// chunk and parent group, the batch as K, the sums added to param_flows once
+// per (p, e)), and element flows (one wave per element row, its block edges
+// summed in a fixed order through the transposed structure).  Blocks of at
+// most 16 parents take both products in one pass instead (blocked_bwd_fused).
+// The result does not depend on scheduling, except that parameters shared by
+// several (block, parent, edge) triples receive their sums in any order.
 #include <math.h>
 #include <stdint.h>
 
@@ -487,6 +488,296 @@ __global__ __launch_bounds__(64) void blocked_bwd_params(float* __restrict__ par
     }
 }
 
+// Both products in one pass, for blocks of at most 16 parents: one wave per
+// (block, edge chunk) walks the batch in 64-column tiles.  Per tile it loads
+// x (the edge-flow cells), g and o once, runs the product over parents as
+// blocked_bwd_edges does, then writes the tile's X and R to LDS and reads
+// them back transposed for the product over the batch (rows padded to 65
+// floats, so the transposed reads of 16 rows hit 16 banks).  The weights are
+// taken once per wave.  NKP: parent K-steps (4 parents each), MP = NKP / 4
+// rounded up: 16-parent tiles of the product over the batch.
+template <int ET, int NKP, bool VEC, bool LOGP>
+__global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge_flows,
+                                                        float* __restrict__ param_flows,
+                                                        const float* __restrict__ gf, const float* __restrict__ om,
+                                                        const float* __restrict__ xm, const float* __restrict__ params,
+                                                        const int64_t* __restrict__ nids,
+                                                        const int64_t* __restrict__ cids,
+                                                        const int64_t* __restrict__ pids, int64_t ne, int64_t bs,
+                                                        int64_t batch, int64_t chunks, int64_t items, int64_t id0) {
+    constexpr int MP = (NKP + 3) / 4;
+    constexpr int LD = 65;  // padded LDS row
+    __shared__ float xt[16 * ET][LD];   // X of the tile: [edge - c0][column - b0]; then one-by-one edge terms
+    __shared__ float rt[16 * MP][LD];   // R of the tile: [parent][column - b0]
+    __shared__ float gx[16 * MP][16 * ET];  // one-by-one parameter terms: [parent][edge - c0]
+    const int64_t id = logical_id(id0);
+    if (id >= items) return;
+    const int64_t c = id % chunks;
+    const int64_t j = id / chunks;
+    const int l = lane_id();
+    const int kq = l >> 4;
+    const int jc = l & 15;
+    const int64_t c0 = c * CE;
+    const int64_t ebase = j * ne;
+    const int64_t nrow0 = nids[j];
+
+    // weights of the edge-flow product, A[p = 4*ks + kq][e = c0 + 16*et + jc], and
+    // the row maxima (log) over the chunk's edges
+    float a[NKP][ET], lwm[NKP];
+    {
+        int64_t qa[ET];
+        bool eva[ET];
+#pragma unroll
+        for (int et = 0; et < ET; ++et) {
+            const int64_t e = c0 + 16 * et + jc;
+            eva[et] = e < ne;
+            qa[et] = pids[ebase + (eva[et] ? e : ne - 1)];
+        }
+#pragma unroll
+        for (int ks = 0; ks < NKP; ++ks) {
+            const int64_t p = 4 * ks + kq;
+            const bool pv = p < bs;
+            const int64_t pcl = pv ? p : bs - 1;
+            float wv[ET];
+#pragma unroll
+            for (int et = 0; et < ET; ++et) {
+                const float w = weight_term<LOGP>(params[qa[et] + pcl]);
+                wv[et] = eva[et] && pv ? w : (LOGP ? -kInf : 0.0f);
+            }
+            float wm = wv[0];
+#pragma unroll
+            for (int et = 1; et < ET; ++et) wm = fmaxf(wm, wv[et]);
+            wm = row16_max(wm);
+#pragma unroll
+            for (int et = 0; et < ET; ++et)
+                a[ks][et] = !pv ? 0.0f
+                            : LOGP ? (wm == -kInf ? 0.0f : fexp2((wv[et] - wm) * kLog2e))
+                                   : wv[et] / wm;
+            lwm[ks] = LOGP ? wm : logf(wm);
+        }
+    }
+
+    f32x4 gacc[MP][ET];
+#pragma unroll
+    for (int pt = 0; pt < MP; ++pt)
+#pragma unroll
+        for (int et = 0; et < ET; ++et) gacc[pt][et] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    bool any_gx = false;
+
+    for (int64_t b0 = 0; b0 < batch; b0 += 64) {
+        const int64_t col = b0 + 4 * jc;
+        float m[4];
+        {
+        float xv[ET][4][4];
+#pragma unroll
+        for (int et = 0; et < ET; ++et)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t e = c0 + 16 * et + 4 * kq + r;
+                const bool ev = e < ne;
+                float v[4];
+                ld4<VEC>(xm + cids[ebase + (ev ? e : ne - 1)] * batch, col, batch, 0.0f, v);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) xv[et][r][u] = ev ? v[u] : -kInf;
+            }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            float mu = xv[0][0][u];
+#pragma unroll
+            for (int et = 0; et < ET; ++et)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) mu = fmaxf(mu, xv[et][r][u]);
+            mu = fmaxf(mu, xor16(mu));
+            m[u] = fmaxf(mu, xor32(mu));
+        }
+#pragma unroll
+        for (int et = 0; et < ET; ++et)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    xt[16 * et + 4 * kq + r][4 * jc + u] =
+                        __builtin_isfinite(m[u]) ? fexp2((xv[et][r][u] - m[u]) * kLog2e) : 0.0f;
+        }  // the tile's X lives in xt from here
+
+        f32x4 z[ET][4];
+#pragma unroll
+        for (int et = 0; et < ET; ++et)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) z[et][u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        uint64_t left = 0;  // bit 4*ks + u
+#pragma unroll
+        for (int k0 = 0; k0 < NKP; k0 += 4) {
+            constexpr int KC = NKP < 4 ? NKP : 4;
+            float rr[KC][4];
+#pragma unroll
+            for (int kk = 0; kk < KC; ++kk) {
+                const int ks = k0 + kk;
+                const int64_t p = 4 * ks + kq;
+                const bool pv = p < bs;
+                const int64_t n = nrow0 + (pv ? p : bs - 1);
+                float ov[4], gv[4];
+                ld4<VEC>(om + n * batch, col, batch, -kInf, ov);
+                ld4<VEC>(gf + n * batch, col, batch, 0.0f, gv);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    bool lf;
+                    rr[kk][u] = r_factor(lwm[ks], m[u], ov[u], gv[u], pv, lf);
+                    left |= (uint64_t)lf << (4 * ks + u);
+                    rt[4 * ks + kq][4 * jc + u] = rr[kk][u];
+                }
+            }
+#pragma unroll
+            for (int kk = 0; kk < KC; ++kk)
+#pragma unroll
+                for (int et = 0; et < ET; ++et)
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        z[et][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[k0 + kk][et], rr[kk][u], z[et][u], 0, 0, 0);
+        }
+        // rows of R past 4*NKP (up to the 16-row tiles) hold zeros
+        if constexpr (4 * NKP < 16 * MP) {
+#pragma unroll
+            for (int pr = 4 * NKP + kq; pr < 16 * MP; pr += 4)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) rt[pr][4 * jc + u] = 0.0f;
+        }
+        __builtin_amdgcn_wave_barrier();
+        // product over the batch: lane l supplies R[16*pt + l%16][16*(l/16) + ks]
+        // and X[16*et + l%16][same column]
+#pragma unroll 2
+        for (int ks = 0; ks < 16; ++ks) {
+            float ra[MP], xb[ET];
+#pragma unroll
+            for (int pt = 0; pt < MP; ++pt) ra[pt] = rt[16 * pt + jc][16 * kq + ks];
+#pragma unroll
+            for (int et = 0; et < ET; ++et) xb[et] = xt[16 * et + jc][16 * kq + ks];
+#pragma unroll
+            for (int pt = 0; pt < MP; ++pt)
+#pragma unroll
+                for (int et = 0; et < ET; ++et)
+                    gacc[pt][et] = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[pt], xb[et], gacc[pt][et], 0, 0, 0);
+        }
+        __builtin_amdgcn_wave_barrier();
+
+        float res[ET][4][4];
+#pragma unroll
+        for (int et = 0; et < ET; ++et)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const float zz = z[et][u][r];
+                    res[et][r][u] = zz == 0.0f ? 0.0f : xt[16 * et + 4 * kq + r][4 * jc + u] * zz;
+                }
+        if (__ballot(left != 0)) {
+            // pairs left out of the products: one lane at a time, each lane's
+            // pairs in order; edge terms into xt (cleared), parameter terms into gx
+#pragma unroll
+            for (int et = 0; et < ET; ++et)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) xt[16 * et + 4 * kq + r][4 * jc + u] = 0.0f;
+            if (!any_gx) {
+#pragma unroll
+                for (int pt = 0; pt < MP; ++pt)
+#pragma unroll
+                    for (int et = 0; et < ET; ++et)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) gx[16 * pt + 4 * kq + r][16 * et + jc] = 0.0f;
+                any_gx = true;
+            }
+            __builtin_amdgcn_wave_barrier();
+            for (int ll = 0; ll < 64; ++ll) {
+                if (l == ll) {
+                    uint64_t lf = left;
+                    while (lf) {
+                        const int bit = __builtin_ctzll(lf);
+                        lf &= lf - 1;
+                        const int64_t p = 4 * (bit >> 2) + kq;
+                        const int cu = 4 * jc + (bit & 3);
+                        const int64_t n = nrow0 + p;
+                        const float gg = gf[n * batch + b0 + cu];
+                        const float oo = om[n * batch + b0 + cu];
+                        for (int ee = 0; ee < 16 * ET && c0 + ee < ne; ++ee) {
+                            const int64_t e = c0 + ee;
+                            const float lw = log_weight<LOGP>(params[pids[ebase + e] + p]);
+                            const float xx = xm[cids[ebase + e] * batch + b0 + cu];
+                            const float t = gg * fexp2((lw + xx - oo) * kLog2e);
+                            xt[ee][cu] += t;
+                            gx[p][ee] += t;
+                        }
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
+            }
+#pragma unroll
+            for (int et = 0; et < ET; ++et)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) res[et][r][u] += xt[16 * et + 4 * kq + r][4 * jc + u];
+            __builtin_amdgcn_wave_barrier();
+        }
+#pragma unroll
+        for (int et = 0; et < ET; ++et)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t e = c0 + 16 * et + 4 * kq + r;
+                if (e >= ne) continue;
+                float* orow = edge_flows + (ebase + e) * batch;
+                if constexpr (VEC) {
+                    if (col < batch)
+                        *reinterpret_cast<f32x4*>(orow + col) =
+                            f32x4{res[et][r][0], res[et][r][1], res[et][r][2], res[et][r][3]};
+                } else {
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        if (col + u < batch) orow[col + u] = res[et][r][u];
+                }
+            }
+    }
+
+    // param_flows[pids[j, e] + p] += (w / W) G + one-by-one terms, at
+    // G[16*pt + 4*kq + r][c0 + 16*et + jc]; W, the row maximum over the chunk's
+    // edges, is taken again from the same weights (lanes of a row hold all edges)
+#pragma unroll
+    for (int pt = 0; pt < MP; ++pt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t p = 16 * pt + 4 * kq + r;
+            const bool pv = p < bs;
+            const int64_t pcl = pv ? p : bs - 1;
+            float wv[ET];
+            int64_t q[ET];
+#pragma unroll
+            for (int et = 0; et < ET; ++et) {
+                const int64_t e = c0 + 16 * et + jc;
+                const bool ev = e < ne;
+                q[et] = pids[ebase + (ev ? e : ne - 1)];
+                const float w = weight_term<LOGP>(params[q[et] + pcl]);
+                wv[et] = ev && pv ? w : (LOGP ? -kInf : 0.0f);
+            }
+            float wm = wv[0];
+#pragma unroll
+            for (int et = 1; et < ET; ++et) wm = fmaxf(wm, wv[et]);
+            wm = row16_max(wm);
+            if (!pv) continue;
+#pragma unroll
+            for (int et = 0; et < ET; ++et) {
+                const int64_t e = c0 + 16 * et + jc;
+                if (e >= ne) continue;
+                const float aw = LOGP ? (wm == -kInf ? 0.0f : fexp2((wv[et] - wm) * kLog2e)) : wv[et] / wm;
+                const float gsum = gacc[pt][et][r];
+                float v = gsum == 0.0f ? 0.0f : aw * gsum;
+                if (any_gx) v += gx[p][16 * et + jc];
+                if (v != 0.0f)
+                    __hip_atomic_fetch_add(param_flows + q[et] + p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+}
+
 // element_flows[c, b] += sum of edge_flows rows csc_edges[csc_offsets[c] ..
 // csc_offsets[c + 1]) in that order: one wave per element row, 256 columns
 // per pass.
@@ -534,6 +825,12 @@ constexpr int64_t kMaxGroups = (int64_t)1 << 30;  // workgroups per launch, a mu
 // 2 K-steps as 4.
 constexpr int kParamCW = 8;
 constexpr int kEdgeKPMax = 4;
+// Largest block_size of the single-pass kernel.  It reads x, g and o once
+// instead of twice, but holds both products' accumulators: at 8 and 16
+// parents it keeps 3-4 waves per SIMD and wins (262144 nodes, 32 edges,
+// batch 512: 2213 -> 1755 us, 1464 -> 1098 us); at 32 and 64 it drops to one
+// wave per SIMD and loses (1087 -> 1423 us, 865 -> 1066 us).
+constexpr int64_t kFusedMaxBs = 16;
 
 template <int ET, int KP, bool VEC, bool LOGP>
 void launch_edges(float* edge_flows, const float* gf, const float* om, const float* xm, const float* params,
@@ -584,14 +881,47 @@ void launch_et(float* edge_flows, float* param_flows, const float* gf, const flo
         launch_params<2, ET, VEC, LOGP>(param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, st);
 }
 
+template <int ET, int NKP, bool VEC, bool LOGP>
+void launch_fused(float* edge_flows, float* param_flows, const float* gf, const float* om, const float* xm,
+                  const float* params, const int64_t* nids, const int64_t* cids, const int64_t* pids, int64_t nb,
+                  int64_t ne, int64_t bs, int64_t batch, hipStream_t st) {
+    const int64_t chunks = (ne + CE - 1) / CE;
+    const int64_t items = nb * chunks;
+    for (int64_t id0 = 0; id0 < items; id0 += kMaxGroups) {
+        const int64_t n = items - id0 < kMaxGroups ? items - id0 : kMaxGroups;
+        blocked_bwd_fused<ET, NKP, VEC, LOGP><<<dim3((unsigned)((n + 7) / 8 * 8)), dim3(64), 0, st>>>(
+            edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, ne, bs, batch, chunks, items, id0);
+    }
+}
+
+template <int ET, bool VEC, bool LOGP>
+void launch_fused_et(float* edge_flows, float* param_flows, const float* gf, const float* om, const float* xm,
+                     const float* params, const int64_t* nids, const int64_t* cids, const int64_t* pids, int64_t nb,
+                     int64_t ne, int64_t bs, int64_t batch, hipStream_t st) {
+    if (bs <= 4)
+        launch_fused<ET, 1, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, st);
+    else if (bs <= 8)
+        launch_fused<ET, 2, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, st);
+    else
+        launch_fused<ET, 4, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, st);
+}
+
 template <bool VEC, bool LOGP>
 void launch_all(float* edge_flows, float* param_flows, const float* gf, const float* om, const float* xm,
                 const float* params, const int64_t* nids, const int64_t* cids, const int64_t* pids, int64_t nb,
                 int64_t ne, int64_t bs, int64_t batch, hipStream_t st) {
-    if (ne <= 16)
+    if (bs <= kFusedMaxBs) {
+        if (ne <= 16)
+            launch_fused_et<1, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs,
+                                          batch, st);
+        else
+            launch_fused_et<2, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs,
+                                          batch, st);
+    } else if (ne <= 16) {
         launch_et<1, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, st);
-    else
+    } else {
         launch_et<2, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, st);
+    }
 }
 
 }  // namespace

@@ -567,11 +567,13 @@ def test_blocked_backward_product_form_unaligned(cuda, offset):
     _check_blocked_bwd(cuda, nids, cids, pids, params, em, bs, batch, False)
 
 
-def test_blocked_backward_product_form_deterministic(cuda):
-    """Element and parameter flows are the same bits on every call."""
-    print("case blocked bwd product determinism", flush=True)
+@pytest.mark.parametrize("bs", [32, 12])
+def test_blocked_backward_product_form_deterministic(cuda, bs):
+    """Element and parameter flows are the same bits on every call (block
+    size 32: the two product kernels; 12: the single-pass kernel)."""
+    print(f"case blocked bwd product determinism bs={bs}", flush=True)
     rng = np.random.default_rng(8)
-    nb, ne, bs, batch, nelem = 40, 33, 32, 300, 20        # few elements: many block edges per element
+    nb, ne, batch, nelem = 40, 33, 300, 20        # few elements: many block edges per element
     nids, cids, pids, params, em = _blocked_bwd_case(cuda, rng, nb, ne, bs, batch, nelem, False)
     d = _to(cuda, em, params, nids, cids, pids)
     nm = torch.zeros(nb * (bs + 1), batch, device=cuda)
