@@ -588,3 +588,57 @@ def test_blocked_backward_product_form_deterministic(cuda, bs):
         outs.append((ef, pf))
     for ef, pf in outs[1:]:
         assert torch.equal(ef, outs[0][0]) and torch.equal(pf, outs[0][1])
+
+
+@pytest.mark.parametrize("bs1,bs2", [(8, 4), (32, 2), (1, 16)])
+def test_blocked_layer_autograd_two_layers(cuda, bs1, bs2):
+    """pc.sparse_blocked_layer: two stacked block-layout layers with log-weights,
+    outputs and gradients of the inputs and of both weight vectors against
+    torch fp64 autograd of the same layers."""
+    from fuselse_amd.pc import sparse_blocked_layer
+
+    print(f"case blocked layer autograd bs={bs1},{bs2}", flush=True)
+    rng = np.random.default_rng(bs1 * 10 + bs2)
+    batch, nx = 70, 24
+
+    def layer_spec(nchild, nb, ne, bs):
+        nids = (np.arange(nb) * bs).astype(np.int64)
+        cids = rng.integers(0, nchild, (nb, ne)).astype(np.int64)
+        pids = (np.arange(nb * ne, dtype=np.int64) * bs).reshape(nb, ne)
+        lw = (rng.standard_normal(nb * ne * bs) * 0.5 - 1.0).astype(np.float32)
+        return nids, cids, pids, lw
+
+    n1b, n2b = 6, 3
+    L1 = layer_spec(nx, n1b, 9, bs1)
+    L2 = layer_spec(n1b * bs1, n2b, 12, bs2)
+    x = np.log(rng.random((nx, batch)) + 1e-6).astype(np.float32)
+
+    def run_gpu():
+        xd = torch.from_numpy(x).to(cuda).requires_grad_(True)
+        w1 = torch.from_numpy(L1[3]).to(cuda).requires_grad_(True)
+        w2 = torch.from_numpy(L2[3]).to(cuda).requires_grad_(True)
+        i1 = [torch.from_numpy(a).to(cuda) for a in L1[:3]]
+        i2 = [torch.from_numpy(a).to(cuda) for a in L2[:3]]
+        h = sparse_blocked_layer(xd, w1, *i1, bs1, n1b * bs1)
+        y = sparse_blocked_layer(h, w2, *i2, bs2, n2b * bs2)
+        (y * torch.linspace(0.5, 1.5, batch, device=cuda)).sum().backward()
+        return y.detach().cpu().numpy(), xd.grad.cpu().numpy(), w1.grad.cpu().numpy(), w2.grad.cpu().numpy()
+
+    def layer_t(ch, spec, lw, bs):
+        nids, cids, pids, _ = spec
+        rows = []
+        for j in range(len(nids)):
+            for p in range(bs):
+                q = torch.from_numpy(pids[j] + p)
+                rows.append(torch.logsumexp(lw[q][:, None] + ch[torch.from_numpy(cids[j])], 0))
+        return torch.stack(rows)
+
+    xt = torch.from_numpy(x).double().requires_grad_(True)
+    w1t = torch.from_numpy(L1[3]).double().requires_grad_(True)
+    w2t = torch.from_numpy(L2[3]).double().requires_grad_(True)
+    yt = layer_t(layer_t(xt, L1, w1t, bs1), L2, w2t, bs2)
+    (yt * torch.linspace(0.5, 1.5, batch, dtype=torch.float64)).sum().backward()
+    y, gx, g1, g2 = run_gpu()
+    np.testing.assert_allclose(y, yt.detach().numpy(), rtol=1e-5, atol=1e-5)
+    for got, want in ((gx, xt.grad), (g1, w1t.grad), (g2, w2t.grad)):
+        np.testing.assert_allclose(got, want.numpy(), rtol=1e-4, atol=1e-5)
