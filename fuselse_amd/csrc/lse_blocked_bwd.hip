@@ -488,14 +488,54 @@ __global__ __launch_bounds__(64) void blocked_bwd_params(float* __restrict__ par
     }
 }
 
-// Both products in one pass, for blocks of at most 16 parents: one wave per
+// x at a lane's cells of a 64-column tile (edges c0 + 16*et + 4*kq + r,
+// columns col .. col + 3; edges past ne read -inf, columns past the batch 0)
+// and the column maxima over the chunk's edges.
+template <int ET, bool VEC>
+__device__ __forceinline__ void tile_x(const float* __restrict__ xm, const int64_t* __restrict__ cids, int64_t ebase,
+                                       int64_t ne, int64_t c0, int kq, int64_t col, int64_t batch,
+                                       float (&xv)[ET][4][4], float (&m)[4]) {
+#pragma unroll
+    for (int et = 0; et < ET; ++et)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t e = c0 + 16 * et + 4 * kq + r;
+            ld4<VEC>(xm + cids[ebase + (e < ne ? e : ne - 1)] * batch, col, batch, 0.0f, xv[et][r]);
+        }
+    // every load of the tile issued before the first use
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int et = 0; et < ET; ++et)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const bool ev = c0 + 16 * et + 4 * kq + r < ne;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) xv[et][r][u] = ev ? xv[et][r][u] : -kInf;
+        }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        float mu = xv[0][0][u];
+#pragma unroll
+        for (int et = 0; et < ET; ++et)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mu = fmaxf(mu, xv[et][r][u]);
+        mu = fmaxf(mu, xor16(mu));
+        m[u] = fmaxf(mu, xor32(mu));
+    }
+}
+
+// Both products in one pass, for blocks of at most 32 parents: one wave per
 // (block, edge chunk) walks the batch in 64-column tiles.  Per tile it loads
 // x (the edge-flow cells), g and o once, runs the product over parents as
 // blocked_bwd_edges does, then writes the tile's X and R to LDS and reads
 // them back transposed for the product over the batch (rows padded to 65
 // floats, so the transposed reads of 16 rows hit 16 banks).  The weights are
-// taken once per wave.  NKP: parent K-steps (4 parents each), MP = NKP / 4
-// rounded up: 16-parent tiles of the product over the batch.
+// taken once per wave.  Pairs left out of the products are only counted in
+// the tile loop; when there are any, a second pass over the tiles finds them
+// again with the same arithmetic and adds their one-by-one terms (the code
+// for them inside the loop cost 55 registers and half the occupancy).
+// NKP: parent K-steps (4 parents each), MP = NKP / 4 rounded up: 16-parent
+// tiles of the product over the batch.
 template <int ET, int NKP, bool VEC, bool LOGP>
 __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge_flows,
                                                         float* __restrict__ param_flows,
@@ -507,7 +547,8 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
                                                         int64_t batch, int64_t chunks, int64_t items, int64_t id0) {
     constexpr int MP = (NKP + 3) / 4;
     constexpr int LD = 65;  // padded LDS row
-    __shared__ float xt[16 * ET][LD];   // X of the tile: [edge - c0][column - b0]; then one-by-one edge terms
+    constexpr int KC = NKP < 4 ? NKP : 4;
+    __shared__ float xt[16 * ET][LD];   // X of the tile: [edge - c0][column - b0]; one-by-one edge terms
     __shared__ float rt[16 * MP][LD];   // R of the tile: [parent][column - b0]
     __shared__ float gx[16 * MP][16 * ET];  // one-by-one parameter terms: [parent][edge - c0]
     const int64_t id = logical_id(id0);
@@ -562,42 +603,22 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
     for (int pt = 0; pt < MP; ++pt)
 #pragma unroll
         for (int et = 0; et < ET; ++et) gacc[pt][et] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    bool any_gx = false;
+    bool any_left = false;
 
     for (int64_t b0 = 0; b0 < batch; b0 += 64) {
         const int64_t col = b0 + 4 * jc;
         float m[4];
         {
-        float xv[ET][4][4];
-#pragma unroll
-        for (int et = 0; et < ET; ++et)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t e = c0 + 16 * et + 4 * kq + r;
-                const bool ev = e < ne;
-                float v[4];
-                ld4<VEC>(xm + cids[ebase + (ev ? e : ne - 1)] * batch, col, batch, 0.0f, v);
-#pragma unroll
-                for (int u = 0; u < 4; ++u) xv[et][r][u] = ev ? v[u] : -kInf;
-            }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            float mu = xv[0][0][u];
+            float xv[ET][4][4];
+            tile_x<ET, VEC>(xm, cids, ebase, ne, c0, kq, col, batch, xv, m);
 #pragma unroll
             for (int et = 0; et < ET; ++et)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) mu = fmaxf(mu, xv[et][r][u]);
-            mu = fmaxf(mu, xor16(mu));
-            m[u] = fmaxf(mu, xor32(mu));
-        }
+                for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int et = 0; et < ET; ++et)
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-#pragma unroll
-                for (int u = 0; u < 4; ++u)
-                    xt[16 * et + 4 * kq + r][4 * jc + u] =
-                        __builtin_isfinite(m[u]) ? fexp2((xv[et][r][u] - m[u]) * kLog2e) : 0.0f;
+                    for (int u = 0; u < 4; ++u)
+                        xt[16 * et + 4 * kq + r][4 * jc + u] =
+                            __builtin_isfinite(m[u]) ? fexp2((xv[et][r][u] - m[u]) * kLog2e) : 0.0f;
         }  // the tile's X lives in xt from here
 
         f32x4 z[ET][4];
@@ -605,25 +626,28 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
         for (int et = 0; et < ET; ++et)
 #pragma unroll
             for (int u = 0; u < 4; ++u) z[et][u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        uint64_t left = 0;  // bit 4*ks + u
+        bool left = false;
 #pragma unroll
-        for (int k0 = 0; k0 < NKP; k0 += 4) {
-            constexpr int KC = NKP < 4 ? NKP : 4;
-            float rr[KC][4];
+        for (int k0 = 0; k0 < NKP; k0 += KC) {
+            float rr[KC][4], ov[KC][4], gv[KC][4];
+#pragma unroll
+            for (int kk = 0; kk < KC; ++kk) {
+                const int64_t p = 4 * (k0 + kk) + kq;
+                const int64_t n = nrow0 + (p < bs ? p : bs - 1);
+                ld4<VEC>(om + n * batch, col, batch, -kInf, ov[kk]);
+                ld4<VEC>(gf + n * batch, col, batch, 0.0f, gv[kk]);
+            }
+            // every g and o load of the chunk issued before the first use
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int kk = 0; kk < KC; ++kk) {
                 const int ks = k0 + kk;
-                const int64_t p = 4 * ks + kq;
-                const bool pv = p < bs;
-                const int64_t n = nrow0 + (pv ? p : bs - 1);
-                float ov[4], gv[4];
-                ld4<VEC>(om + n * batch, col, batch, -kInf, ov);
-                ld4<VEC>(gf + n * batch, col, batch, 0.0f, gv);
+                const bool pv = 4 * ks + kq < bs;
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     bool lf;
-                    rr[kk][u] = r_factor(lwm[ks], m[u], ov[u], gv[u], pv, lf);
-                    left |= (uint64_t)lf << (4 * ks + u);
+                    rr[kk][u] = r_factor(lwm[ks], m[u], ov[kk][u], gv[kk][u], pv, lf);
+                    left = left || lf;
                     rt[4 * ks + kq][4 * jc + u] = rr[kk][u];
                 }
             }
@@ -635,6 +659,7 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
                     for (int u = 0; u < 4; ++u)
                         z[et][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[k0 + kk][et], rr[kk][u], z[et][u], 0, 0, 0);
         }
+        any_left = any_left || __ballot(left) != 0;
         // rows of R past 4*NKP (up to the 16-row tiles) hold zeros
         if constexpr (4 * NKP < 16 * MP) {
 #pragma unroll
@@ -658,36 +683,87 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
                 for (int et = 0; et < ET; ++et)
                     gacc[pt][et] = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[pt], xb[et], gacc[pt][et], 0, 0, 0);
         }
-        __builtin_amdgcn_wave_barrier();
-
-        float res[ET][4][4];
+        // edge flows F = X .* Z at rows c0 + 16*et + 4*kq + r
 #pragma unroll
         for (int et = 0; et < ET; ++et)
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
+            for (int r = 0; r < 4; ++r) {
+                const int64_t e = c0 + 16 * et + 4 * kq + r;
+                float res[4];
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     const float zz = z[et][u][r];
-                    res[et][r][u] = zz == 0.0f ? 0.0f : xt[16 * et + 4 * kq + r][4 * jc + u] * zz;
+                    res[u] = zz == 0.0f ? 0.0f : xt[16 * et + 4 * kq + r][4 * jc + u] * zz;
                 }
-        if (__ballot(left != 0)) {
-            // pairs left out of the products: one lane at a time, each lane's
-            // pairs in order; edge terms into xt (cleared), parameter terms into gx
+                if (e >= ne) continue;
+                float* orow = edge_flows + (ebase + e) * batch;
+                if constexpr (VEC) {
+                    if (col < batch) *reinterpret_cast<f32x4*>(orow + col) = f32x4{res[0], res[1], res[2], res[3]};
+                } else {
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        if (col + u < batch) orow[col + u] = res[u];
+                }
+            }
+        __builtin_amdgcn_wave_barrier();
+    }
+
+    if (any_left) {
+        // Second pass: the same column maxima and R tests find the pairs left
+        // out; their terms go, one lane at a time and each lane's pairs in
+        // order, into xt (edge terms of the tile, then added by each cell's
+        // owner to its stored edge flow) and gx (parameter terms).
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");  // this wave's tile stores are visible
+#pragma unroll
+        for (int pt = 0; pt < MP; ++pt)
+#pragma unroll
+            for (int et = 0; et < ET; ++et)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) gx[16 * pt + 4 * kq + r][16 * et + jc] = 0.0f;
+        for (int64_t b0 = 0; b0 < batch; b0 += 64) {
+            const int64_t col = b0 + 4 * jc;
+            float m[4];
+            {
+                float xv[ET][4][4];
+                tile_x<ET, VEC>(xm, cids, ebase, ne, c0, kq, col, batch, xv, m);
+            }
+            uint64_t left = 0;  // bit 4*ks + u
+            // one K-step at a time (this pass is rare; its registers count
+            // against the whole kernel), the row maximum taken again as the
+            // first pass took it
+#pragma unroll 1
+            for (int ks = 0; ks < NKP; ++ks) {
+                const int64_t p = 4 * ks + kq;
+                const bool pv = p < bs;
+                const int64_t pcl = pv ? p : bs - 1;
+                float wm = LOGP ? -kInf : 0.0f;
+#pragma unroll
+                for (int et = 0; et < ET; ++et) {
+                    const int64_t e = c0 + 16 * et + jc;
+                    const bool ev = e < ne;
+                    const float w = weight_term<LOGP>(params[pids[ebase + (ev ? e : ne - 1)] + pcl]);
+                    wm = ev && pv ? fmaxf(wm, w) : wm;
+                }
+                wm = row16_max(wm);
+                const float lw = LOGP ? wm : logf(wm);
+                const int64_t n = nrow0 + pcl;
+                float ov[4], gv[4];
+                ld4<VEC>(om + n * batch, col, batch, -kInf, ov);
+                ld4<VEC>(gf + n * batch, col, batch, 0.0f, gv);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    bool lf;
+                    (void)r_factor(lw, m[u], ov[u], gv[u], pv, lf);
+                    left |= (uint64_t)lf << (4 * ks + u);
+                }
+            }
+            if (__ballot(left != 0) == 0) continue;
 #pragma unroll
             for (int et = 0; et < ET; ++et)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
 #pragma unroll
                     for (int u = 0; u < 4; ++u) xt[16 * et + 4 * kq + r][4 * jc + u] = 0.0f;
-            if (!any_gx) {
-#pragma unroll
-                for (int pt = 0; pt < MP; ++pt)
-#pragma unroll
-                    for (int et = 0; et < ET; ++et)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) gx[16 * pt + 4 * kq + r][16 * et + jc] = 0.0f;
-                any_gx = true;
-            }
             __builtin_amdgcn_wave_barrier();
             for (int ll = 0; ll < 64; ++ll) {
                 if (l == ll) {
@@ -715,28 +791,19 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
 #pragma unroll
             for (int et = 0; et < ET; ++et)
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t e = c0 + 16 * et + 4 * kq + r;
+                    if (e >= ne) continue;
+                    float* orow = edge_flows + (ebase + e) * batch;
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) res[et][r][u] += xt[16 * et + 4 * kq + r][4 * jc + u];
+                    for (int u = 0; u < 4; ++u) {
+                        const float t = xt[16 * et + 4 * kq + r][4 * jc + u];
+                        if (t != 0.0f && col + u < batch) orow[col + u] += t;
+                    }
+                }
             __builtin_amdgcn_wave_barrier();
         }
-#pragma unroll
-        for (int et = 0; et < ET; ++et)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t e = c0 + 16 * et + 4 * kq + r;
-                if (e >= ne) continue;
-                float* orow = edge_flows + (ebase + e) * batch;
-                if constexpr (VEC) {
-                    if (col < batch)
-                        *reinterpret_cast<f32x4*>(orow + col) =
-                            f32x4{res[et][r][0], res[et][r][1], res[et][r][2], res[et][r][3]};
-                } else {
-#pragma unroll
-                    for (int u = 0; u < 4; ++u)
-                        if (col + u < batch) orow[col + u] = res[et][r][u];
-                }
-            }
+        __builtin_amdgcn_wave_barrier();
     }
 
     // param_flows[pids[j, e] + p] += (w / W) G + one-by-one terms, at
@@ -771,7 +838,7 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
                 const float aw = LOGP ? (wm == -kInf ? 0.0f : fexp2((wv[et] - wm) * kLog2e)) : wv[et] / wm;
                 const float gsum = gacc[pt][et][r];
                 float v = gsum == 0.0f ? 0.0f : aw * gsum;
-                if (any_gx) v += gx[p][16 * et + jc];
+                if (any_left) v += gx[p][16 * et + jc];
                 if (v != 0.0f)
                     __hip_atomic_fetch_add(param_flows + q[et] + p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
@@ -826,11 +893,12 @@ constexpr int64_t kMaxGroups = (int64_t)1 << 30;  // workgroups per launch, a mu
 constexpr int kParamCW = 8;
 constexpr int kEdgeKPMax = 4;
 // Largest block_size of the single-pass kernel.  It reads x, g and o once
-// instead of twice, but holds both products' accumulators: at 8 and 16
-// parents it keeps 3-4 waves per SIMD and wins (262144 nodes, 32 edges,
-// batch 512: 2213 -> 1755 us, 1464 -> 1098 us); at 32 and 64 it drops to one
-// wave per SIMD and loses (1087 -> 1423 us, 865 -> 1066 us).
-constexpr int64_t kFusedMaxBs = 16;
+// instead of twice (262144 nodes, 32 edges, batch 512: 8 parents 2213 ->
+// 1667 us, 16: 1464 -> 1041 us, 24: 1284 -> 971 us, 32: 1088 -> 833 us
+// against the two kernels).  Its loads are issued ahead of their first use
+// behind scheduling barriers: without them the compiler waited on every load
+// of a tile in turn (16 parents: 1312 us).
+constexpr int64_t kFusedMaxBs = 32;
 
 template <int ET, int KP, bool VEC, bool LOGP>
 void launch_edges(float* edge_flows, const float* gf, const float* om, const float* xm, const float* params,
@@ -902,8 +970,10 @@ void launch_fused_et(float* edge_flows, float* param_flows, const float* gf, con
         launch_fused<ET, 1, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, st);
     else if (bs <= 8)
         launch_fused<ET, 2, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, st);
-    else
+    else if (bs <= 16)
         launch_fused<ET, 4, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, st);
+    else
+        launch_fused<ET, 8, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, st);
 }
 
 template <bool VEC, bool LOGP>

@@ -531,15 +531,16 @@ def test_blocked_backward_product_form_matches_fp64(cuda, bs, ne, batch, log_par
     _check_blocked_bwd(cuda, nids, cids, pids, params, em, bs, batch, log_params)
 
 
-def test_blocked_backward_product_form_pairs_left_out(cuda):
+@pytest.mark.parametrize("bs", [16, 32, 48])
+def test_blocked_backward_product_form_pairs_left_out(cuda, bs):
     """Pairs (parent, column) whose scale factor would pass 2^24 take the
     one-by-one terms: a parent whose only large weight meets a child ~200
     below the column maximum (held by a child of weight zero); a column where
-    every child is -inf (parents of probability 0, no flow); +inf and NaN
-    upstream flows."""
-    print("case blocked bwd product left-out pairs", flush=True)
+    every child is -inf (parents of probability 0, no flow).  Block sizes 16
+    and 32 run the single-pass kernel (its second pass), 48 the two kernels."""
+    print(f"case blocked bwd product left-out pairs bs={bs}", flush=True)
     rng = np.random.default_rng(23)
-    nb, ne, bs, batch, nelem = 3, 40, 16, 68, 90
+    nb, ne, batch, nelem = 3, 40, 68, 90
     nids = (np.arange(nb) * bs).astype(np.int64)
     cids = np.stack([rng.permutation(nelem)[:ne] for _ in range(nb)]).astype(np.int64)
     pids = (np.arange(nb * ne, dtype=np.int64) * bs).reshape(nb, ne)
