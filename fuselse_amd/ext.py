@@ -372,12 +372,18 @@ def sparse_blocked_transpose(nids, cids, pids, block_size, num_elements):
         _check(t.is_cuda and t.dtype == torch.int64 and t.is_contiguous(), f"{name} must be a contiguous CUDA int64 tensor")
     _check(cids.dim() == 2 and pids.shape == cids.shape and nids.dim() == 1 and nids.size(0) == cids.size(0),
            "nids [nblocks], cids and pids [nblocks, num_edges] shapes disagree")
+    return _blocked_plan(nids, cids, pids, block_size, num_elements)
+
+
+def _blocked_plan(nids, cids, pids, block_size, num_elements):
+    """sparse_blocked_transpose's construction, on the tensors' own device."""
     nb, ne = cids.shape
     bs = int(block_size)
     _check(nb * ne < 2 ** 31 and nb * bs * ne < 2 ** 31 and num_elements < 2 ** 31,
            "edges and element rows must each be < 2^31")
     dev = cids.device
     child_ids = cids.reshape(-1)
+    _check(child_ids.numel() == 0 or int(child_ids.min()) >= 0, "cids hold negative ids")
     order = torch.sort(child_ids, stable=True).indices
     counts = torch.bincount(child_ids, minlength=num_elements)
     _check(counts.numel() == num_elements, "cids hold ids >= element_mars rows")

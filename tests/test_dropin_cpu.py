@@ -283,3 +283,32 @@ def test_reference_edge_cases_of_the_dispatch():
     out = lse(fake(torch.randn(3, 4)))
     assert ext.calls and ext.calls[-1][0] == "fwd_robust" and tuple(out.shape) == (3,)
     assert not hasattr(lse, "out")
+
+
+@pytest.mark.parametrize("bs", [1, 4])
+def test_blocked_plan_lists_each_elements_block_edges_in_order(bs):
+    """The block-layout backward's plan (built by torch ops on the tensors'
+    device; here the CPU): csc_offsets delimit, for each element row, the
+    block edges j * num_edges + e with cids[j, e] equal to it, in increasing
+    order; block size 1 adds each edge's node row and parameter id."""
+    from fuselse_amd.ext import _blocked_plan
+
+    g = torch.Generator().manual_seed(3)
+    nb, ne, nel = 7, 5, 9
+    nids = torch.arange(nb, dtype=torch.int64) * bs + 2
+    cids = torch.randint(0, nel, (nb, ne), generator=g)
+    cids[0, :3] = 4                                     # repeats within a block
+    pids = (torch.arange(nb * ne, dtype=torch.int64) * bs).reshape(nb, ne)
+    plan = _blocked_plan(nids, cids, pids, bs, nel + 2)  # two element rows no block uses
+    off, edges = plan.csc_offsets.tolist(), plan.csc_edges.tolist()
+    assert len(off) == nel + 3 and off[0] == 0 and off[-1] == nb * ne
+    for c in range(nel + 2):
+        want = [j * ne + e for j in range(nb) for e in range(ne) if int(cids[j, e]) == c]
+        assert edges[off[c]:off[c + 1]] == want
+    if bs == 1:
+        assert plan.csc_nodes.tolist() == [int(nids[k // ne]) for k in edges]
+        assert plan.param_ids.tolist() == pids.reshape(-1).tolist()
+    else:
+        assert plan.csc_nodes is None and plan.param_ids is None
+    with pytest.raises(RuntimeError, match=">= element_mars rows"):
+        _blocked_plan(nids, cids, pids, bs, 3)
