@@ -297,6 +297,14 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
             bufs = [torch.randn(bt, 1023, v, device=dev, generator=gen) * 2 for _ in range(2)]
             idx = torch.randint(0, v, (bt, 1023), device=dev, generator=gen)
             ms = _time_calls(torch, stream, lambda i: fuselse_amd.selective_log_softmax(bufs[i % 2], idx), 2, 20)
+            # trl's own argument, logits[:, :-1, :] of (bt, 1024, v) model logits:
+            # one launch per leading slice, against copying the view first
+            full = torch.randn(bt, 1024, v, device=dev, generator=gen) * 2
+            ms_slice = _time_calls(torch, stream, lambda i: fuselse_amd.selective_log_softmax(full[:, :-1, :], idx), 1,
+                                   10)
+            ms_copy = _time_calls(torch, stream,
+                                  lambda i: fuselse_amd.selective_log_softmax(full[:, :-1, :].contiguous(), idx), 1, 10)
+            del full
             ms_trl = _time_calls(torch, stream, lambda i: _trl_algorithm(bufs[i % 2], idx), 2, 10)
             saved = torch.logsumexp
             torch.logsumexp = fuselse_amd.logsumexp
@@ -308,7 +316,8 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
             ref = _trl_algorithm(bufs[0], idx)
             assert torch.allclose(got, ref, rtol=1e-4, atol=1e-4), "selective log-softmax mismatch"
             rec(f"sls_fwd_{name}_{bt}x1023x{v}", ms, 4 * rows * v + 16 * rows, trl_torch_us=round(ms_trl * 1e3, 1),
-                trl_with_fuselse_lse_us=round(ms_trl_fl * 1e3, 1))
+                trl_with_fuselse_lse_us=round(ms_trl_fl * 1e3, 1), trl_slice_us=round(ms_slice * 1e3, 1),
+                trl_slice_copied_us=round(ms_copy * 1e3, 1))
             del bufs
     if want("C4"):
         # C4: IntLSE fixed point

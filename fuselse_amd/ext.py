@@ -127,14 +127,15 @@ def onepass_lse_float_backward(grad_output: torch.Tensor, x: torch.Tensor, lse_o
     return grad_input
 
 
-def selective_log_softmax_float(logits: torch.Tensor, index: torch.Tensor, robust: bool = True):
+def selective_log_softmax_float(logits: torch.Tensor, index: torch.Tensor, robust: bool = True, out=None):
     """Fused selective log-softmax over fp32 (B, N) logits and int64 (B,)
     targets: returns (logp, lse) with logp[r] = logits[r, index[r]] - lse[r],
     in one pass over the logits.  It fuses the fp32 branch of
     trl.trainer.utils.selective_log_softmax (trl 1.0.0: gather, per-row
     torch.logsumexp, subtraction), which the reference's RLHF experiment
     times (experiment_rlhf_logsumexp/run_rlhf.py:28,145,155).  An index
-    outside [0, N) gives NaN."""
+    outside [0, N) gives NaN.  out: an optional (logp, lse) pair of
+    contiguous fp32 (B,) tensors to write."""
     _check(logits.is_cuda, "logits must be CUDA")
     _check(index.is_cuda, "index must be CUDA")
     _check(logits.dtype == torch.float32, "logits must be float32")
@@ -145,8 +146,14 @@ def selective_log_softmax_float(logits: torch.Tensor, index: torch.Tensor, robus
     _check(index.is_contiguous(), "index must be contiguous")
     _check(index.size(0) == logits.size(0), "index batch dimension must match logits")
     B, N = logits.shape
-    logp = torch.empty((B,), dtype=torch.float32, device=logits.device)
-    lse = torch.empty((B,), dtype=torch.float32, device=logits.device)
+    if out is None:
+        logp = torch.empty((B,), dtype=torch.float32, device=logits.device)
+        lse = torch.empty((B,), dtype=torch.float32, device=logits.device)
+    else:
+        logp, lse = out
+        for t in (logp, lse):
+            _check(t.is_cuda and t.dtype == torch.float32 and t.is_contiguous() and tuple(t.shape) == (B,)
+                   and t.device == logits.device, "out must hold two contiguous CUDA float32 (B,) tensors")
     if B == 0:
         return logp, lse
     with _on_device(logits):
@@ -159,9 +166,10 @@ def selective_log_softmax_float(logits: torch.Tensor, index: torch.Tensor, robus
 
 
 def selective_log_softmax_float_backward(grad_output: torch.Tensor, logits: torch.Tensor, index: torch.Tensor,
-                                         lse: torch.Tensor) -> torch.Tensor:
+                                         lse: torch.Tensor, out=None) -> torch.Tensor:
     """grad_logits[r, i] = grad_output[r] * ((i == index[r]) - exp(logits[r, i] - lse[r])),
-    one pass over the logits."""
+    one pass over the logits.  out: an optional contiguous fp32 (B, N) tensor
+    to write."""
     for t, nm in ((grad_output, "grad_output"), (logits, "logits"), (index, "index"), (lse, "lse")):
         _check(t.is_cuda, f"{nm} must be CUDA")
         _check(t.is_contiguous(), f"{nm} must be contiguous")
@@ -173,7 +181,13 @@ def selective_log_softmax_float_backward(grad_output: torch.Tensor, logits: torc
     B, N = logits.shape
     _check(grad_output.size(0) == B and index.size(0) == B and lse.size(0) == B,
            "grad_output, index and lse batch dimensions must match logits")
-    grad = torch.empty_like(logits)
+    if out is None:
+        grad = torch.empty_like(logits)
+    else:
+        grad = out
+        _check(grad.is_cuda and grad.dtype == torch.float32 and grad.is_contiguous()
+               and tuple(grad.shape) == (B, N) and grad.device == logits.device,
+               "out must be a contiguous CUDA float32 (B, N) tensor")
     if B * N == 0:
         return grad
     with _on_device(logits):

@@ -37,28 +37,71 @@ def _trl_algorithm(logits: torch.Tensor, index: torch.Tensor) -> torch.Tensor:
     return torch.stack(rows)
 
 
+# Most leading slices taken one launch each instead of copying the logits.
+_MAX_SLICES = 64
+
+
+def _row_slices(x: torch.Tensor):
+    """Contiguous [rows, V] views covering x's rows in order, without a copy:
+    x itself when it is contiguous, or x[b] for each b of a 3-D x whose rows
+    are contiguous within each leading index (trl takes the logits as
+    logits[:, :-1, :], whose rows skip one row at every leading index).  None
+    when neither holds."""
+    n = x.shape[-1]
+    if x.is_contiguous():
+        return [x.reshape(-1, n)]
+    if x.dim() == 3 and 1 <= x.size(0) <= _MAX_SLICES and x.stride(-1) == 1 and x.stride(1) == n:
+        return [x[b] for b in range(x.size(0))]
+    return None
+
+
 def make_selective_log_softmax(ext, original=None, robust: bool = True):
     fwd = ext.selective_log_softmax_float
     bwd = ext.selective_log_softmax_float_backward
     fallback = original if original is not None else _trl_algorithm
 
+    def forward_rows(logits, idx):
+        """(logp, lse, slices): one launch per contiguous slice of rows (a
+        copy of the logits only when they have none)."""
+        slices = _row_slices(logits)
+        if slices is None:
+            slices = [logits.reshape(-1, logits.shape[-1]).contiguous()]
+        if len(slices) == 1:
+            logp, lse = fwd(slices[0], idx, robust)
+            return logp, lse, slices
+        logp = torch.empty(idx.shape, dtype=torch.float32, device=logits.device)
+        lse = torch.empty(idx.shape, dtype=torch.float32, device=logits.device)
+        r0 = 0
+        for sl in slices:
+            r = sl.shape[0]
+            fwd(sl, idx[r0:r0 + r], robust, out=(logp[r0:r0 + r], lse[r0:r0 + r]))
+            r0 += r
+        return logp, lse, slices
+
     class _SelectiveLogSoftmax(torch.autograd.Function):
         @staticmethod
         def forward(ctx, logits, index):
-            n = logits.shape[-1]
-            rows = logits.reshape(-1, n).contiguous()
             idx = index.reshape(-1).to(torch.int64).contiguous()
-            logp, lse = fwd(rows, idx, robust)
-            ctx.save_for_backward(rows, idx, lse)
+            logp, lse, slices = forward_rows(logits, idx)
+            ctx.save_for_backward(idx, lse, *slices)
             ctx.in_shape = tuple(logits.shape)
             ctx.mark_non_differentiable(lse)
             return logp.reshape(index.shape)
 
         @staticmethod
         def backward(ctx, grad_out):
-            rows, idx, lse = ctx.saved_tensors
-            g = bwd(grad_out.reshape(-1).to(torch.float32).contiguous(), rows, idx, lse)
-            return g.reshape(ctx.in_shape), None
+            idx, lse, *slices = ctx.saved_tensors
+            g = grad_out.reshape(-1).to(torch.float32).contiguous()
+            if len(slices) == 1:
+                return bwd(g, slices[0], idx, lse).reshape(ctx.in_shape), None
+            grad = torch.empty(ctx.in_shape, dtype=torch.float32, device=lse.device)
+            rows = grad.view(-1, ctx.in_shape[-1])
+            r0 = 0
+            for sl in slices:
+                r = sl.shape[0]
+                bwd(g[r0:r0 + r], sl, idx[r0:r0 + r], lse[r0:r0 + r], out=rows[r0:r0 + r])
+                r0 += r
+            return grad, None
 
     def selective_log_softmax(logits, index):
         ok = (logits.is_cuda and logits.dtype == torch.float32 and logits.dim() >= 1
@@ -68,8 +111,7 @@ def make_selective_log_softmax(ext, original=None, robust: bool = True):
             return fallback(logits, index)
         if torch.is_grad_enabled() and logits.requires_grad:
             return _SelectiveLogSoftmax.apply(logits, index)
-        n = logits.shape[-1]
-        logp, _ = fwd(logits.reshape(-1, n).contiguous(), index.reshape(-1).to(torch.int64).contiguous(), robust)
+        logp, _, _ = forward_rows(logits, index.reshape(-1).to(torch.int64).contiguous())
         return logp.reshape(index.shape)
 
     selective_log_softmax.fuselse_robust = robust

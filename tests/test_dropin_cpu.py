@@ -157,20 +157,29 @@ class FakeSelExt:
     def __init__(self):
         self.calls = []
 
-    def selective_log_softmax_float(self, logits, index, robust=True):
+    def selective_log_softmax_float(self, logits, index, robust=True, out=None):
         self.calls.append(("fwd", tuple(logits.shape), tuple(index.shape), index.dtype, robust))
+        self.ptrs = getattr(self, "ptrs", []) + [logits.data_ptr()]
         assert logits.dim() == 2 and logits.is_contiguous() and index.dim() == 1
         lt = logits.as_subclass(torch.Tensor)
         lse = torch.logsumexp(lt, -1)
         logp = lt.gather(-1, index.as_subclass(torch.Tensor)[:, None])[:, 0] - lse
+        if out is not None:
+            out[0].copy_(logp)
+            out[1].copy_(lse)
+            return out
         return logp.as_subclass(FakeCuda), lse.as_subclass(FakeCuda)
 
-    def selective_log_softmax_float_backward(self, g, logits, index, lse):
+    def selective_log_softmax_float_backward(self, g, logits, index, lse, out=None):
         self.calls.append(("bwd", tuple(g.shape), tuple(logits.shape), tuple(index.shape), tuple(lse.shape)))
         gt, lt, it, st = (t.as_subclass(torch.Tensor) for t in (g, logits, index, lse))
-        out = -gt[:, None] * torch.exp(lt - st[:, None])
-        out[torch.arange(len(it)), it] += gt
-        return out.as_subclass(FakeCuda)
+        grad = -gt[:, None] * torch.exp(lt - st[:, None])
+        grad[torch.arange(len(it)), it] += gt
+        if out is not None:
+            assert out.is_contiguous()
+            out.copy_(grad)
+            return out
+        return grad.as_subclass(FakeCuda)
 
 
 def test_selective_dispatch_shapes_and_autograd():
@@ -191,6 +200,40 @@ def test_selective_dispatch_shapes_and_autograd():
     (ref * w).sum().backward()
     torch.testing.assert_close(logits.grad, l2.grad)
     torch.testing.assert_close(y.as_subclass(torch.Tensor), ref.detach())
+
+
+def test_selective_takes_trl_slices_without_copying_the_logits():
+    """trl passes logits[:, :-1, :]: rows contiguous within each leading index
+    but not across.  The kernel runs once per leading slice on views of the
+    caller's tensor (no copy); values and gradients match torch."""
+    from fuselse_amd.selective import make_selective_log_softmax
+
+    ext = FakeSelExt()
+    sls = make_selective_log_softmax(ext)
+    full = torch.randn(3, 5, 11)
+    logits = fake(full)[:, :-1, :]
+    assert not logits.is_contiguous()
+    leaf = full.clone().requires_grad_(True)
+    index = torch.randint(0, 11, (3, 4))
+    with torch.no_grad():
+        y0 = sls(logits, fake(index))
+    assert [c[1] for c in ext.calls] == [(4, 11)] * 3
+    assert ext.ptrs == [full[b].data_ptr() for b in range(3)]
+    ext.calls.clear()
+    view = fake(leaf)[:, :-1, :]
+    y = sls(view, fake(index))
+    w = torch.randn(3, 4)
+    (y.as_subclass(torch.Tensor) * w).sum().backward()
+    assert [c[0] for c in ext.calls] == ["fwd"] * 3 + ["bwd"] * 3
+    l2 = full.clone().requires_grad_(True)
+    ref = torch.log_softmax(l2[:, :-1, :], -1).gather(-1, index[..., None])[..., 0]
+    (ref * w).sum().backward()
+    torch.testing.assert_close(y0.as_subclass(torch.Tensor), ref.detach())
+    torch.testing.assert_close(leaf.grad, l2.grad)
+    # a layout with no contiguous slices is copied once
+    ext.calls.clear()
+    sls(fake(torch.randn(11, 3, 4)).permute(1, 2, 0), fake(torch.randint(0, 11, (3, 4))))
+    assert [c[1] for c in ext.calls] == [(12, 11)]
 
 
 def test_selective_fallbacks_do_not_touch_the_extension():

@@ -153,3 +153,36 @@ def test_selective_split_path_small_b(cuda):
     logp, lse = _ext().selective_log_softmax_float(torch.from_numpy(x).to(cuda), torch.from_numpy(idx).to(cuda))
     _check_fwd(logp.cpu().numpy(), lse.cpu().numpy(), x, idx)
     del rng
+
+
+@pytest.mark.parametrize("Bt,T,V", [(3, 34, 5003), (2, 400, 32000), (4, 9, 128256)])
+def test_selective_dropin_on_trl_slice(cuda, Bt, T, V):
+    """trl's actual argument, logits[:, :-1, :] (not contiguous): one launch per
+    leading slice on views of the caller's tensor.  Result and gradient
+    against torch autograd in fp64, and the gradient is the input's shape."""
+    print(f"case sls drop-in trl slice {Bt}x{T}x{V}", flush=True)
+    import fuselse_amd
+
+    rng = np.random.default_rng(T)
+    x = (rng.standard_normal((Bt, T, V)) * 2).astype(np.float32)
+    idx = rng.integers(0, V, (Bt, T - 1))
+    w = rng.standard_normal((Bt, T - 1)).astype(np.float32)
+    xd = torch.from_numpy(x).to(cuda).requires_grad_(True)
+    view = xd[:, :-1, :]
+    assert not view.is_contiguous()
+    y = fuselse_amd.selective_log_softmax(view, torch.from_numpy(idx).to(cuda))
+    (y * torch.from_numpy(w).to(cuda)).sum().backward()
+    xr = torch.from_numpy(x).double().requires_grad_(True)
+    ref = torch.log_softmax(xr[:, :-1, :], -1).gather(-1, torch.from_numpy(idx)[..., None])[..., 0]
+    (ref * torch.from_numpy(w).double()).sum().backward()
+    lse = torch.logsumexp(xr.detach()[:, :-1, :], -1).numpy()
+    assert np.all(np.abs(y.detach().cpu().numpy() - ref.detach().numpy()) <= 1e-5 * (np.abs(lse) + 1))
+    g = xd.grad.cpu().numpy()
+    assert (g[:, -1, :] == 0).all()
+    gw = np.abs(w)[..., None]
+    err = np.abs(g[:, :-1, :] - xr.grad.numpy()[:, :-1, :])
+    assert (err <= 1e-5 * np.abs(xr.grad.numpy()[:, :-1, :]) + 1e-6 * gw).all(), err.max()
+    with torch.no_grad():
+        y2 = fuselse_amd.selective_log_softmax(view, torch.from_numpy(idx).to(cuda))
+        y3 = fuselse_amd.selective_log_softmax(view.contiguous(), torch.from_numpy(idx).to(cuda))
+    torch.testing.assert_close(y2, y3, rtol=1e-6, atol=1e-6)
