@@ -591,7 +591,7 @@ def test_blocked_backward_product_form_deterministic(cuda, bs):
         assert torch.equal(ef, outs[0][0]) and torch.equal(pf, outs[0][1])
 
 
-@pytest.mark.parametrize("bs1,bs2", [(8, 4), (32, 2), (1, 16)])
+@pytest.mark.parametrize("bs1,bs2", [(8, 4), (32, 2), (1, 16), (48, 3)])
 def test_blocked_layer_autograd_two_layers(cuda, bs1, bs2):
     """pc.sparse_blocked_layer: two stacked block-layout layers with log-weights,
     outputs and gradients of the inputs and of both weight vectors against
