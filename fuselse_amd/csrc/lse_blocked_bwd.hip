@@ -26,7 +26,7 @@
 // chunk and parent group, the batch as K, the sums added to param_flows once
 // per (p, e)), and element flows (one wave per element row, its block edges
 // summed in a fixed order through the transposed structure).  Blocks of at
-// most 16 parents take both products in one pass instead (blocked_bwd_fused).
+// most 32 parents take both products in one pass instead (blocked_bwd_fused).
 // The result does not depend on scheduling, except that parameters shared by
 // several (block, parent, edge) triples receive their sums in any order.
 #include <math.h>
@@ -68,24 +68,32 @@ __device__ __forceinline__ float log_weight(float w) {
 
 // Four consecutive columns col .. col + 3 of a row; columns past the batch
 // read `fill`.  With VEC, col is a multiple of 4 and rows are 16-byte aligned.
+// ld4_raw issues the loads (columns past the batch read column 0) and
+// ld4_fill puts `fill` in those columns, so a kernel can issue a tile's loads
+// together behind a scheduling barrier before the first fill waits on one.
+template <bool VEC>
+__device__ __forceinline__ void ld4_raw(const float* __restrict__ row, int64_t col, int64_t batch, float (&v)[4]) {
+    if constexpr (VEC) {
+        const f32x4 t = *reinterpret_cast<const f32x4*>(row + (col < batch ? col : 0));
+        v[0] = t.x;
+        v[1] = t.y;
+        v[2] = t.z;
+        v[3] = t.w;
+    } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = row[col + u < batch ? col + u : 0];
+    }
+}
+template <bool VEC>
+__device__ __forceinline__ void ld4_fill(int64_t col, int64_t batch, float fill, float (&v)[4]) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = (VEC ? col : col + u) < batch ? v[u] : fill;
+}
 template <bool VEC>
 __device__ __forceinline__ void ld4(const float* __restrict__ row, int64_t col, int64_t batch, float fill,
                                     float (&v)[4]) {
-    if constexpr (VEC) {
-        const bool cv = col < batch;
-        const f32x4 t = *reinterpret_cast<const f32x4*>(row + (cv ? col : 0));
-        v[0] = cv ? t.x : fill;
-        v[1] = cv ? t.y : fill;
-        v[2] = cv ? t.z : fill;
-        v[3] = cv ? t.w : fill;
-    } else {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const bool cv = col + u < batch;
-            const float t = row[cv ? col + u : 0];
-            v[u] = cv ? t : fill;
-        }
-    }
+    ld4_raw<VEC>(row, col, batch, v);
+    ld4_fill<VEC>(col, batch, fill, v);
 }
 
 // R = g * exp(lw + m - o) for one (p, b); `left` when the pair must take the
@@ -490,25 +498,30 @@ __global__ __launch_bounds__(64) void blocked_bwd_params(float* __restrict__ par
 
 // x at a lane's cells of a 64-column tile (edges c0 + 16*et + 4*kq + r,
 // columns col .. col + 3; edges past ne read -inf, columns past the batch 0)
-// and the column maxima over the chunk's edges.
+// and the column maxima over the chunk's edges.  tile_x_raw issues the loads,
+// tile_x_finish masks them and takes the maxima; tile_x does both with a
+// scheduling barrier between, so every load is issued before the first use.
 template <int ET, bool VEC>
-__device__ __forceinline__ void tile_x(const float* __restrict__ xm, const int64_t* __restrict__ cids, int64_t ebase,
-                                       int64_t ne, int64_t c0, int kq, int64_t col, int64_t batch,
-                                       float (&xv)[ET][4][4], float (&m)[4]) {
+__device__ __forceinline__ void tile_x_raw(const float* __restrict__ xm, const int64_t* __restrict__ cids,
+                                           int64_t ebase, int64_t ne, int64_t c0, int kq, int64_t col,
+                                           int64_t batch, float (&xv)[ET][4][4]) {
 #pragma unroll
     for (int et = 0; et < ET; ++et)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int64_t e = c0 + 16 * et + 4 * kq + r;
-            ld4<VEC>(xm + cids[ebase + (e < ne ? e : ne - 1)] * batch, col, batch, 0.0f, xv[et][r]);
+            ld4_raw<VEC>(xm + cids[ebase + (e < ne ? e : ne - 1)] * batch, col, batch, xv[et][r]);
         }
-    // every load of the tile issued before the first use
-    __builtin_amdgcn_sched_barrier(0);
+}
+template <int ET, bool VEC>
+__device__ __forceinline__ void tile_x_finish(int64_t ne, int64_t c0, int kq, int64_t col, int64_t batch,
+                                              float (&xv)[ET][4][4], float (&m)[4]) {
 #pragma unroll
     for (int et = 0; et < ET; ++et)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const bool ev = c0 + 16 * et + 4 * kq + r < ne;
+            ld4_fill<VEC>(col, batch, 0.0f, xv[et][r]);
 #pragma unroll
             for (int u = 0; u < 4; ++u) xv[et][r][u] = ev ? xv[et][r][u] : -kInf;
         }
@@ -522,6 +535,14 @@ __device__ __forceinline__ void tile_x(const float* __restrict__ xm, const int64
         mu = fmaxf(mu, xor16(mu));
         m[u] = fmaxf(mu, xor32(mu));
     }
+}
+template <int ET, bool VEC>
+__device__ __forceinline__ void tile_x(const float* __restrict__ xm, const int64_t* __restrict__ cids, int64_t ebase,
+                                       int64_t ne, int64_t c0, int kq, int64_t col, int64_t batch,
+                                       float (&xv)[ET][4][4], float (&m)[4]) {
+    tile_x_raw<ET, VEC>(xm, cids, ebase, ne, c0, kq, col, batch, xv);
+    __builtin_amdgcn_sched_barrier(0);
+    tile_x_finish<ET, VEC>(ne, c0, kq, col, batch, xv, m);
 }
 
 // Both products in one pass, for blocks of at most 32 parents: one wave per
@@ -607,10 +628,22 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
 
     for (int64_t b0 = 0; b0 < batch; b0 += 64) {
         const int64_t col = b0 + 4 * jc;
+        // x, o and g of the whole tile are issued as one group: the tile
+        // waits for memory once, not once per load phase
         float m[4];
+        float ov[NKP][4], gv[NKP][4];
         {
             float xv[ET][4][4];
-            tile_x<ET, VEC>(xm, cids, ebase, ne, c0, kq, col, batch, xv, m);
+            tile_x_raw<ET, VEC>(xm, cids, ebase, ne, c0, kq, col, batch, xv);
+#pragma unroll
+            for (int ks = 0; ks < NKP; ++ks) {
+                const int64_t p = 4 * ks + kq;
+                const int64_t n = nrow0 + (p < bs ? p : bs - 1);
+                ld4_raw<VEC>(om + n * batch, col, batch, ov[ks]);
+                ld4_raw<VEC>(gf + n * batch, col, batch, gv[ks]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            tile_x_finish<ET, VEC>(ne, c0, kq, col, batch, xv, m);
 #pragma unroll
             for (int et = 0; et < ET; ++et)
 #pragma unroll
@@ -629,24 +662,17 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
         bool left = false;
 #pragma unroll
         for (int k0 = 0; k0 < NKP; k0 += KC) {
-            float rr[KC][4], ov[KC][4], gv[KC][4];
-#pragma unroll
-            for (int kk = 0; kk < KC; ++kk) {
-                const int64_t p = 4 * (k0 + kk) + kq;
-                const int64_t n = nrow0 + (p < bs ? p : bs - 1);
-                ld4<VEC>(om + n * batch, col, batch, -kInf, ov[kk]);
-                ld4<VEC>(gf + n * batch, col, batch, 0.0f, gv[kk]);
-            }
-            // every g and o load of the chunk issued before the first use
-            __builtin_amdgcn_sched_barrier(0);
+            float rr[KC][4];
 #pragma unroll
             for (int kk = 0; kk < KC; ++kk) {
                 const int ks = k0 + kk;
                 const bool pv = 4 * ks + kq < bs;
+                ld4_fill<VEC>(col, batch, -kInf, ov[ks]);
+                ld4_fill<VEC>(col, batch, 0.0f, gv[ks]);
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     bool lf;
-                    rr[kk][u] = r_factor(lwm[ks], m[u], ov[kk][u], gv[kk][u], pv, lf);
+                    rr[kk][u] = r_factor(lwm[ks], m[u], ov[ks][u], gv[ks][u], pv, lf);
                     left = left || lf;
                     rt[4 * ks + kq][4 * jc + u] = rr[kk][u];
                 }
