@@ -421,13 +421,16 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
         ms_np = _time_calls(torch, stream, lambda i: ext.sparse_blocked_backward(nf, ef, nm, em, params, pf, nids, cids,
                                                                                  pids, bs), 1, max(5, iters // 5))
         # algorithmic bytes of the whole call: node_flows and node_mars once,
-        # each block's child rows once, element_flows read and written, the
-        # weights read and param_flows read and written, the edge metadata
-        # (the edge-flow workspace's round trip is the kernels' own traffic)
-        bbytes = (2 * nbk * bs * batch * 4 + nbk * ne * batch * 4 + 2 * nel * batch * 4 + 3 * nbk * ne * bs * 4
+        # each block's child rows once, the element_flows rows some block edge
+        # reaches read and written (random child ids leave about 37% of the
+        # rows untouched), the weights read and param_flows read and written,
+        # the edge metadata (the edge-flow workspace's round trip is the
+        # kernels' own traffic)
+        touched = int(torch.unique(cids).numel())
+        bbytes = (2 * nbk * bs * batch * 4 + nbk * ne * batch * 4 + 2 * touched * batch * 4 + 3 * nbk * ne * bs * 4
                   + nbk * ne * 16)
         rec("C5_blocked_bwd_fp32_8192x32_e32_b512", ms, bbytes, nnz=nbk * bs * ne,
-            without_plan_us=round(ms_np * 1e3, 1), plan_build_ms=round(plan_ms, 2))
+            without_plan_us=round(ms_np * 1e3, 1), plan_build_ms=round(plan_ms, 2), element_rows_touched=touched)
         del em, nm, nf, ef, pf, plan
     return res
 
