@@ -115,6 +115,55 @@ __device__ __forceinline__ int64_t logical_id(int64_t id0) {
 
 }  // namespace
 
+// x at a lane's cells of a 64-column tile (edges c0 + 16*et + 4*kq + r,
+// columns col .. col + 3; edges past ne read -inf, columns past the batch 0)
+// and the column maxima over the chunk's edges.  tile_x_raw issues the loads,
+// tile_x_finish masks them and takes the maxima; tile_x does both with a
+// scheduling barrier between, so every load is issued before the first use.
+template <int ET, bool VEC>
+__device__ __forceinline__ void tile_x_raw(const float* __restrict__ xm, const int64_t* __restrict__ cids,
+                                           int64_t ebase, int64_t ne, int64_t c0, int kq, int64_t col,
+                                           int64_t batch, float (&xv)[ET][4][4]) {
+#pragma unroll
+    for (int et = 0; et < ET; ++et)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t e = c0 + 16 * et + 4 * kq + r;
+            ld4_raw<VEC>(xm + cids[ebase + (e < ne ? e : ne - 1)] * batch, col, batch, xv[et][r]);
+        }
+}
+template <int ET, bool VEC>
+__device__ __forceinline__ void tile_x_finish(int64_t ne, int64_t c0, int kq, int64_t col, int64_t batch,
+                                              float (&xv)[ET][4][4], float (&m)[4]) {
+#pragma unroll
+    for (int et = 0; et < ET; ++et)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const bool ev = c0 + 16 * et + 4 * kq + r < ne;
+            ld4_fill<VEC>(col, batch, 0.0f, xv[et][r]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) xv[et][r][u] = ev ? xv[et][r][u] : -kInf;
+        }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        float mu = xv[0][0][u];
+#pragma unroll
+        for (int et = 0; et < ET; ++et)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mu = fmaxf(mu, xv[et][r][u]);
+        mu = fmaxf(mu, xor16(mu));
+        m[u] = fmaxf(mu, xor32(mu));
+    }
+}
+template <int ET, bool VEC>
+__device__ __forceinline__ void tile_x(const float* __restrict__ xm, const int64_t* __restrict__ cids, int64_t ebase,
+                                       int64_t ne, int64_t c0, int kq, int64_t col, int64_t batch,
+                                       float (&xv)[ET][4][4], float (&m)[4]) {
+    tile_x_raw<ET, VEC>(xm, cids, ebase, ne, c0, kq, col, batch, xv);
+    __builtin_amdgcn_sched_barrier(0);
+    tile_x_finish<ET, VEC>(ne, c0, kq, col, batch, xv, m);
+}
+
 // Edge flows F[j, e, b] for edges c0 .. c0 + 16*ET - 1 and columns b0 .. b0 + 63.
 // Product Z[e, b] = sum_p A[p, e] R[p, b]: lane l supplies A[e = c0 + 16*et + l%16]
 // [p = pc0 + 4*ks + l/16] and R[p][b = b0 + 4*(l%16) + u] (N-tile u) and holds
@@ -148,28 +197,8 @@ __global__ __launch_bounds__(64) void blocked_bwd_edges(float* __restrict__ edge
 
     // x at the lane's output cells; edges past ne read -inf, columns past the batch 0
     float xv[ET][4][4];
-#pragma unroll
-    for (int et = 0; et < ET; ++et)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int64_t e = c0 + 16 * et + 4 * kq + r;
-            const bool ev = e < ne;
-            float v[4];
-            ld4<VEC>(xm + cids[ebase + (ev ? e : ne - 1)] * batch, col, batch, 0.0f, v);
-#pragma unroll
-            for (int u = 0; u < 4; ++u) xv[et][r][u] = ev ? v[u] : -kInf;
-        }
     float m[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        float mu = xv[0][0][u];
-#pragma unroll
-        for (int et = 0; et < ET; ++et)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) mu = fmaxf(mu, xv[et][r][u]);
-        mu = fmaxf(mu, xor16(mu));
-        m[u] = fmaxf(mu, xor32(mu));
-    }
+    tile_x<ET, VEC>(xm, cids, ebase, ne, c0, kq, col, batch, xv, m);
 #pragma unroll
     for (int et = 0; et < ET; ++et)
 #pragma unroll
@@ -198,15 +227,25 @@ __global__ __launch_bounds__(64) void blocked_bwd_edges(float* __restrict__ edge
     for (int64_t pc0 = 0; pc0 < bs; pc0 += 4 * KP) {
         float a[KP][ET], rr[KP][4];
         uint32_t left = 0;  // bit 4*ks + u
+        float wraw[KP][ET], ovk[KP][4], gvk[KP][4];
+#pragma unroll
+        for (int ks = 0; ks < KP; ++ks) {
+            const int64_t p = pc0 + 4 * ks + kq;
+            const int64_t pcl = p < bs ? p : bs - 1;
+#pragma unroll
+            for (int et = 0; et < ET; ++et) wraw[ks][et] = params[qa[et] + pcl];
+            ld4_raw<VEC>(om + (nrow0 + pcl) * batch, col, batch, ovk[ks]);
+            ld4_raw<VEC>(gf + (nrow0 + pcl) * batch, col, batch, gvk[ks]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int ks = 0; ks < KP; ++ks) {
             const int64_t p = pc0 + 4 * ks + kq;
             const bool pv = p < bs;
-            const int64_t pcl = pv ? p : bs - 1;
             float wv[ET];
 #pragma unroll
             for (int et = 0; et < ET; ++et) {
-                const float w = weight_term<LOGP>(params[qa[et] + pcl]);
+                const float w = weight_term<LOGP>(wraw[ks][et]);
                 wv[et] = eva[et] && pv ? w : (LOGP ? -kInf : 0.0f);
             }
             float wm = wv[0];
@@ -219,13 +258,12 @@ __global__ __launch_bounds__(64) void blocked_bwd_edges(float* __restrict__ edge
                             : LOGP ? (wm == -kInf ? 0.0f : fexp2((wv[et] - wm) * kLog2e))
                                    : wv[et] / wm;
             const float lwm = LOGP ? wm : logf(wm);
-            float ov[4], gv[4];
-            ld4<VEC>(om + (nrow0 + pcl) * batch, col, batch, -kInf, ov);
-            ld4<VEC>(gf + (nrow0 + pcl) * batch, col, batch, 0.0f, gv);
+            ld4_fill<VEC>(col, batch, -kInf, ovk[ks]);
+            ld4_fill<VEC>(col, batch, 0.0f, gvk[ks]);
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 bool lf;
-                rr[ks][u] = r_factor(lwm, m[u], ov[u], gv[u], pv, lf);
+                rr[ks][u] = r_factor(lwm, m[u], ovk[ks][u], gvk[ks][u], pv, lf);
                 left |= (uint32_t)lf << (4 * ks + u);
             }
         }
@@ -377,15 +415,27 @@ __global__ __launch_bounds__(64) void blocked_bwd_params(float* __restrict__ par
 
     for (int64_t b0 = 0; b0 < batch; b0 += 4 * CW) {
         const int64_t cb = b0 + CW * kq;  // K-step ks takes column cb + ks
-        float xv[ET][CW];
+        float xv[ET][CW], ovp[MT][CW], gvp[MT][CW];
 #pragma unroll
-        for (int et = 0; et < ET; ++et)
+        for (int q = 0; q < CW / 4; ++q) {
 #pragma unroll
-            for (int q = 0; q < CW / 4; ++q) {
-                float v[4];
-                ld4<VEC>(xrow[et], cb + 4 * q, batch, 0.0f, v);
+            for (int et = 0; et < ET; ++et)
+                ld4_raw<VEC>(xrow[et], cb + 4 * q, batch, *reinterpret_cast<float(*)[4]>(&xv[et][4 * q]));
 #pragma unroll
-                for (int u = 0; u < 4; ++u) xv[et][4 * q + u] = evb[et] ? v[u] : -kInf;
+            for (int pt = 0; pt < MT; ++pt) {
+                ld4_raw<VEC>(orow[pt], cb + 4 * q, batch, *reinterpret_cast<float(*)[4]>(&ovp[pt][4 * q]));
+                ld4_raw<VEC>(grow[pt], cb + 4 * q, batch, *reinterpret_cast<float(*)[4]>(&gvp[pt][4 * q]));
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < CW / 4; ++q)
+#pragma unroll
+            for (int et = 0; et < ET; ++et) {
+                float(&v)[4] = *reinterpret_cast<float(*)[4]>(&xv[et][4 * q]);
+                ld4_fill<VEC>(cb + 4 * q, batch, 0.0f, v);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) v[u] = evb[et] ? v[u] : -kInf;
             }
         float m[CW];
 #pragma unroll
@@ -407,9 +457,10 @@ __global__ __launch_bounds__(64) void blocked_bwd_params(float* __restrict__ par
             left[pt] = 0;
 #pragma unroll
             for (int q = 0; q < CW / 4; ++q) {
-                float ov[4], gv[4];
-                ld4<VEC>(orow[pt], cb + 4 * q, batch, -kInf, ov);
-                ld4<VEC>(grow[pt], cb + 4 * q, batch, 0.0f, gv);
+                float(&ov)[4] = *reinterpret_cast<float(*)[4]>(&ovp[pt][4 * q]);
+                float(&gv)[4] = *reinterpret_cast<float(*)[4]>(&gvp[pt][4 * q]);
+                ld4_fill<VEC>(cb + 4 * q, batch, -kInf, ov);
+                ld4_fill<VEC>(cb + 4 * q, batch, 0.0f, gv);
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     bool lf;
@@ -494,55 +545,6 @@ __global__ __launch_bounds__(64) void blocked_bwd_params(float* __restrict__ par
             }
         }
     }
-}
-
-// x at a lane's cells of a 64-column tile (edges c0 + 16*et + 4*kq + r,
-// columns col .. col + 3; edges past ne read -inf, columns past the batch 0)
-// and the column maxima over the chunk's edges.  tile_x_raw issues the loads,
-// tile_x_finish masks them and takes the maxima; tile_x does both with a
-// scheduling barrier between, so every load is issued before the first use.
-template <int ET, bool VEC>
-__device__ __forceinline__ void tile_x_raw(const float* __restrict__ xm, const int64_t* __restrict__ cids,
-                                           int64_t ebase, int64_t ne, int64_t c0, int kq, int64_t col,
-                                           int64_t batch, float (&xv)[ET][4][4]) {
-#pragma unroll
-    for (int et = 0; et < ET; ++et)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int64_t e = c0 + 16 * et + 4 * kq + r;
-            ld4_raw<VEC>(xm + cids[ebase + (e < ne ? e : ne - 1)] * batch, col, batch, xv[et][r]);
-        }
-}
-template <int ET, bool VEC>
-__device__ __forceinline__ void tile_x_finish(int64_t ne, int64_t c0, int kq, int64_t col, int64_t batch,
-                                              float (&xv)[ET][4][4], float (&m)[4]) {
-#pragma unroll
-    for (int et = 0; et < ET; ++et)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const bool ev = c0 + 16 * et + 4 * kq + r < ne;
-            ld4_fill<VEC>(col, batch, 0.0f, xv[et][r]);
-#pragma unroll
-            for (int u = 0; u < 4; ++u) xv[et][r][u] = ev ? xv[et][r][u] : -kInf;
-        }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        float mu = xv[0][0][u];
-#pragma unroll
-        for (int et = 0; et < ET; ++et)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) mu = fmaxf(mu, xv[et][r][u]);
-        mu = fmaxf(mu, xor16(mu));
-        m[u] = fmaxf(mu, xor32(mu));
-    }
-}
-template <int ET, bool VEC>
-__device__ __forceinline__ void tile_x(const float* __restrict__ xm, const int64_t* __restrict__ cids, int64_t ebase,
-                                       int64_t ne, int64_t c0, int kq, int64_t col, int64_t batch,
-                                       float (&xv)[ET][4][4], float (&m)[4]) {
-    tile_x_raw<ET, VEC>(xm, cids, ebase, ne, c0, kq, col, batch, xv);
-    __builtin_amdgcn_sched_barrier(0);
-    tile_x_finish<ET, VEC>(ne, c0, kq, col, batch, xv, m);
 }
 
 // Both products in one pass, for blocks of at most 32 parents: one wave per
