@@ -551,8 +551,9 @@ __global__ __launch_bounds__(64) void blocked_bwd_params(float* __restrict__ par
 // (block, edge chunk) walks the batch in 64-column tiles.  Per tile it loads
 // x (the edge-flow cells), g and o once, runs the product over parents as
 // blocked_bwd_edges does, then writes the tile's X and R to LDS and reads
-// them back transposed for the product over the batch (rows padded to 65
-// floats, so the transposed reads of 16 rows hit 16 banks).  The weights are
+// them back transposed for the product over the batch (rows padded to 68
+// floats: every LDS access is one 16-byte vector per lane, and each group of
+// 8 lanes covers 32 distinct banks).  The weights are
 // taken once per wave.  Pairs left out of the products are only counted in
 // the tile loop; when there are any, a second pass over the tiles finds them
 // again with the same arithmetic and adds their one-by-one terms (the code
@@ -569,10 +570,10 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
                                                         const int64_t* __restrict__ pids, int64_t ne, int64_t bs,
                                                         int64_t batch, int64_t chunks, int64_t items, int64_t id0) {
     constexpr int MP = (NKP + 3) / 4;
-    constexpr int LD = 65;  // padded LDS row
+    constexpr int LD = 68;  // padded LDS row: 16-byte aligned, four banks past the last row's
     constexpr int KC = NKP < 4 ? NKP : 4;
-    __shared__ float xt[16 * ET][LD];   // X of the tile: [edge - c0][column - b0]; one-by-one edge terms
-    __shared__ float rt[16 * MP][LD];   // R of the tile: [parent][column - b0]
+    __shared__ __align__(16) float xt[16 * ET][LD];  // X of the tile: [edge - c0][column - b0]; one-by-one edge terms
+    __shared__ __align__(16) float rt[16 * MP][LD];  // R of the tile: [parent][column - b0]
     __shared__ float gx[16 * MP][16 * ET];  // one-by-one parameter terms: [parent][edge - c0]
     const int64_t id = logical_id(id0);
     if (id >= items) return;
@@ -649,11 +650,13 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
 #pragma unroll
             for (int et = 0; et < ET; ++et)
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
+                for (int r = 0; r < 4; ++r) {
+                    f32x4 xe;
 #pragma unroll
                     for (int u = 0; u < 4; ++u)
-                        xt[16 * et + 4 * kq + r][4 * jc + u] =
-                            __builtin_isfinite(m[u]) ? fexp2((xv[et][r][u] - m[u]) * kLog2e) : 0.0f;
+                        xe[u] = __builtin_isfinite(m[u]) ? fexp2((xv[et][r][u] - m[u]) * kLog2e) : 0.0f;
+                    *reinterpret_cast<f32x4*>(&xt[16 * et + 4 * kq + r][4 * jc]) = xe;
+                }
         }  // the tile's X lives in xt from here
 
         f32x4 z[ET][4];
@@ -676,8 +679,8 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
                     bool lf;
                     rr[kk][u] = r_factor(lwm[ks], m[u], ov[ks][u], gv[ks][u], pv, lf);
                     left = left || lf;
-                    rt[4 * ks + kq][4 * jc + u] = rr[kk][u];
                 }
+                *reinterpret_cast<f32x4*>(&rt[4 * ks + kq][4 * jc]) = f32x4{rr[kk][0], rr[kk][1], rr[kk][2], rr[kk][3]};
             }
 #pragma unroll
             for (int kk = 0; kk < KC; ++kk)
@@ -692,24 +695,26 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
         if constexpr (4 * NKP < 16 * MP) {
 #pragma unroll
             for (int pr = 4 * NKP + kq; pr < 16 * MP; pr += 4)
-#pragma unroll
-                for (int u = 0; u < 4; ++u) rt[pr][4 * jc + u] = 0.0f;
+                *reinterpret_cast<f32x4*>(&rt[pr][4 * jc]) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
         __builtin_amdgcn_wave_barrier();
         // product over the batch: lane l supplies R[16*pt + l%16][16*(l/16) + ks]
-        // and X[16*et + l%16][same column]
-#pragma unroll 2
-        for (int ks = 0; ks < 16; ++ks) {
-            float ra[MP], xb[ET];
+        // and X[16*et + l%16][same column], K-steps ks in order, read four at a
+        // time as one 16-byte vector per row
+#pragma unroll 1
+        for (int i = 0; i < 4; ++i) {
+            f32x4 ra[MP], xb[ET];
 #pragma unroll
-            for (int pt = 0; pt < MP; ++pt) ra[pt] = rt[16 * pt + jc][16 * kq + ks];
+            for (int pt = 0; pt < MP; ++pt) ra[pt] = *reinterpret_cast<const f32x4*>(&rt[16 * pt + jc][16 * kq + 4 * i]);
 #pragma unroll
-            for (int et = 0; et < ET; ++et) xb[et] = xt[16 * et + jc][16 * kq + ks];
+            for (int et = 0; et < ET; ++et) xb[et] = *reinterpret_cast<const f32x4*>(&xt[16 * et + jc][16 * kq + 4 * i]);
 #pragma unroll
-            for (int pt = 0; pt < MP; ++pt)
+            for (int t = 0; t < 4; ++t)
 #pragma unroll
-                for (int et = 0; et < ET; ++et)
-                    gacc[pt][et] = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[pt], xb[et], gacc[pt][et], 0, 0, 0);
+                for (int pt = 0; pt < MP; ++pt)
+#pragma unroll
+                    for (int et = 0; et < ET; ++et)
+                        gacc[pt][et] = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[pt][t], xb[et][t], gacc[pt][et], 0, 0, 0);
         }
         // edge flows F = X .* Z at rows c0 + 16*et + 4*kq + r
 #pragma unroll
@@ -717,11 +722,12 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t e = c0 + 16 * et + 4 * kq + r;
+                const f32x4 xe = *reinterpret_cast<const f32x4*>(&xt[16 * et + 4 * kq + r][4 * jc]);
                 float res[4];
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     const float zz = z[et][u][r];
-                    res[u] = zz == 0.0f ? 0.0f : xt[16 * et + 4 * kq + r][4 * jc + u] * zz;
+                    res[u] = zz == 0.0f ? 0.0f : xe[u] * zz;
                 }
                 if (e >= ne) continue;
                 float* orow = edge_flows + (ebase + e) * batch;
@@ -790,8 +796,7 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
             for (int et = 0; et < ET; ++et)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) xt[16 * et + 4 * kq + r][4 * jc + u] = 0.0f;
+                    *reinterpret_cast<f32x4*>(&xt[16 * et + 4 * kq + r][4 * jc]) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             __builtin_amdgcn_wave_barrier();
             for (int ll = 0; ll < 64; ++ll) {
                 if (l == ll) {
