@@ -694,8 +694,8 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
         // rows of R past 4*NKP (up to the 16-row tiles) hold zeros
         if constexpr (4 * NKP < 16 * MP) {
 #pragma unroll
-            for (int pr = 4 * NKP + kq; pr < 16 * MP; pr += 4)
-                *reinterpret_cast<f32x4*>(&rt[pr][4 * jc]) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int i = 0; i < 4 * MP - NKP; ++i)
+                *reinterpret_cast<f32x4*>(&rt[4 * (NKP + i) + kq][4 * jc]) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
         __builtin_amdgcn_wave_barrier();
         // product over the batch: lane l supplies R[16*pt + l%16][16*(l/16) + ks]
