@@ -63,7 +63,9 @@ __device__ __forceinline__ int pair(int a, int b, const int* __restrict__ lut) {
     const uint32_t shc = sh < 31u ? sh : 31u;
     const uint32_t fr = 0x10000u | ((uint32_t)sub & 0xFFFFu);
     const uint32_t m = fr >> shc;
-    const uint32_t off = ((fr >> 8) >> shc) & 0xFCu;
+    // (fr >> 8) >> shc == m >> 8 (logical shifts compose); byte 1 of m masked
+    // is one instruction on this target
+    const uint32_t off = (m >> 8) & 0xFCu;
     return (int)((uint32_t)hi + m + (uint32_t)*reinterpret_cast<const int*>(reinterpret_cast<const char*>(lut) + off));
 }
 
