@@ -552,8 +552,8 @@ __global__ __launch_bounds__(64) void blocked_bwd_params(float* __restrict__ par
 // x (the edge-flow cells), g and o once, runs the product over parents as
 // blocked_bwd_edges does, then writes the tile's X and R to LDS and reads
 // them back transposed for the product over the batch (rows padded to 68
-// floats: every LDS access is one 16-byte vector per lane, and each group of
-// 8 lanes covers 32 distinct banks).  The weights are
+// floats, so every LDS access is one aligned 16-byte vector per lane).  The
+// weights are
 // taken once per wave.  Pairs left out of the products are only counted in
 // the tile loop; when there are any, a second pass over the tiles finds them
 // again with the same arithmetic and adds their one-by-one terms (the code
@@ -570,7 +570,7 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
                                                         const int64_t* __restrict__ pids, int64_t ne, int64_t bs,
                                                         int64_t batch, int64_t chunks, int64_t items, int64_t id0) {
     constexpr int MP = (NKP + 3) / 4;
-    constexpr int LD = 68;  // padded LDS row: 16-byte aligned, four banks past the last row's
+    constexpr int LD = 68;  // padded LDS row, 16-byte aligned
     constexpr int KC = NKP < 4 ? NKP : 4;
     __shared__ __align__(16) float xt[16 * ET][LD];  // X of the tile: [edge - c0][column - b0]; one-by-one edge terms
     __shared__ __align__(16) float rt[16 * MP][LD];  // R of the tile: [parent][column - b0]
