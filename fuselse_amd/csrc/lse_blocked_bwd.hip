@@ -574,7 +574,11 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
     constexpr int KC = NKP < 4 ? NKP : 4;
     __shared__ __align__(16) float xt[16 * ET][LD];  // X of the tile: [edge - c0][column - b0]; one-by-one edge terms
     __shared__ __align__(16) float rt[16 * MP][LD];  // R of the tile: [parent][column - b0]
-    __shared__ float gx[16 * MP][16 * ET];  // one-by-one parameter terms: [parent][edge - c0]
+    // one-by-one parameter terms, [parent][edge - c0]: used only by the second
+    // pass and the final adds, after the last read of rt, so they share its
+    // storage (keeps a workgroup at 17 KB of LDS: eight per CU)
+    static_assert(16 * MP * 16 * ET <= 16 * MP * LD, "parameter terms fit in the R tile");
+    float(*gx)[16 * ET] = reinterpret_cast<float(*)[16 * ET]>(&rt[0][0]);
     const int64_t id = logical_id(id0);
     if (id >= items) return;
     const int64_t c = id % chunks;
