@@ -12,12 +12,15 @@
  *   or_intlse_cpu_row[_neg_inf]    : compiled reference (oracle/_ref), bit-exact.
  *   or_q10_6_pair                  : closed forms, exhaustive log2 error bound,
  *                                    LUT = round(Q16 LUT / 1024) identity.
- *   or_q16_gpu_rows / or_q10_6_rows: closed-form special rows (single chain,
- *                                    all-equal rows) plus the reference's published
- *                                    accuracy envelopes (mean |err| vs fp64 per N);
- *                                    exact NVIDIA bits are otherwise unpinned.
- *   or_sparse_q16_*                : closed forms (one edge, equal edges) and the
- *                                    float oracle envelope.
+ *   or_q16_gpu_rows / or_q10_6_rows: hand-computed rows that fix the tree shape
+ *                                    (single chain, all-equal rows, prefix/suffix
+ *                                    layout, chunk t+256k striding in ascending k
+ *                                    with x..w element order) plus the reference's
+ *                                    published accuracy envelopes (mean |err| vs
+ *                                    fp64 per N).
+ *   or_sparse_q16_*                : closed forms (one edge, equal edges), a
+ *                                    hand-computed row fixing the e mod ET edge
+ *                                    striding, and the float oracle envelope.
  *   or_fuselse_cpu_rows            : glibc expf/log1pf sequential chain; pinned by
  *                                    fp64 envelope and N=2 textbook identity.
  */

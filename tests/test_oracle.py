@@ -251,6 +251,57 @@ def test_gpu_tree_prefix_and_suffix():
     assert raw_al == want_al
 
 
+def _one(pair, a, b):
+    return int(pair(np.array([a], np.int32), np.array([b], np.int32))[0])
+
+
+@pytest.mark.parametrize("kind", ["q16", "q10_6"])
+def test_gpu_tree_chunk_striding(kind):
+    """Chunk-to-thread striding of the GPU trees (lse_kernel.cu:110,
+    lse_kernel_q10_6.cu:96): virtual thread t folds chunks t, t+256, t+512, ...
+    in ascending order, each chunk's elements in x, y, z, w order.
+
+    An aligned row of N = 3072 has 768 four-element chunks.  Every element is a
+    filler far below the rest (more than 16 units of the format, also after the
+    fillers' own chains and butterflies), so each pair with a filler is exact,
+    except for five values: A at chunk 0, B at chunk 256, D and D2 at elements
+    0 and 3 of chunk 512 (all thread 0) and C at chunk 1 (thread 1).  Thread 0
+    is then chain(A, B, D, D2); threads 0 and 1 meet at the butterfly's last
+    warp level and the other lanes carry fillers or the identity, so the row is
+    pair(chain(A, B, D, D2), C).  The expected value is computed by hand from
+    the pair op; the alternatives a plausible slip would give (descending chunk
+    order, chunk elements in w..x order, contiguous thread ranges: thread 0 =
+    {A, C}, thread 85 = {B}, thread 170 = {D, D2}) are checked to differ."""
+    if kind == "q16":
+        pair, dt, filler = O.q16_pair, np.int32, -50 * 65536
+        A, B, D, D2, C = 124043, 134170, 197962, 249158, 9136
+    else:
+        pair, dt, filler = O.q10_6_pair, np.int16, -20000
+        A, B, D, D2, C = 202, 137, 89, 137, 114
+    row = np.full(3072, filler, dt)
+    row[4 * 0] = A
+    row[4 * 256] = B
+    row[4 * 512] = D
+    row[4 * 512 + 3] = D2
+    row[4 * 1] = C
+    raw = (O.q16_gpu_rows if kind == "q16" else O.q10_6_rows)(row[None, :], raw=True)[1][0]
+
+    def chain(vals):
+        acc = vals[0]
+        for v in vals[1:]:
+            acc = _one(pair, acc, v)
+        return acc
+
+    want = _one(pair, chain([A, B, D, D2]), C)
+    wrong = {
+        "descending chunks": _one(pair, chain([D2, D, B, A]), C),
+        "chunk elements w..x": _one(pair, chain([A, B, D2, D]), C),
+        "contiguous threads": _one(pair, _one(pair, _one(pair, A, C), B), chain([D, D2])),
+    }
+    assert all(v != want for v in wrong.values()), wrong
+    assert raw == want, (raw, want, wrong)
+
+
 # Published envelopes: intlse_gpu / intlse_nolut / intlse_cpu mean |err| vs fp64
 # at B=512, 20 seeds, inputs U(lo, 0) (experiment_microbenchmark/microbench/
 # outputs/benchmark_results.json, ranges U(-1,0), U(-100,0), U(-500,0)).
@@ -329,6 +380,40 @@ def test_sparse_q16_closed_forms():
     # an empty node gives -inf
     out = O.sparse_q16_csr(child, np.array([0, 0], np.int64), np.zeros(0, np.int32), np.zeros(0, np.float32))
     assert np.all(np.isneginf(out))
+
+
+def test_sparse_q16_edge_striding():
+    """Edge-to-chain striding of the sparse Q16 tree (sparse_q16_kernel.cu:110):
+    with fan-in 9 there are ET = 2 chains, chain c folding edges c, c+2, c+4, ...
+    in ascending order from the identity seed.  Edges 0, 1, 2 and 4 carry
+    values; the other edges are fillers 100 nats lower, whose pairs are exact.
+    So chain 0 = chain(a0, a2, a4), chain 1 = a1, and the node is
+    pair(chain 0, chain 1).  A contiguous split (chain 0 = edges 0..4) would give
+    chain(a0, a1, a2, a4), and a descending walk chain(a4, a2, a0) paired with
+    a1; both are checked to differ."""
+    vals = np.full(9, -100.0, np.float32)
+    vals[[0, 1, 2, 4]] = np.array([-1.25, -0.5, -0.25, 0.375], np.float32)
+    child = vals[:, None].copy()  # 9 children x batch 1, one child per edge
+    lp = np.full(9, -0.5, np.float32)
+    out = O.sparse_q16_csr(child, np.array([0, 9], np.int64), np.arange(9, dtype=np.int32), lp)
+    q = [int(O.q16_quant(np.array([vals[e] + lp[e]], np.float32), "sparse")[0]) for e in range(9)]
+    p = O.q16_pair
+
+    def chain(vs):
+        acc = vs[0]
+        for v in vs[1:]:
+            acc = _one(p, acc, v)
+        return acc
+
+    want = _one(p, chain([q[0], q[2], q[4]]), q[1])
+    wrong = {"contiguous": chain([q[0], q[1], q[2], q[4]]),
+             "descending": _one(p, chain([q[4], q[2], q[0]]), q[1])}
+    assert all(v != want for v in wrong.values()), wrong
+    assert out[0, 0] == np.float32(np.float32(want) * O.Q16_OUT), (out[0, 0], want, wrong)
+    # the block layout walks the same chains
+    nm = O.sparse_q16_blocked(np.zeros((1, 1), np.float32), child, lp.reshape(1, 1, 9),
+                              np.array([0], np.int64), np.arange(9, dtype=np.int64).reshape(1, 9), 1)
+    assert nm[0, 0] == out[0, 0]
 
 
 def test_sparse_q16_tracks_float_oracle():
