@@ -436,8 +436,12 @@ static void launch(const LAYOUT& L, const float* child, const float* out_any, in
 // The kernel walks the transposed structure (CSC: for child c the edges that
 // point at it, each with its parent node): one wave per child row, every
 // 512-column tile of the batch in turn.  Each child row and each edge belongs
-// to one wave, so both gradients are written once, without atomics, and the
-// summation order is fixed.
+// to one wave.  grad_child is accumulated in registers and written once.
+// grad_lw[e] is stored by the first column tile and, for batches over 512
+// columns, increased by the later tiles with a no-return atomic add; all of
+// these come from lane 0 of the one wave that owns edge e, in tile order, and
+// same-address accesses of one lane are performed in program order, so the
+// summation order is fixed and the result deterministic.
 // ---------------------------------------------------------------------------
 struct ParentMeta {
     int64_t node;

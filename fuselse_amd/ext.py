@@ -251,11 +251,15 @@ def batched_logsumexp_bf16(x: torch.Tensor, robust: bool = False) -> torch.Tenso
 # ---------------------------------------------------------------------------
 # IntLSE (fixed point)
 # ---------------------------------------------------------------------------
-def _acc_ptr(acc_out) -> int:
+def _acc_ptr(acc_out, input: torch.Tensor) -> int:
+    """Device pointer of the optional raw-accumulator output: the kernels write
+    acc_out[r] for every row r < B, so it must hold B int32 on input's GPU."""
     if acc_out is None:
         return 0
     _check(acc_out.is_cuda and acc_out.dtype == torch.int32 and acc_out.is_contiguous(),
            "acc_out must be a contiguous CUDA int32 tensor")
+    _check(acc_out.device == input.device, "acc_out must be on the input's device")
+    _check(acc_out.numel() >= input.shape[0], "acc_out must hold one int32 per row")
     return acc_out.data_ptr()
 
 
@@ -270,7 +274,7 @@ def _intlse_q16_f32(input: torch.Tensor, use_lut: bool, acc_out=None) -> torch.T
     if B == 0:
         return out
     with _on_device(input):
-        _lib.call("fl_intlse_q16_f32", input.data_ptr(), out.data_ptr(), _acc_ptr(acc_out), B, N, int(use_lut),
+        _lib.call("fl_intlse_q16_f32", input.data_ptr(), out.data_ptr(), _acc_ptr(acc_out, input), B, N, int(use_lut),
                   _stream(input))
     return out
 
@@ -298,7 +302,7 @@ def batched_logsumexp_q16_i32(input: torch.Tensor, use_lut: bool = True, acc_out
     if B == 0:
         return out
     with _on_device(input):
-        _lib.call("fl_intlse_q16_i32", input.data_ptr(), out.data_ptr(), _acc_ptr(acc_out), B, N, int(use_lut),
+        _lib.call("fl_intlse_q16_i32", input.data_ptr(), out.data_ptr(), _acc_ptr(acc_out, input), B, N, int(use_lut),
                   _stream(input))
     return out
 
@@ -315,7 +319,7 @@ def batched_logsumexp_q10_6(input: torch.Tensor, acc_out=None) -> torch.Tensor:
     if B == 0:
         return out
     with _on_device(input):
-        _lib.call("fl_intlse_q10_6", input.data_ptr(), out.data_ptr(), _acc_ptr(acc_out), B, N, _stream(input))
+        _lib.call("fl_intlse_q10_6", input.data_ptr(), out.data_ptr(), _acc_ptr(acc_out, input), B, N, _stream(input))
     return out
 
 

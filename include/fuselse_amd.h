@@ -173,7 +173,11 @@ int fl_sparse_blocked_fwd(float* node_mars, const float* element_mars, const flo
  * edge ids pointing at each child in increasing order; csc_nodes int32 [nnz],
  * the parent node of each of those edges.  child, grad_child: fp32
  * [num_children, batch]; out, grad_out: fp32 [num_nodes, batch]; both
- * gradients are written (not accumulated).  Deterministic: no atomics.
+ * gradients are written (not accumulated).  Deterministic: one wave owns each
+ * child row and each edge.  grad_child is written once; grad_logparams[e] is
+ * stored by the first 512-column tile of the batch and, when batch > 512,
+ * increased by the later tiles with atomic adds from that same wave in tile
+ * order, so the summation order is fixed.
  * ------------------------------------------------------------------------- */
 int fl_sparse_csr_bwd(const float* child, const float* out, const float* grad_out, const float* logparams,
                       const int64_t* csc_offsets, const int32_t* csc_edges, const int32_t* csc_nodes,

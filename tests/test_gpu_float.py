@@ -83,6 +83,46 @@ def test_fwd_f32_c2_full_size(cuda):
     _close(got2, O.lse_fp64(x), RTOL32)
 
 
+def test_bwd_f32_c2_full_size(cuda):
+    """BASELINE C2 fused backward at (512, 128256) with g ~ N(0, 1), the
+    bench's workload (fused_fp32_kernel.cu:135-150): every element against
+    g * exp(x - lse) in fp64, and each row's sum against g."""
+    print("case bwd_f32 C2 512x128256", flush=True)
+    x = O.make_c2_input(512, 128256, seed=0)
+    g = np.random.default_rng(1).standard_normal(512).astype(np.float32)
+    xd = torch.from_numpy(x).to(cuda)
+    ext = _ext()
+    lse = ext.onepass_lse_float_robust(xd)
+    gx = ext.onepass_lse_float_backward(torch.from_numpy(g).to(cuda), xd, lse).cpu().numpy()
+    want = O.lse_bwd_fp64(g, x, O.lse_fp64(x))
+    np.testing.assert_allclose(gx, want, rtol=RTOL32, atol=1e-30)
+    np.testing.assert_allclose(gx.astype(np.float64).sum(1), g, rtol=1e-4, atol=1e-6)
+
+
+def test_f32_c2_robust_set_full_size(cuda):
+    """BASELINE C2 robust set at (512, 128256), the shape and kernel the bench
+    times: 1% of rows with 10% -inf entries, an all -inf row, a +inf row, a NaN
+    row, a row with +inf and -inf.  Forward against fp64 and torch with
+    torch.logsumexp's special values; fused backward against g * exp(x - lse)
+    in fp64 and torch autograd (NaN where torch gives NaN)."""
+    print("case fwd+bwd_f32 C2 robust set 512x128256", flush=True)
+    x = O.make_robust_rows(O.make_c2_input(512, 128256, seed=0), seed=1)
+    g = np.random.default_rng(2).standard_normal(512).astype(np.float32)
+    xd = torch.from_numpy(x).to(cuda)
+    ext = _ext()
+    lse = ext.onepass_lse_float_robust(xd)
+    got = lse.cpu().numpy()
+    want = O.lse_fp64(x)
+    assert np.isneginf(got[0]) and np.isposinf(got[1]) and np.isnan(got[2]) and np.isposinf(got[3])
+    _close(got, want, RTOL32)
+    _close(got, torch.logsumexp(xd, dim=-1).cpu().numpy(), RTOL32, atol=2e-6)
+    gx = ext.onepass_lse_float_backward(torch.from_numpy(g).to(cuda), xd, lse).cpu().numpy()
+    np.testing.assert_allclose(gx, O.lse_bwd_fp64(g, x, want), rtol=RTOL32, atol=1e-30, equal_nan=True)
+    xt = xd.clone().requires_grad_(True)
+    torch.logsumexp(xt, -1).backward(torch.from_numpy(g).to(cuda))
+    np.testing.assert_allclose(gx, xt.grad.cpu().numpy(), rtol=RTOL32, atol=1e-30, equal_nan=True)
+
+
 def test_fwd_f32_robust_special_values(cuda):
     print("case fwd_f32 robust specials", flush=True)
     for B, N in [(8, 5), (300, 1000), (64, 128256)]:
@@ -169,6 +209,24 @@ def test_fwd_half_matches_fp64(cuda, dtype, B, N):
     _close(got, want, RTOL16)
     # fp32 accumulation: in fact far inside 1e-3
     _close(got, want, 2e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("B,N,step", [(4096, 32000, 1), (2048, 128256, 7)])
+def test_fwd_half_c3_full_size(cuda, dtype, B, N, step):
+    """BASELINE C3 shapes at full size, x ~ N(0, 2^2) cast from fp32 (the bench's
+    recipe).  The kernel runs over the whole matrix; every step-th row is
+    checked against fp64 of the rounded inputs (all rows at (4096, 32000))."""
+    print(f"case fwd_half C3 {dtype} {B}x{N}", flush=True)
+    x = (np.random.default_rng(B + N).standard_normal((B, N), dtype=np.float32) * np.float32(2.0))
+    xh = torch.from_numpy(x).to(dtype)
+    ext = _ext()
+    fn = ext.batched_logsumexp_fp16 if dtype == torch.float16 else ext.batched_logsumexp_bf16
+    got = fn(xh.to(cuda)).cpu().numpy()
+    rows = np.arange(0, B, step)
+    want = O.lse_fp64(xh[rows].float().numpy())
+    _close(got[rows], want, RTOL16)
+    _close(got[rows], want, 2e-5, atol=1e-5)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
@@ -374,8 +432,24 @@ def test_fwd_pipelined_batch_boundaries(cuda, dtype, label, B, vecs, step):
     boundary of each geometry, with row lengths that are not a multiple of
     the vector width (so rows of one wave start at different alignments and
     the masked last batch holds 0 .. all of a lane's vectors), on aligned and
-    offset storage; robust and plain against fp64."""
-    ve = 16 // torch.empty((), dtype=dtype).element_size()
+    offset storage; robust and plain against fp64.  The no-workspace C entries
+    run the one-pass geometry the label names for every B (the reference-named
+    functions send some of these row counts to the split-row path); where no
+    split applies, the reference-named function must give the same bits."""
+    from fuselse_amd import _lib
+
+    lib = _lib.load()
+    esize = torch.empty((), dtype=dtype).element_size()
+    entry = {torch.float32: "fl_lse_fwd_f32", torch.float16: "fl_lse_fwd_f16",
+             torch.bfloat16: "fl_lse_fwd_bf16"}[dtype]
+
+    def one_pass(xd, robust):
+        out = torch.empty(xd.shape[0], device=xd.device)
+        _lib.call(entry, xd.data_ptr(), out.data_ptr(), xd.shape[0], xd.shape[1], int(robust),
+                  torch.cuda.current_stream().cuda_stream)
+        return out
+
+    ve = 16 // esize
     if step is None:
         ns = [vecs * ve, vecs * ve - 1]
     else:
@@ -391,11 +465,12 @@ def test_fwd_pipelined_batch_boundaries(cuda, dtype, label, B, vecs, step):
             xd = _offset_view(xt, cuda, off)
             want = O.lse_fp64(xt.double().numpy())
             for robust in (False, True):
-                if dtype == torch.float32:
-                    got = (ext.onepass_lse_float_robust if robust else ext.onepass_lse_float)(xd)
-                    tol = RTOL32
-                else:
-                    fn = ext.batched_logsumexp_fp16 if dtype == torch.float16 else ext.batched_logsumexp_bf16
-                    got = fn(xd, robust=robust)
-                    tol = RTOL16
-                _close(got.cpu().numpy(), want, tol, atol=1e-6)
+                got = one_pass(xd, robust)
+                _close(got.cpu().numpy(), want, RTOL32 if dtype == torch.float32 else RTOL16, atol=1e-6)
+                if lib.fl_lse_fwd_workspace_bytes(B, N, esize) == 0:
+                    if dtype == torch.float32:
+                        named = (ext.onepass_lse_float_robust if robust else ext.onepass_lse_float)(xd)
+                    else:
+                        fn = ext.batched_logsumexp_fp16 if dtype == torch.float16 else ext.batched_logsumexp_bf16
+                        named = fn(xd, robust=robust)
+                    assert torch.equal(named, got)

@@ -150,3 +150,16 @@ def test_intlse_messages_and_empty(cuda):
     with pytest.raises(RuntimeError, match="Expected 2-D tensor"):
         ext.batched_logsumexp(torch.zeros(3, device=cuda))
     assert ext.batched_logsumexp(torch.zeros(0, 5, device=cuda)).shape == (0,)
+
+
+def test_acc_out_rejected_when_short(cuda):
+    """The kernels write acc_out[r] for every row, so a buffer shorter than B
+    (or of the wrong type) is rejected before any launch."""
+    xd = torch.zeros((8, 64), dtype=torch.float32, device=cuda)
+    for bad in (torch.empty(7, dtype=torch.int32, device=cuda), torch.empty(8, dtype=torch.int64, device=cuda),
+                torch.empty(8, dtype=torch.int32)):
+        with pytest.raises(RuntimeError, match="acc_out"):
+            _ext().batched_logsumexp(xd, acc_out=bad)
+    q = torch.zeros((8, 64), dtype=torch.int16, device=cuda)
+    with pytest.raises(RuntimeError, match="acc_out must hold one int32 per row"):
+        _ext().batched_logsumexp_q10_6(q, acc_out=torch.empty(3, dtype=torch.int32, device=cuda))

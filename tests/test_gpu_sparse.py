@@ -568,10 +568,11 @@ def test_blocked_backward_product_form_unaligned(cuda, offset):
     _check_blocked_bwd(cuda, nids, cids, pids, params, em, bs, batch, False)
 
 
-@pytest.mark.parametrize("bs", [32, 12])
+@pytest.mark.parametrize("bs", [48, 12])
 def test_blocked_backward_product_form_deterministic(cuda, bs):
     """Element and parameter flows are the same bits on every call (block
-    size 32: the two product kernels; 12: the single-pass kernel)."""
+    size 48: the two product kernels, which take blocks of more than 32
+    parents; 12: the single-pass kernel)."""
     print(f"case blocked bwd product determinism bs={bs}", flush=True)
     rng = np.random.default_rng(8)
     nb, ne, batch, nelem = 40, 33, 300, 20        # few elements: many block edges per element
