@@ -36,6 +36,7 @@ SIGNATURES = {
     "fl_lse_fwd_f32_ws": (_int, [_vp, _vp, _i64, _i64, _int, _vp, ctypes.c_size_t, _vp]),
     "fl_lse_fwd_f16_ws": (_int, [_vp, _vp, _i64, _i64, _int, _vp, ctypes.c_size_t, _vp]),
     "fl_lse_fwd_bf16_ws": (_int, [_vp, _vp, _i64, _i64, _int, _vp, ctypes.c_size_t, _vp]),
+    "fl_lse_fwd_f32_noalloc": (_int, [_vp, _vp, _i64, _i64, _int, _vp]),
     "fl_intlse_q16_f32": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _vp]),
     "fl_intlse_q16_i32": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _vp]),
     "fl_intlse_q10_6": (_int, [_vp, _vp, _vp, _i64, _i64, _vp]),

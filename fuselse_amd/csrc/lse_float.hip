@@ -19,6 +19,8 @@
 // wave-uniform.
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/fuselse_amd.h"
 #include "fl_status.hpp"
 #include "lse_common.hpp"
@@ -819,6 +821,64 @@ extern "C" int fl_lse_fwd_bf16_ws(const void* x, float* out, int64_t B, int64_t 
                                   size_t workspace_bytes, void* stream) {
     return fwd_entry<bf16_t>("fl_lse_fwd_bf16_ws", static_cast<const bf16_t*>(x), out, B, N, robust, workspace,
                              workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free split forward.  The split plan needs B * S partial pairs with
+// B < kSplitMaxRows and S <= 64, at most 319 * 64 * 8 = 163,328 bytes, so one
+// static 160 KiB array per GPU holds every plan's partials.  Host code never
+// uses the array's name as an address (on the host it is only a stand-in for
+// the symbol): each device's address comes from hipGetSymbolAddress, taken
+// once per device on the first call made with that device current.  Every
+// partial is written by the partials kernel before the merge kernel reads it,
+// so the array needs no clearing between calls.  Calls on one GPU share the
+// array: calls whose work can overlap (different streams of one device) race.
+// ---------------------------------------------------------------------------
+namespace fl {
+constexpr int64_t kNoAllocPairs = 20480;  // 160 KiB of float2
+static_assert((kSplitMaxRows - 1) * 64 <= kNoAllocPairs, "static scratch smaller than the largest split plan");
+static __device__ __align__(256) float2 scratch[kNoAllocPairs];
+
+constexpr int kMaxDevices = 64;
+struct ScratchSlot {
+    std::once_flag once;
+    void* ptr = nullptr;
+    hipError_t err = hipSuccess;
+};
+static ScratchSlot g_scratch[kMaxDevices];
+
+// Device address of `scratch` on the current device.
+static int scratch_address(const char* name, void** ptr) {
+    int dev = -1;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return set_error(FL_ELAUNCH, "%s: hipGetDevice failed: %s", name, hipGetErrorString(e));
+    FL_CHECK(dev >= 0 && dev < kMaxDevices, "%s: device %d beyond the %d the library tracks", name, dev, kMaxDevices);
+    ScratchSlot& slot = g_scratch[dev];
+    std::call_once(slot.once, [&slot] { slot.err = hipGetSymbolAddress(&slot.ptr, HIP_SYMBOL(scratch)); });
+    if (slot.err != hipSuccess || slot.ptr == nullptr)
+        return set_error(FL_ELAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", name, dev,
+                         hipGetErrorString(slot.err));
+    *ptr = slot.ptr;
+    return FL_OK;
+}
+}  // namespace fl
+
+extern "C" int fl_lse_fwd_f32_noalloc(const float* x, float* out, int64_t B, int64_t N, int robust, void* stream) {
+    const char* name = "fl_lse_fwd_f32_noalloc";
+    FL_CHECK(B >= 0 && N >= 0, "%s: negative shape (B=%lld, N=%lld)", name, (long long)B, (long long)N);
+    if (B == 0) return ok();
+    FL_CHECK(out != nullptr, "%s: out is NULL", name);
+    const int64_t need = split_ws_bytes(B, default_split_plan(B, N, (int64_t)sizeof(float)));
+    if (need > (int64_t)sizeof(scratch))
+        return set_error(FL_ERANGE, "%s: %lld bytes of partials needed, the static scratch holds %lld", name,
+                         (long long)need, (long long)sizeof(scratch));
+    void* ws = nullptr;
+    if (need > 0) {
+        const int rc = scratch_address(name, &ws);
+        if (rc != FL_OK) return rc;
+    }
+    return fwd_launch<float>(name, x, LseOut{out}, B, N, robust, ws, sizeof(scratch),
+                             reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int fl_lse_bwd_f32(const float* grad, const float* x, const float* lse, float* grad_x, int64_t B,

@@ -118,6 +118,23 @@ int fl_lse_fwd_bf16_ws(const void* x, float* out, int64_t B, int64_t N, int robu
                        size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * fl_lse_fwd_f32_noalloc: fl_lse_fwd_f32_ws with the split partials in a
+ * static device array instead of a caller workspace, so the call allocates
+ * nothing (no hipMalloc, no workspace argument).  No counterpart in the
+ * reference: it is for callers that cannot allocate, such as code under HIP
+ * graph capture or a serving loop that forbids allocation.  Same kernels,
+ * plan and results as fl_lse_fwd_f32_ws (bit-identical).
+ * Limit: the array holds 160 KiB per GPU (held until the process ends); every
+ * split plan fits (B < 320 rows, at most 64 segments), and a shape needing
+ * more is rejected with FL_ERANGE.  The first call on a device takes the
+ * array's address on that device (hipGetSymbolAddress), so make it once
+ * outside graph capture.  All calls on one GPU share the array: calls that
+ * can run concurrently on one GPU (different streams) race and must not
+ * overlap.
+ * ------------------------------------------------------------------------- */
+int fl_lse_fwd_f32_noalloc(const float* x, float* out, int64_t B, int64_t N, int robust, void* stream);
+
+/* ---------------------------------------------------------------------------
  * IntLSE fixed-point row LSE, bit-exact to the reference's GPU reduction tree
  * (256 virtual threads, warp-32 butterflies).  out is fp32 base-e [B];
  * acc_out (may be NULL) receives the final base-2 fixed-point accumulators.

@@ -34,7 +34,12 @@ def test_invalid_arguments_rejected_without_launch():
     assert b"out is NULL" in lib.fl_last_error()
     assert lib.fl_lse_bwd_f32(None, None, None, None, 2, 3, None) == 1
     assert b"NULL" in lib.fl_last_error()
+    assert lib.fl_lse_fwd_f32_noalloc(None, None, -1, 4, 1, None) == 1
+    assert b"negative shape" in lib.fl_last_error()
+    assert lib.fl_lse_fwd_f32_noalloc(None, None, 3, 4, 1, None) == 1
+    assert b"out is NULL" in lib.fl_last_error()
     # B == 0 is a no-op success
+    assert lib.fl_lse_fwd_f32_noalloc(None, None, 0, 4, 1, None) == 0
     assert lib.fl_lse_fwd_f32(None, None, 0, 4, 1, None) == 0
     assert lib.fl_last_error() == b""
 
