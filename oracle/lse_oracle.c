@@ -21,8 +21,10 @@
  *   or_sparse_q16_*                : closed forms (one edge, equal edges), a
  *                                    hand-computed row fixing the e mod ET edge
  *                                    striding, and the float oracle envelope.
- *   or_fuselse_cpu_rows            : glibc expf/log1pf sequential chain; pinned by
- *                                    fp64 envelope and N=2 textbook identity.
+ *   or_fuselse_cpu_rows            : compiled reference fuselse/cpu/fused_fp32_cpu.cpp
+ *                                    (oracle/_ref, bit-exact, and the fixture
+ *                                    tests/golden/fuselse_cpu_ref.npz written from it),
+ *                                    fp64 envelope, N=2 textbook identity.
  */
 #include <math.h>
 #include <stdint.h>

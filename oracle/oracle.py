@@ -16,7 +16,8 @@ Two kinds of oracle live here:
   Q16 ET tree) and the FuseLSE-CPU chain used as the CPU baseline.
 
 ``ref_intlse_cpu_rows`` calls the reference's own ``intlse/cpu/lse_kernel_simd.c``
-compiled into ``oracle/_ref`` (when it was built), which pins the restatement.
+compiled into ``oracle/_ref`` (when it was built), and ``ref_fuselse_cpu`` its
+``fuselse/cpu/fused_fp32_cpu.cpp``; both pin the restatements.
 """
 
 from __future__ import annotations
@@ -103,6 +104,38 @@ def ref():
             fn.argtypes = [_f32p, ctypes.c_int, ctypes.c_int, _f32p]
         _ref = R
     return _ref
+
+
+_REF_FUSE_PATH = os.path.join(HERE, "_ref", "fused_fp32_cpu.so")
+_ref_fuse = None
+
+
+def ref_fuselse_available() -> bool:
+    return os.path.exists(_REF_FUSE_PATH)
+
+
+def ref_fuselse_cpu(x) -> np.ndarray:
+    """The reference's FuseLSE-CPU (fuselse/cpu/fused_fp32_cpu.cpp:28-46)
+    compiled from its own source into oracle/_ref by oracle/Makefile: its
+    cpu_lse_float over rows of a 2-D fp32 array.  Present only where the
+    reference tree is mounted; used to write tests/golden fixtures and to
+    check the C port."""
+    global _ref_fuse
+    if _ref_fuse is None:
+        import importlib.util
+
+        import torch  # noqa: F401  (the module links libtorch)
+
+        if not ref_fuselse_available():
+            raise RuntimeError(f"reference build missing: {_REF_FUSE_PATH}")
+        spec = importlib.util.spec_from_file_location("fused_fp32_cpu", _REF_FUSE_PATH)
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        _ref_fuse = mod
+    import torch
+
+    x = np.ascontiguousarray(x, np.float32)
+    return _ref_fuse.cpu_lse_float(torch.from_numpy(x)).numpy()
 
 
 def _p(a, t):

@@ -499,6 +499,37 @@ def test_fuselse_cpu_port_envelope_and_pair():
     assert abs(e / 1.06e-4 - 1) < 0.25, e
 
 
+def _same_bits(got, want):
+    got = np.asarray(got, np.float32)
+    want = np.asarray(want, np.float32)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(want)
+    np.testing.assert_array_equal(got[ok].view(np.int32), want[ok].view(np.int32))
+
+
+def test_fuselse_cpu_port_matches_reference_fixture():
+    """The C port equals the reference's own cpu_lse_float bit for bit on the
+    fixture tests/golden/make_golden.py wrote from the compiled reference
+    (fuselse/cpu/fused_fp32_cpu.cpp built by oracle/Makefile): the C1 shapes,
+    a C2-style sample, N = 1..3 and special-value rows."""
+    d = np.load(os.path.join(GOLD, "fuselse_cpu_ref.npz"))
+    xo = oo = 0
+    for B, N in d["shapes"]:
+        x = d["x"][xo:xo + int(B * N)].reshape(int(B), int(N))
+        want = d["out"][oo:oo + int(B)]
+        xo += int(B * N)
+        oo += int(B)
+        _same_bits(O.fuselse_cpu_rows(x), want)
+    assert xo == d["x"].size and oo == d["out"].size
+
+
+@pytest.mark.skipif(not O.ref_fuselse_available(), reason="reference FuseLSE-CPU build (oracle/_ref) absent")
+@pytest.mark.parametrize("B,N,scale", [(3, 2, 1.0), (16, 4097, 3.0), (8, 128256, 3.0), (5, 1000, 80.0)])
+def test_fuselse_cpu_port_matches_compiled_reference(B, N, scale):
+    x = (np.random.default_rng(B * N).standard_normal((B, N), dtype=np.float32) * np.float32(scale))
+    _same_bits(O.fuselse_cpu_rows(x), O.ref_fuselse_cpu(x))
+
+
 # ---------------------------------------------------------------------------
 # selective log-softmax (trl.trainer.utils.selective_log_softmax, fp32 branch)
 # ---------------------------------------------------------------------------
