@@ -345,6 +345,30 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
             rec(f"published_{tag}_fwd_512x128256", ms, nbytes, resident_us=round(ms_res * 1e3, 2),
                 v100_ms=ref_ms, v100_pct_peak=round(100 * nbytes / (ref_ms * 1e-3) / 900e9, 1))
             del bufs
+    if want("latency"):
+        # Dependent-chain latencies of the IntLSE pair steps on one CU
+        # (fl_diag_chain_latency): shader-clock cycles per step of one wave
+        # alone on its SIMD, of four waves (one per SIMD) and of sixteen (four
+        # per SIMD, the occupancy of the C4 Q10.6 kernel), median over waves.
+        from fuselse_amd import _lib
+
+        steps = 4096
+        kinds = {0: "v_add_u32", 1: "ds_read_u8", 2: "q10_6_pair_step", 3: "q16_pair_step"}
+        lat = {}
+        for kind, kname in kinds.items():
+            for waves in (1, 4, 16):
+                tbuf = torch.zeros(3 * waves, dtype=torch.int64, device=dev)
+                per = []
+                for _ in range(3):
+                    _lib.call("fl_diag_chain_latency", kind, steps, waves, tbuf.data_ptr(), stream.cuda_stream)
+                    torch.cuda.synchronize()
+                    r = tbuf.view(waves, 3).cpu()
+                    per.append(float(r[:, 0].double().median()) / steps)
+                    mhz = float(r[:, 0].double().sum() / (r[:, 1].double().sum() * 10e-3))  # cycles per us
+                lat[f"{kname}_{waves}_waves"] = {
+                    "cycles_per_step": round(sorted(per)[1], 2), "shader_clock_mhz": round(mhz, 0)}
+                log(f"latency {kname} {waves} waves: {sorted(per)[1]:.2f} cycles per step at {mhz:.0f} MHz")
+        res["chain_latency"] = lat
     if want("C4"):
         # C4: IntLSE fixed point
         b, n = 512, 128256
@@ -469,7 +493,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-configs", action="store_true", help="skip the other BASELINE configs")
     ap.add_argument("--only", default=None,
-                    help="comma-separated config groups (C3, split, sls, published, C4, C5) to run alone, without the C2 "
+                    help="comma-separated config groups (C3, split, sls, published, latency, C4, C5) to run alone, "
+                         "without the C2 "
                          "step; for profiling passes over one group")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also launch one plain 1 GiB device copy (counter calibration runs)")
@@ -487,7 +512,7 @@ def main():
         import fuselse_amd
 
         groups = set(args.only.split(","))
-        unknown = groups - {"C3", "split", "sls", "published", "C4", "C5"}
+        unknown = groups - {"C3", "split", "sls", "published", "latency", "C4", "C5"}
         if unknown:
             log(f"bench.py: unknown config groups {sorted(unknown)}")
             sys.exit(2)

@@ -9,6 +9,7 @@
 #include "../../include/fuselse_amd.h"
 #include "fl_status.hpp"
 #include "lse_common.hpp"
+#include "lse_pair.hpp"
 
 namespace fl {
 
@@ -37,9 +38,76 @@ __global__ __launch_bounds__(256) void read_stream_kernel(const char* __restrict
     if (acc == 0x9E3779B9u) sink[0] = acc;
 }
 
+// Dependent-chain latencies of the IntLSE pair steps (no counterpart in the
+// reference).  Each wave of one block (one CU) runs `steps` (a multiple of
+// 16) dependent steps
+// of one kind and records the shader-clock cycles (s_memtime) and the 100 MHz
+// real-time ticks (s_memrealtime) the chain took:
+//   KIND 0: v_add_u32 of the previous value;
+//   KIND 1: ds_read_u8 addressed by the previous value (a table of bytes);
+//   KIND 2: the Q10.6 pair step of the row kernels (max, two subtracts, med3,
+//           ds_read_u8 of the gap table, add), q10_pair;
+//   KIND 3: the Q16.16 pair step with its LDS correction table, q16_pair.
+// The operand each step pairs with comes from the step index (a scalar
+// value), so the only dependence is through the chain.  With 64 * w threads
+// the block puts w / 4 waves on each of the CU's four SIMDs.
+template <int KIND>
+__global__ __launch_bounds__(1024) void chain_latency_kernel(int steps, uint64_t* __restrict__ rec) {
+    __shared__ uint8_t tab8[512];  // first: its LDS address is the byte index
+    __shared__ int lut[64];
+    for (int i = threadIdx.x; i < 512; i += blockDim.x) tab8[i] = (uint8_t)((i * 7) % 70);
+    for (int i = threadIdx.x; i < 64; i += blockDim.x) lut[i] = (i * 613) & 0x1FFF;
+    __syncthreads();
+    int a = (int)(threadIdx.x & 7);
+    const uint64_t t0 = __builtin_amdgcn_s_memtime();
+    const uint64_t r0 = __builtin_amdgcn_s_memrealtime();
+    // 16 steps per loop trip, fully unrolled, so the loop's own scalar
+    // instructions and branch fall on one step in 16
+    for (int k0 = 0; k0 < steps; k0 += 16) {
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int k = k0 + u;
+            if constexpr (KIND == 0) {
+                asm volatile("v_add_u32 %0, %0, %1" : "+v"(a) : "s"(k));
+            } else if constexpr (KIND == 1) {
+                a = tab8[a];  // table bytes are below 70, so the chain stays in the table
+            } else if constexpr (KIND == 2) {
+                a = q10_pair(a, (int)(((uint32_t)k * 2654435761u) >> 22) - 512, tab8);
+            } else {
+                a = q16_pair<true>(a, (int)((uint32_t)k * 2654435761u) >> 6, lut);
+            }
+        }
+    }
+    const uint64_t t1 = __builtin_amdgcn_s_memtime();
+    const uint64_t r1 = __builtin_amdgcn_s_memrealtime();
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        rec[3 * w + 0] = t1 - t0;
+        rec[3 * w + 1] = r1 - r0;
+        rec[3 * w + 2] = (uint64_t)(uint32_t)a;  // keeps the chain live
+    }
+}
+
 }  // namespace fl
 
 using namespace fl;
+
+extern "C" int fl_diag_chain_latency(int kind, int steps, int waves, uint64_t* rec, void* stream) {
+    const char* name = "fl_diag_chain_latency";
+    FL_CHECK(kind >= 0 && kind <= 3, "%s: kind must be 0..3", name);
+    FL_CHECK(steps > 0 && steps % 16 == 0, "%s: steps must be a positive multiple of 16", name);
+    FL_CHECK(waves >= 1 && waves <= 16, "%s: waves must be 1..16", name);
+    FL_CHECK(rec != nullptr, "%s: rec is NULL", name);
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const dim3 blk(64 * waves);
+    switch (kind) {
+    case 0: chain_latency_kernel<0><<<1, blk, 0, st>>>(steps, rec); break;
+    case 1: chain_latency_kernel<1><<<1, blk, 0, st>>>(steps, rec); break;
+    case 2: chain_latency_kernel<2><<<1, blk, 0, st>>>(steps, rec); break;
+    default: chain_latency_kernel<3><<<1, blk, 0, st>>>(steps, rec); break;
+    }
+    return launch_status(name);
+}
 
 extern "C" int fl_diag_read_stream(const void* x, int64_t nbytes, int blocks, int unroll, uint32_t* sink,
                                    void* stream) {

@@ -26,22 +26,23 @@
 // The 64-entry correction tables live in LDS; the Q10.6 pair op, which depends
 // only on the operand gap d and is the identity for d > 384, is read from a
 // 386-entry LDS table of (M + LUT) built per block from the same formula.
+// Both are built from immediates, without memory loads.
 #include <stdint.h>
+
+#include <type_traits>
 
 #include "../../include/fuselse_amd.h"
 #include "fl_status.hpp"
 #include "lse_common.hpp"
+#include "lse_pair.hpp"
 
 namespace fl {
 
-constexpr int kQNegInf = -0x3fffffff;
-// chunks per lane kept in flight ahead of the pair chain
-constexpr int kPrefetch = 8;
 // cache-policy bits of the raw buffer loads: nontemporal (streamed once)
 constexpr int kBufNT = 2;
 
 // lse_kernel.cu:35-44 (Mitchell-error correction per 1/64 bin, Q16.16)
-__constant__ int kLutQ16[64] = {
+constexpr int kLutQ16[64] = {
        0,  571,  907, 1282, 1634, 1745, 2054, 2592,
     2900, 2859, 2895, 3015, 3222, 3522, 3922, 4426,
     4617, 4441, 4294, 4178, 4093, 4039, 4018, 4030,
@@ -53,7 +54,7 @@ __constant__ int kLutQ16[64] = {
 };
 
 // lse_kernel_q10_6.cu:27-32 (the same table at 6 fractional bits)
-__constant__ int kLutQ10[64] = {
+constexpr int kLutQ10[64] = {
     0, 1, 1, 1, 2, 2, 2, 3, 3, 3, 3, 3, 3, 3, 4, 4,
     5, 4, 4, 4, 4, 4, 4, 4, 4, 4, 4, 4, 5, 5, 5, 5,
     5, 5, 5, 4, 4, 4, 3, 3, 3, 3, 2, 2, 2, 2, 2, 1,
@@ -65,43 +66,6 @@ __constant__ int kLutQ10[64] = {
 constexpr float kQ16Conv = 1.44269504089f * 65536.0f;
 constexpr float kQ16Out = 0.69314718056f / 65536.0f;
 constexpr float kQ10Out = 0.69314718056f / 64.0f;
-
-// Q16.16 pair: max + M + LUT[(M >> 10) & 63], M = (2^16 + (sub & 0xFFFF)) >> -(sub >> 16).
-template <bool USE_LUT>
-__device__ __forceinline__ int q16_pair(int a, int b, const int* __restrict__ lut) {
-    const int hi = a > b ? a : b;
-    const int lo = a > b ? b : a;
-    const int sub = (int)((uint32_t)lo - (uint32_t)hi);
-    const uint32_t sh = (uint32_t)(-(sub >> 16));
-    const uint32_t shc = sh < 31u ? sh : 31u;
-    const uint32_t fr = 0x10000u | ((uint32_t)sub & 0xFFFFu);
-    const int m = (int)(fr >> shc);
-    const uint32_t r = (uint32_t)hi + (uint32_t)m;
-    if constexpr (USE_LUT) {
-        // LUT index (m >> 10) & 63 as a byte offset, (m >> 8) & 0xFC, taken as
-        // ((fr >> 8) >> shc) & 0xFC so it does not wait for m.
-        const uint32_t off = ((fr >> 8) >> shc) & 0xFCu;
-        return (int)(r + (uint32_t)*reinterpret_cast<const int*>(reinterpret_cast<const char*>(lut) + off));
-    } else {
-        return (int)r;
-    }
-}
-
-// Q10.6 pair through the gap table: max(a, b) + g[min(|a - b|, 385)],
-// g[385] = 0.  Every table entry is at most 69, so the table is bytes and the
-// clamped gap is the LDS address itself; the clamp is one v_med3_i32 of
-// (a - b, b - a, 385), the median being min(|a - b|, 385).  The differences
-// cannot overflow: inputs are int16, an accumulator exceeds the largest input
-// by at most 64 * log2(N), and the identity -0x3fffffff stays below 2^30 in
-// magnitude after any number of pair steps.  Measured 18% shorter per pair
-// step than max/min, subtract, clamp and a word address.
-__device__ __forceinline__ int q10_pair(int a, int b, const uint8_t* __restrict__ g) {
-    const int hi = a > b ? a : b;
-    const int u = a - b, nu = b - a;
-    int d;
-    asm("v_med3_i32 %0, %1, %2, %3" : "=v"(d) : "v"(u), "v"(nu), "s"(385));
-    return hi + (int)g[d];
-}
 
 // __float2int_rn semantics: round half to even, saturate, NaN -> 0
 // (v_rndne_f32, then v_cvt_i32_f32, which clamps and maps NaN to 0).
@@ -163,11 +127,11 @@ struct SrcI16 {
 // The reference tree over one row per block (grid-stride over rows).
 // ALIGN is the vector alignment the reference uses for the chunks (16 bytes
 // for 4-byte elements, 8 for int16); PAIR folds two accumulators.
-// SETUP builds the kernel's LDS table on a block's first row in two steps:
-// issue() reads the table's source before any row load, finish() stores it
-// and syncs once the row's first loads are in flight.  The vector-memory
-// counter retires in order, so a table read issued after the row loads would
-// make its wait cover all of them.
+// SETUP builds the kernel's LDS table once the row's first loads are in
+// flight (finish(), which ends with the block barrier); issue() runs before
+// any row load and is free for setup work that must precede them.  The
+// tables' source is held in registers as immediates, so building them waits
+// for no memory access.
 template <typename SRC, int ALIGN, int D, typename TAB, typename PAIR, typename SETUP>
 __device__ __forceinline__ int tree_row(const typename SRC::T* row, int64_t n, const TAB* __restrict__ tab, PAIR pair,
                                         int* __restrict__ sh_warp, SETUP& setup) {
@@ -289,6 +253,19 @@ __device__ __forceinline__ int tree_row(const typename SRC::T* row, int64_t n, c
     return v;
 }
 
+// A 64-entry table held across a wave's lanes: lane i gets tab[i], written
+// lane by lane as immediates (v_writelane), with no memory access.  The
+// tables' source used to be loaded from memory at the start of each block;
+// those loads queued behind the whole CU's row loads (in flight at once at
+// the kernel's start), so the table, and with it each block's first pair
+// step, waited 2.5 us (median) to 8 us (99th percentile) at (1024, 32000).
+__device__ __forceinline__ int lanes_table(const int (&tab)[64]) {
+    int v = 0;
+#pragma unroll
+    for (int i = 0; i < 64; ++i) asm("v_writelane_b32 %0, %1, %2" : "+v"(v) : "s"(tab[i]), "i"(i));
+    return v;
+}
+
 // One row per block: with no loop over rows, no load issued for a later
 // round (the prefetch runs past the end of a row's chunks) can be in flight
 // when the next row would reuse its registers, so nothing waits for it.
@@ -296,21 +273,17 @@ template <bool USE_LUT>
 struct Q16Setup {
     int* lut;
     int v;
-    __device__ __forceinline__ void issue() {
-        if constexpr (USE_LUT) {
-            if (threadIdx.x < 64) v = kLutQ16[threadIdx.x];
-        }
-    }
+    __device__ __forceinline__ void issue() {}
     __device__ __forceinline__ void finish() {
         if constexpr (USE_LUT) {
             __builtin_amdgcn_sched_barrier(0);
-            if (threadIdx.x < 64) lut[threadIdx.x] = v;
+            if (threadIdx.x < 64) lut[threadIdx.x] = lanes_table(kLutQ16);
             __syncthreads();
         }
     }
 };
 
-template <typename SRC, bool USE_LUT, int D = kPrefetch>
+template <typename SRC, bool USE_LUT, int D>
 __global__ __launch_bounds__(256) void intlse_q16_rows(const typename SRC::T* __restrict__ x, float* __restrict__ out,
                                                        int32_t* __restrict__ acc_out, int64_t N) {
     __shared__ int lut[64];
@@ -326,7 +299,8 @@ __global__ __launch_bounds__(256) void intlse_q16_rows(const typename SRC::T* __
 }
 
 // gap[d] = M + LUT[M & 63], M = (64 + ((-d) & 63)) >> ceil(d / 64), for
-// d <= 384; gap[385] = 0.  Thread t builds entries t and t + 256.
+// d <= 384; gap[385] = 0.  Thread t builds entries t and t + 256, reading
+// LUT[M & 63] from a lane-held copy of the table with a lane shuffle.
 struct Q10Setup {
     uint8_t* gap;
     int l0, l1;
@@ -335,16 +309,14 @@ struct Q10Setup {
         const uint32_t sh = (uint32_t)(-(sub >> 6));
         return (int)((64u | ((uint32_t)sub & 63u)) >> (sh < 31u ? sh : 31u));
     }
-    __device__ __forceinline__ void issue() {
-        const int d0 = threadIdx.x, d1 = threadIdx.x + 256;
-        l0 = kLutQ10[m_of(d0) & 63];
-        l1 = d1 <= 384 ? kLutQ10[m_of(d1) & 63] : 0;
-    }
+    __device__ __forceinline__ void issue() {}
     __device__ __forceinline__ void finish() {
-        // keep the table stores (which wait for their reads) after the row's
-        // first loads are issued
+        // keep the table work after the row's first loads are issued
         __builtin_amdgcn_sched_barrier(0);
+        const int lutv = lanes_table(kLutQ10);
         const int d0 = threadIdx.x, d1 = threadIdx.x + 256;
+        l0 = __shfl(lutv, m_of(d0) & 63, 64);
+        l1 = __shfl(lutv, m_of(d1 <= 384 ? d1 : 384) & 63, 64);
         gap[d0] = (uint8_t)(m_of(d0) + l0);
         if (d1 <= 384)
             gap[d1] = (uint8_t)(m_of(d1) + l1);
@@ -354,7 +326,7 @@ struct Q10Setup {
     }
 };
 
-template <int D = kPrefetch>
+template <int D>
 __global__ __launch_bounds__(256) void intlse_q10_6_rows(const int16_t* __restrict__ x, float* __restrict__ out,
                                                          int32_t* __restrict__ acc_out, int64_t N) {
     __shared__ __align__(16) uint8_t gap[388];
@@ -376,6 +348,30 @@ static void for_row_chunks(const T* x, float* out, int32_t* acc, int64_t B, int6
     for (int64_t r0 = 0; r0 < B; r0 += kMaxGrid) {
         const int64_t rows = B - r0 < kMaxGrid ? B - r0 : kMaxGrid;
         launch(dim3((unsigned)rows), x + r0 * N, out + r0, acc ? acc + r0 : nullptr);
+    }
+}
+
+// Chunks per lane kept in flight ahead of the pair chain.  Every block starts
+// its row at once and issues its first chunks together; a wave whose loads
+// cannot issue yet (its CU's queue is full) also cannot start its chain, so
+// a deep prefetch delays the first pair steps while a shallow one starves
+// long rows.  Same-process sweeps of 1..8 chunks over 256..8192 rows of both
+// formats put the best at about 20 KB in flight per CU: 1024 x 32000 Q10.6
+// 15.9 -> 12.8 us and 512 x 128256 Q16.16 45.4 -> 41.3 us against 8 chunks.
+static int prefetch_chunks(int64_t rows, int64_t chunk_bytes) {
+    const int64_t blocks_per_cu = (rows + 255) / 256 < 8 ? (rows + 255) / 256 : 8;
+    const double t = 20480.0 / (double)(4 * blocks_per_cu * 64 * chunk_bytes);
+    return t <= 2.5 ? 2 : t < 3.5 ? 3 : t < 5.0 ? 4 : 6;
+}
+
+// Launches KERNEL<D> with the prefetch depth for this shape.
+template <typename LAUNCH>
+static void with_prefetch(int64_t rows, int64_t chunk_bytes, LAUNCH launch) {
+    switch (prefetch_chunks(rows, chunk_bytes)) {
+    case 2: launch(std::integral_constant<int, 2>{}); break;
+    case 3: launch(std::integral_constant<int, 3>{}); break;
+    case 4: launch(std::integral_constant<int, 4>{}); break;
+    default: launch(std::integral_constant<int, 6>{}); break;
     }
 }
 
@@ -402,10 +398,12 @@ extern "C" int fl_intlse_q16_f32(const float* x, float* out, int32_t* acc_out, i
     if (B == 0) return ok();
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     for_row_chunks(x, out, acc_out, B, N, [&](dim3 g, const float* xc, float* oc, int32_t* ac) {
-        if (use_lut)
-            intlse_q16_rows<SrcF32, true><<<g, dim3(256), 0, st>>>(xc, oc, ac, N);
-        else
-            intlse_q16_rows<SrcF32, false><<<g, dim3(256), 0, st>>>(xc, oc, ac, N);
+        with_prefetch(g.x, 16, [&](auto d) {
+            if (use_lut)
+                intlse_q16_rows<SrcF32, true, d.value><<<g, dim3(256), 0, st>>>(xc, oc, ac, N);
+            else
+                intlse_q16_rows<SrcF32, false, d.value><<<g, dim3(256), 0, st>>>(xc, oc, ac, N);
+        });
     });
     return launch_status(name);
 }
@@ -417,10 +415,12 @@ extern "C" int fl_intlse_q16_i32(const int32_t* q, float* out, int32_t* acc_out,
     if (B == 0) return ok();
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     for_row_chunks(q, out, acc_out, B, N, [&](dim3 g, const int32_t* qc, float* oc, int32_t* ac) {
-        if (use_lut)
-            intlse_q16_rows<SrcI32, true><<<g, dim3(256), 0, st>>>(qc, oc, ac, N);
-        else
-            intlse_q16_rows<SrcI32, false><<<g, dim3(256), 0, st>>>(qc, oc, ac, N);
+        with_prefetch(g.x, 16, [&](auto d) {
+            if (use_lut)
+                intlse_q16_rows<SrcI32, true, d.value><<<g, dim3(256), 0, st>>>(qc, oc, ac, N);
+            else
+                intlse_q16_rows<SrcI32, false, d.value><<<g, dim3(256), 0, st>>>(qc, oc, ac, N);
+        });
     });
     return launch_status(name);
 }
@@ -431,7 +431,7 @@ extern "C" int fl_intlse_q10_6(const int16_t* q, float* out, int32_t* acc_out, i
     if (B == 0) return ok();
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     for_row_chunks(q, out, acc_out, B, N, [&](dim3 g, const int16_t* qc, float* oc, int32_t* ac) {
-        intlse_q10_6_rows<><<<g, dim3(256), 0, st>>>(qc, oc, ac, N);
+        with_prefetch(g.x, 8, [&](auto d) { intlse_q10_6_rows<d.value><<<g, dim3(256), 0, st>>>(qc, oc, ac, N); });
     });
     return launch_status(name);
 }

@@ -240,6 +240,15 @@ int fl_sparse_blocked_bwd(const float* node_flows, const float* node_mars, const
  * ------------------------------------------------------------------------- */
 int fl_diag_read_stream(const void* x, int64_t nbytes, int blocks, int unroll, uint32_t* sink, void* stream);
 
+/* Measurement aid (no counterpart in the reference): one block of 64 * waves
+ * threads (waves 1..16, on one CU) in which every wave runs `steps` (a
+ * positive multiple of 16) dependent steps of one kind: 0 = v_add_u32, 1 = ds_read_u8 addressed by the
+ * previous value, 2 = the Q10.6 pair step of fl_intlse_q10_6, 3 = the Q16.16
+ * pair step with its LDS table.  rec (device, 3 * waves uint64) receives per
+ * wave: shader-clock cycles, 100 MHz real-time ticks, and the chain's final
+ * value. */
+int fl_diag_chain_latency(int kind, int steps, int waves, uint64_t* rec, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -143,6 +143,40 @@ def test_q10_6_prefix_and_extremes(cuda, elem_offset):
     _assert_bits(out, acc, want, want_acc)
 
 
+@pytest.mark.parametrize("B,N", [(1, 8), (3, 1024), (5, 1032), (2, 4104), (511, 2048), (600, 1040), (1030, 3200)])
+@pytest.mark.parametrize("elem_offset", [0, 5, 6, 7])
+def test_q10_6_rows_and_prefixes(cuda, B, N, elem_offset):
+    """Rows of whole 16-byte multiples with prefixes of 0..3 elements (row
+    starts 0, 10, 12 and 14 bytes past a 256-byte boundary), rows with and
+    without extra chunks (n4 % 256) and with no whole 256-chunk round
+    (n4 < 256), saturated entries, against the oracle's tree bit for bit."""
+    print(f"case q10_6 rows B={B} N={N} off={elem_offset}", flush=True)
+    rng = np.random.default_rng(B * 131 + N + elem_offset)
+    x = (rng.standard_normal((B, N), dtype=np.float32) * np.float32(2.0))
+    q = O.to_q10_6(x)
+    q[0, ::5] = 32767
+    if B > 2:
+        q[1, :] = -32768
+        q[2, 1::3] = -32768
+    qd = _offset_view(q, cuda, elem_offset) if elem_offset else torch.from_numpy(q).to(cuda)
+    out, acc = _run(_ext().batched_logsumexp_q10_6, qd)
+    want, want_acc = O.q10_6_rows(q, base_mod=qd.data_ptr() & 7, raw=True)
+    _assert_bits(out, acc, want, want_acc)
+
+
+def test_q10_6_published_shape(cuda):
+    """The reference's published reduced-bit shape (512, 128256) with its
+    U(-100, 0) inputs (reduced_bit/run_bench.py:58-71)."""
+    print("case q10_6 512x128256 U(-100,0)", flush=True)
+    rng = np.random.default_rng(42)
+    x = (rng.random((512, 128256), dtype=np.float32) * np.float32(100.0) - np.float32(100.0))
+    q = O.to_q10_6(x)
+    qd = torch.from_numpy(q).to(cuda)
+    out, acc = _run(_ext().batched_logsumexp_q10_6, qd)
+    want, want_acc = O.q10_6_rows(q, base_mod=qd.data_ptr() & 7, raw=True)
+    _assert_bits(out, acc, want, want_acc)
+
+
 def test_intlse_messages_and_empty(cuda):
     ext = _ext()
     with pytest.raises(RuntimeError, match="Input must be int16"):
