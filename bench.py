@@ -226,6 +226,23 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
                      "bytes": int(nbytes), **extra}
         log(f"{name}: {ms * 1e3:.2f} us, {gbps:.1f} GB/s")
 
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def read_ceiling_us(bufs):
+        """The read ceiling of the same buffers: fl_diag_read_stream (the
+        forward's load form, flat grid-stride order), best of three launch
+        shapes, timed like the kernels."""
+        from fuselse_amd import _lib
+
+        nb = len(bufs)
+        best = None
+        for blocks, unroll in ((1024, 4), (2048, 4), (4096, 2)):
+            ms = _time_calls(torch, stream, lambda i: _lib.call(
+                "fl_diag_read_stream", bufs[i % nb].data_ptr(), bufs[i % nb].numel() * bufs[i % nb].element_size(),
+                blocks, unroll, sink.data_ptr(), stream.cuda_stream), nb, iters)
+            best = ms if best is None or ms < best else best
+        return round(best * 1e3, 2)
+
     def nbuf_for(nbytes):
         return max(2, int(np.ceil(2 * 256e6 / nbytes)) + 1)
 
@@ -242,7 +259,7 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
                 nb = nbuf_for(2 * b * n)
                 bufs = [(torch.randn(b, n, device=dev, generator=gen) * 2).to(dt) for _ in range(nb)]
                 ms = _time_calls(torch, stream, lambda i: fn(bufs[i % nb]), nb, iters)
-                rec(f"C3_{tag}_fwd_{b}x{n}", ms, 2 * b * n + 4 * b)
+                rec(f"C3_{tag}_fwd_{b}x{n}", ms, 2 * b * n + 4 * b, read_ceiling_us=read_ceiling_us(bufs))
                 if n > 256:
                     # the fused half backward (fp32 grad and lse, half x and grad_x)
                     gsv = torch.randn(b, device=dev, generator=gen)
@@ -343,8 +360,38 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
             ms_res = _time_calls(torch, stream, lambda i: fn(bufs[0]), 1, iters)
             ref_ms = v100[tag][0]
             rec(f"published_{tag}_fwd_512x128256", ms, nbytes, resident_us=round(ms_res * 1e3, 2),
+                read_ceiling_us=read_ceiling_us(bufs),
                 v100_ms=ref_ms, v100_pct_peak=round(100 * nbytes / (ref_ms * 1e-3) / 900e9, 1))
             del bufs
+    if want("ramp"):
+        # Fixed cost against streaming rate: the read ceiling kernel and the
+        # fp16 forward over rows of 256 (the C3 small-row geometry) at 8..526 MB,
+        # each over enough disjoint regions of one buffer to exceed twice the
+        # Infinity Cache; a least-squares fit t = a + bytes / bw per kernel.
+        import numpy as np
+
+        sizes = [8 << 20, 16 << 20, 32 << 20, 64 << 20, 128 << 20, 256 << 20, 512 << 20]
+        big = torch.empty(3 * (512 << 20) // 2, dtype=torch.float16, device=dev)
+        big.normal_(0.0, 2.0, generator=gen)
+        pts = {"read": [], "fp16_fwd_rows_of_256": []}
+        for sz in sizes:
+            nreg = max(2, int(np.ceil(2 * 256e6 / sz)) + 1)
+            nreg = min(nreg, (big.numel() * 2) // sz)
+            regs = [big[k * (sz // 2):(k + 1) * (sz // 2)].view(-1, 256) for k in range(nreg)]
+            t_read = read_ceiling_us(regs)
+            ms = _time_calls(torch, stream, lambda i: ext.batched_logsumexp_fp16(regs[i % nreg]), nreg, iters)
+            pts["read"].append((sz, t_read))
+            pts["fp16_fwd_rows_of_256"].append((sz, round(ms * 1e3, 2)))
+            log(f"ramp {sz >> 20} MB: read {t_read:.2f} us, fp16 rows of 256 {ms * 1e3:.2f} us")
+        ramp = {}
+        for name, p in pts.items():
+            xb = np.array([q[0] for q in p], np.float64)
+            yt = np.array([q[1] for q in p], np.float64)
+            slope, icpt = np.polyfit(xb, yt, 1)
+            ramp[name] = {"points_mb_us": [[q[0] >> 20, q[1]] for q in p], "fixed_us": round(icpt, 2),
+                          "streaming_gbps": round(1e-3 / slope, 1)}
+        res["ramp"] = ramp
+        del big
     if want("latency"):
         # Dependent-chain latencies of the IntLSE pair steps on one CU
         # (fl_diag_chain_latency): shader-clock cycles per step of one wave
@@ -375,7 +422,7 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
         nb = 3
         xs = [torch.randn(b, n, device=dev, generator=gen) * 2 for _ in range(nb)]
         ms = _time_calls(torch, stream, lambda i: ext.batched_logsumexp(xs[i % nb]), nb, iters)
-        rec("C4_q16_f32in_512x128256", ms, 4 * b * n + 4 * b)
+        rec("C4_q16_f32in_512x128256", ms, 4 * b * n + 4 * b, read_ceiling_us=read_ceiling_us(xs))
         ms = _time_calls(torch, stream, lambda i: ext.batched_logsumexp_nolut(xs[i % nb]), nb, iters)
         rec("C4_q16_f32in_nolut_512x128256", ms, 4 * b * n + 4 * b)
         qs = [torch.clamp(torch.round(x * 94548.4609375), -2 ** 31, 2 ** 31 - 1).to(torch.int32) for x in xs]
@@ -388,7 +435,7 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
         q6 = [torch.clamp(torch.round(torch.randn(b, n, device=dev, generator=gen) * 2 * 92.33248),
                           -32768, 32767).to(torch.int16) for _ in range(nb)]
         ms = _time_calls(torch, stream, lambda i: ext.batched_logsumexp_q10_6(q6[i % nb]), nb, iters)
-        rec("C4_q10_6_i16in_1024x32000", ms, 2 * b * n + 4 * b)
+        rec("C4_q10_6_i16in_1024x32000", ms, 2 * b * n + 4 * b, read_ceiling_us=read_ceiling_us(q6))
         del q6
     if want("C5"):
         # C5: sparse PC, 1M sum nodes, power-law fan-in (alpha = 2) on [2, 256], batch 512
@@ -493,7 +540,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-configs", action="store_true", help="skip the other BASELINE configs")
     ap.add_argument("--only", default=None,
-                    help="comma-separated config groups (C3, split, sls, published, latency, C4, C5) to run alone, "
+                    help="comma-separated config groups (C3, split, sls, published, ramp, latency, C4, C5) to run alone, "
                          "without the C2 "
                          "step; for profiling passes over one group")
     ap.add_argument("--copy-calib", action="store_true",
@@ -512,7 +559,7 @@ def main():
         import fuselse_amd
 
         groups = set(args.only.split(","))
-        unknown = groups - {"C3", "split", "sls", "published", "latency", "C4", "C5"}
+        unknown = groups - {"C3", "split", "sls", "published", "ramp", "latency", "C4", "C5"}
         if unknown:
             log(f"bench.py: unknown config groups {sorted(unknown)}")
             sys.exit(2)
