@@ -393,14 +393,18 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
         res["ramp"] = ramp
         del big
     if want("latency"):
-        # Dependent-chain latencies of the IntLSE pair steps on one CU
-        # (fl_diag_chain_latency): shader-clock cycles per step of one wave
+        # Dependent-chain latencies of the IntLSE pair steps and of 16-byte
+        # LDS access patterns on one CU (fl_diag_chain_latency): shader-clock
+        # cycles per step of one wave
         # alone on its SIMD, of four waves (one per SIMD) and of sixteen (four
         # per SIMD, the occupancy of the C4 Q10.6 kernel), median over waves.
         from fuselse_amd import _lib
 
         steps = 4096
-        kinds = {0: "v_add_u32", 1: "ds_read_u8", 2: "q10_6_pair_step", 3: "q16_pair_step"}
+        kinds = {0: "v_add_u32", 1: "ds_read_u8", 2: "q10_6_pair_step", 3: "q16_pair_step", 4: "ds_read_b128_own_slot",
+                 5: "ds_write_read_b128_own_slot", 6: "ds_read_b128_rows_of_68_transposed",
+                 7: "ds_write_read_b128_rows_of_68", 8: "ds_read_b128_tile_layout_transposed",
+                 9: "ds_write_read_b128_tile_layout"}
         lat = {}
         for kind, kname in kinds.items():
             for waves in (1, 4, 16):

@@ -10,6 +10,7 @@
 #include "fl_status.hpp"
 #include "lse_common.hpp"
 #include "lse_pair.hpp"
+#include "lse_tile_layout.hpp"
 
 namespace fl {
 
@@ -47,18 +48,42 @@ __global__ __launch_bounds__(256) void read_stream_kernel(const char* __restrict
 //   KIND 1: ds_read_u8 addressed by the previous value (a table of bytes);
 //   KIND 2: the Q10.6 pair step of the row kernels (max, two subtracts, med3,
 //           ds_read_u8 of the gap table, add), q10_pair;
-//   KIND 3: the Q16.16 pair step with its LDS correction table, q16_pair.
+//   KIND 3: the Q16.16 pair step with its LDS correction table, q16_pair;
+//   KIND 4: ds_read_b128, lane l reading words 4l .. 4l+3 of the table
+//           (no two lanes share a bank row), addressed by the previous value
+//           (the table holds each slot's own index): the reference figure
+//           for the LDS bank-conflict counter on 16-byte accesses;
+//   KIND 5: ds_write_b128 of the lane's own 16-byte slot, then the KIND 4
+//           read of it (the same figure for 16-byte writes);
+//   KIND 6: ds_read_b128 at row l % 16, block 4 (l / 16) of rows of 68 words:
+//           the transposed tile read with the rows padded in place;
+//   KIND 7: ds_write_b128, then the read, at row 4 (l / 16), block l % 16 of the
+//           same rows: the row-wise tile stores and reloads;
+//   KIND 8, 9: KIND 6 and 7 in the layout the block-layout backward keeps
+//           its tiles in (rows of kTileLD words, blocks placed by tile_col).
 // The operand each step pairs with comes from the step index (a scalar
 // value), so the only dependence is through the chain.  With 64 * w threads
 // the block puts w / 4 waves on each of the CU's four SIMDs.
 template <int KIND>
+__device__ __forceinline__ int slot_word(int i) {
+    if constexpr (KIND == 6) return 68 * (i & 15) + 16 * (i >> 4);
+    else if constexpr (KIND == 7) return 68 * 4 * (i >> 4) + 4 * (i & 15);
+    else if constexpr (KIND == 8) return sparse::kTileLD * (i & 15) + sparse::tile_col(i & 15, 16 * (i >> 4));
+    else if constexpr (KIND == 9) return sparse::kTileLD * 4 * (i >> 4) + sparse::tile_col(4 * (i >> 4), 4 * (i & 15));
+    else return 4 * i;
+}
+
+template <int KIND>
 __global__ __launch_bounds__(1024) void chain_latency_kernel(int steps, uint64_t* __restrict__ rec) {
     __shared__ uint8_t tab8[512];  // first: its LDS address is the byte index
     __shared__ int lut[64];
+    __shared__ __align__(16) uint32_t tabw[16 * sparse::kTileLD];  // 16-byte slots: slot_word(i) holds {i, i, 0, 0}
     for (int i = threadIdx.x; i < 512; i += blockDim.x) tab8[i] = (uint8_t)((i * 7) % 70);
     for (int i = threadIdx.x; i < 64; i += blockDim.x) lut[i] = (i * 613) & 0x1FFF;
+    for (int i = threadIdx.x; i < 64; i += blockDim.x)
+        *reinterpret_cast<u32x4*>(&tabw[slot_word<KIND>(i)]) = u32x4{(uint32_t)i, (uint32_t)i, 0u, 0u};
     __syncthreads();
-    int a = (int)(threadIdx.x & 7);
+    int a = KIND >= 4 ? (int)(threadIdx.x & 63) : (int)(threadIdx.x & 7);
     const uint64_t t0 = __builtin_amdgcn_s_memtime();
     const uint64_t r0 = __builtin_amdgcn_s_memrealtime();
     // 16 steps per loop trip, fully unrolled, so the loop's own scalar
@@ -73,8 +98,18 @@ __global__ __launch_bounds__(1024) void chain_latency_kernel(int steps, uint64_t
                 a = tab8[a];  // table bytes are below 70, so the chain stays in the table
             } else if constexpr (KIND == 2) {
                 a = q10_pair(a, (int)(((uint32_t)k * 2654435761u) >> 22) - 512, tab8);
-            } else {
+            } else if constexpr (KIND == 3) {
                 a = q16_pair<true>(a, (int)((uint32_t)k * 2654435761u) >> 6, lut);
+            } else {
+                u32x4* slot = reinterpret_cast<u32x4*>(&tabw[slot_word<KIND>(a)]);
+                // the lane's own slot only: every wave writes the same words,
+                // and slot a keeps holding a, so the chain stays on it
+                if constexpr (KIND == 5 || KIND == 7 || KIND == 9) {
+                    *slot = u32x4{(uint32_t)a, (uint32_t)k, 0u, 0u};
+                    asm volatile("" ::: "memory");  // the read goes to LDS, not back from the stored registers
+                }
+                const u32x4 v = *slot;
+                a = (int)(v.x | v.z);
             }
         }
     }
@@ -94,7 +129,7 @@ using namespace fl;
 
 extern "C" int fl_diag_chain_latency(int kind, int steps, int waves, uint64_t* rec, void* stream) {
     const char* name = "fl_diag_chain_latency";
-    FL_CHECK(kind >= 0 && kind <= 3, "%s: kind must be 0..3", name);
+    FL_CHECK(kind >= 0 && kind <= 9, "%s: kind must be 0..9", name);
     FL_CHECK(steps > 0 && steps % 16 == 0, "%s: steps must be a positive multiple of 16", name);
     FL_CHECK(waves >= 1 && waves <= 16, "%s: waves must be 1..16", name);
     FL_CHECK(rec != nullptr, "%s: rec is NULL", name);
@@ -104,7 +139,13 @@ extern "C" int fl_diag_chain_latency(int kind, int steps, int waves, uint64_t* r
     case 0: chain_latency_kernel<0><<<1, blk, 0, st>>>(steps, rec); break;
     case 1: chain_latency_kernel<1><<<1, blk, 0, st>>>(steps, rec); break;
     case 2: chain_latency_kernel<2><<<1, blk, 0, st>>>(steps, rec); break;
-    default: chain_latency_kernel<3><<<1, blk, 0, st>>>(steps, rec); break;
+    case 3: chain_latency_kernel<3><<<1, blk, 0, st>>>(steps, rec); break;
+    case 4: chain_latency_kernel<4><<<1, blk, 0, st>>>(steps, rec); break;
+    case 5: chain_latency_kernel<5><<<1, blk, 0, st>>>(steps, rec); break;
+    case 6: chain_latency_kernel<6><<<1, blk, 0, st>>>(steps, rec); break;
+    case 7: chain_latency_kernel<7><<<1, blk, 0, st>>>(steps, rec); break;
+    case 8: chain_latency_kernel<8><<<1, blk, 0, st>>>(steps, rec); break;
+    default: chain_latency_kernel<9><<<1, blk, 0, st>>>(steps, rec); break;
     }
     return launch_status(name);
 }

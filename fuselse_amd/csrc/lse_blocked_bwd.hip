@@ -35,6 +35,7 @@
 #include "../../include/fuselse_amd.h"
 #include "fl_status.hpp"
 #include "lse_common.hpp"
+#include "lse_tile_layout.hpp"
 
 namespace fl {
 namespace sparse {
@@ -570,13 +571,14 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
                                                         const int64_t* __restrict__ pids, int64_t ne, int64_t bs,
                                                         int64_t batch, int64_t chunks, int64_t items, int64_t id0) {
     constexpr int MP = (NKP + 3) / 4;
-    constexpr int LD = 68;  // padded LDS row, 16-byte aligned
+    constexpr int LD = kTileLD;  // tile row; columns placed by tile_col
     constexpr int KC = NKP < 4 ? NKP : 4;
     __shared__ __align__(16) float xt[16 * ET][LD];  // X of the tile: [edge - c0][column - b0]; one-by-one edge terms
     __shared__ __align__(16) float rt[16 * MP][LD];  // R of the tile: [parent][column - b0]
     // one-by-one parameter terms, [parent][edge - c0]: used only by the second
     // pass and the final adds, after the last read of rt, so they share its
-    // storage (keeps a workgroup at 17 KB of LDS: eight per CU)
+    // storage (keeps a workgroup at 18 KB of LDS: eight per CU, as many as
+    // the registers allow)
     static_assert(16 * MP * 16 * ET <= 16 * MP * LD, "parameter terms fit in the R tile");
     float(*gx)[16 * ET] = reinterpret_cast<float(*)[16 * ET]>(&rt[0][0]);
     const int64_t id = logical_id(id0);
@@ -589,6 +591,11 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
     const int64_t c0 = c * CE;
     const int64_t ebase = j * ne;
     const int64_t nrow0 = nids[j];
+    // this lane's column word in the row-wise tile accesses (rows 16 et +
+    // 4 kq + r: their swizzle depends on kq only) and its swizzle in the
+    // transposed reads (rows 16 pt + jc)
+    const int colw = tile_col(4 * kq, 4 * jc);
+    const int swt = tile_swz(jc);
 
     // weights of the edge-flow product, A[p = 4*ks + kq][e = c0 + 16*et + jc], and
     // the row maxima (log) over the chunk's edges
@@ -659,7 +666,8 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
 #pragma unroll
                     for (int u = 0; u < 4; ++u)
                         xe[u] = __builtin_isfinite(m[u]) ? fexp2((xv[et][r][u] - m[u]) * kLog2e) : 0.0f;
-                    *reinterpret_cast<f32x4*>(&xt[16 * et + 4 * kq + r][4 * jc]) = xe;
+                    const int row = 16 * et + 4 * kq + r;
+                    *reinterpret_cast<f32x4*>(&xt[row][colw]) = xe;
                 }
         }  // the tile's X lives in xt from here
 
@@ -684,7 +692,8 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
                     rr[kk][u] = r_factor(lwm[ks], m[u], ov[ks][u], gv[ks][u], pv, lf);
                     left = left || lf;
                 }
-                *reinterpret_cast<f32x4*>(&rt[4 * ks + kq][4 * jc]) = f32x4{rr[kk][0], rr[kk][1], rr[kk][2], rr[kk][3]};
+                *reinterpret_cast<f32x4*>(&rt[4 * ks + kq][4 * (jc ^ tile_swz(4 * ks))]) =
+                    f32x4{rr[kk][0], rr[kk][1], rr[kk][2], rr[kk][3]};
             }
 #pragma unroll
             for (int kk = 0; kk < KC; ++kk)
@@ -699,7 +708,8 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
         if constexpr (4 * NKP < 16 * MP) {
 #pragma unroll
             for (int i = 0; i < 4 * MP - NKP; ++i)
-                *reinterpret_cast<f32x4*>(&rt[4 * (NKP + i) + kq][4 * jc]) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                *reinterpret_cast<f32x4*>(&rt[4 * (NKP + i) + kq][4 * (jc ^ tile_swz(4 * (NKP + i)))]) =
+                    f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
         __builtin_amdgcn_wave_barrier();
         // product over the batch: lane l supplies R[16*pt + l%16][16*(l/16) + ks]
@@ -709,9 +719,11 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
         for (int i = 0; i < 4; ++i) {
             f32x4 ra[MP], xb[ET];
 #pragma unroll
-            for (int pt = 0; pt < MP; ++pt) ra[pt] = *reinterpret_cast<const f32x4*>(&rt[16 * pt + jc][16 * kq + 4 * i]);
+            for (int pt = 0; pt < MP; ++pt)
+                ra[pt] = *reinterpret_cast<const f32x4*>(&rt[16 * pt + jc][4 * ((4 * kq + i) ^ swt)]);
 #pragma unroll
-            for (int et = 0; et < ET; ++et) xb[et] = *reinterpret_cast<const f32x4*>(&xt[16 * et + jc][16 * kq + 4 * i]);
+            for (int et = 0; et < ET; ++et)
+                xb[et] = *reinterpret_cast<const f32x4*>(&xt[16 * et + jc][4 * ((4 * kq + i) ^ swt)]);
 #pragma unroll
             for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -726,7 +738,8 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t e = c0 + 16 * et + 4 * kq + r;
-                const f32x4 xe = *reinterpret_cast<const f32x4*>(&xt[16 * et + 4 * kq + r][4 * jc]);
+                const int row = 16 * et + 4 * kq + r;
+                const f32x4 xe = *reinterpret_cast<const f32x4*>(&xt[row][colw]);
                 float res[4];
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
@@ -800,7 +813,8 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
             for (int et = 0; et < ET; ++et)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    *reinterpret_cast<f32x4*>(&xt[16 * et + 4 * kq + r][4 * jc]) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    *reinterpret_cast<f32x4*>(&xt[16 * et + 4 * kq + r][colw]) =
+                        f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             __builtin_amdgcn_wave_barrier();
             for (int ll = 0; ll < 64; ++ll) {
                 if (l == ll) {
@@ -818,7 +832,7 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
                             const float lw = log_weight<LOGP>(params[pids[ebase + e] + p]);
                             const float xx = xm[cids[ebase + e] * batch + b0 + cu];
                             const float t = gg * fexp2((lw + xx - oo) * kLog2e);
-                            xt[ee][cu] += t;
+                            xt[ee][tile_col(ee, cu)] += t;
                             gx[p][ee] += t;
                         }
                     }
@@ -834,7 +848,7 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
                     float* orow = edge_flows + (ebase + e) * batch;
 #pragma unroll
                     for (int u = 0; u < 4; ++u) {
-                        const float t = xt[16 * et + 4 * kq + r][4 * jc + u];
+                        const float t = xt[16 * et + 4 * kq + r][colw + u];
                         if (t != 0.0f && col + u < batch) orow[col + u] += t;
                     }
                 }

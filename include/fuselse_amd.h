@@ -244,7 +244,11 @@ int fl_diag_read_stream(const void* x, int64_t nbytes, int blocks, int unroll, u
  * threads (waves 1..16, on one CU) in which every wave runs `steps` (a
  * positive multiple of 16) dependent steps of one kind: 0 = v_add_u32, 1 = ds_read_u8 addressed by the
  * previous value, 2 = the Q10.6 pair step of fl_intlse_q10_6, 3 = the Q16.16
- * pair step with its LDS table.  rec (device, 3 * waves uint64) receives per
+ * pair step with its LDS table, 4 = ds_read_b128 of the lane's own 16 bytes
+ * (a conflict-free 16-byte LDS access), 5 = ds_write_b128 of the lane's own
+ * 16 bytes followed by that read, 6 and 7 = the transposed 16-byte read and
+ * the row-wise write+read of 64-column tiles in rows of 68 words, 8 and 9 =
+ * the same in the layout the block-layout backward keeps its tiles in.  rec (device, 3 * waves uint64) receives per
  * wave: shader-clock cycles, 100 MHz real-time ticks, and the chain's final
  * value. */
 int fl_diag_chain_latency(int kind, int steps, int waves, uint64_t* rec, void* stream);
