@@ -678,15 +678,30 @@ def main():
                                              unroll, sink.data_ptr(), stream.cuda_stream))
         read_shapes[f"{blocks}x256_u{unroll}"] = round(rms * 1e3, 2)
     read_us = min(read_shapes.values())
+    # The copy ceiling of the backward's buffers: fl_diag_copy_stream, x into
+    # the grad_x ring with the backward's load and store forms, best of a few
+    # launch shapes (the first is the backward's own: one 4 KB chunk per block).
+    copy_shapes = {}
+    for blocks, unroll in ((4 * B * N // 4096, 1), (2048, 4), (4096, 4), (8192, 2), (16384, 1)):
+        cms = per_launch(lambda i: _lib.call("fl_diag_copy_stream", xs[i % NBUF].data_ptr(),
+                                             ring[(i + 1) % NBUF].data_ptr(), 4 * B * N, blocks, unroll,
+                                             stream.cuda_stream))
+        copy_shapes[f"{blocks}x256_u{unroll}"] = round(cms * 1e3, 2)
+    copy_us = min(copy_shapes.values())
     stream_ceilings = {
         "read_gbps": round(4 * B * N / (read_us * 1e-6) / 1e9, 1),
         "read_pct_peak": round(100 * 4 * B * N / (read_us * 1e-6) / HBM_PEAK, 2),
         "read_us": read_us,
         "read_us_by_launch_shape": read_shapes,
+        "copy_gbps": round(2 * 4 * B * N / (copy_us * 1e-6) / 1e9, 1),
+        "copy_pct_peak": round(100 * 2 * 4 * B * N / (copy_us * 1e-6) / HBM_PEAK, 2),
+        "copy_us": copy_us,
+        "copy_us_by_launch_shape": copy_shapes,
         "torch_mul_read_write_gbps": round(2 * 4 * B * N / (mul_ms * 1e-3) / 1e9, 1),
         "torch_fill_write_gbps": round(4 * B * N / (fill_ms * 1e-3) / 1e9, 1),
     }
     log(f"reference streams: read {stream_ceilings['read_gbps']} GB/s ({read_us} us), "
+        f"copy {stream_ceilings['copy_gbps']} GB/s ({copy_us} us), "
         f"torch mul r+w {stream_ceilings['torch_mul_read_write_gbps']} GB/s, "
         f"fill {stream_ceilings['torch_fill_write_gbps']} GB/s")
 
@@ -761,7 +776,8 @@ def main():
                 "robust_set_extra_pct_vs_plain": round(100 * (fwd_rob_ms / fwd_plain_ms - 1), 2),
                 "pct_of_read_ceiling": round(100 * read_us / (fwd_ms * 1e3), 2)},
         "bwd": {"us": round(bwd_ms * 1e3, 2), "gbps": round(bwd_gbps, 1),
-                "pct_peak": round(100 * bwd_gbps * 1e9 / HBM_PEAK, 2), "bytes": BWD_BYTES},
+                "pct_peak": round(100 * bwd_gbps * 1e9 / HBM_PEAK, 2), "bytes": BWD_BYTES,
+                "pct_of_copy_ceiling": round(100 * copy_us / (bwd_ms * 1e3), 2)},
         "roofline": {"bound": "hbm", "kernel": "lse_bwd_row_chunks<float, 1, LseGrad, true> (fused backward)",
                      "achieved": round(bwd_gbps, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                      "frac": round(bwd_gbps * 1e9 / HBM_PEAK, 4), "traffic": traffic,

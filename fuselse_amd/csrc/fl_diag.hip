@@ -1,4 +1,6 @@
-// Read-bandwidth reference for the measurements (no counterpart in the
+// Bandwidth and latency references for the measurements.
+//
+// Read-bandwidth reference (no counterpart in the
 // reference): streams a buffer from HBM with the forward kernels' load form
 // (16-byte buffer loads with the nontemporal hint) in a flat grid-stride
 // order, and does nothing else with the data.  Its rate over the forward's own
@@ -37,6 +39,30 @@ __global__ __launch_bounds__(256) void read_stream_kernel(const char* __restrict
         for (int u = 0; u < U; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
     }
     if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+
+// Read+write reference (no counterpart in the reference): copies a buffer
+// with the backward kernels' forms, 16-byte nontemporal buffer loads and
+// 16-byte buffer stores written through to memory (sc1 nt), in the same flat
+// grid-stride order as read_stream_kernel.  Its rate is the copy ceiling the
+// fused backward (one read and one write of the row) is held against.
+template <int U>
+__global__ __launch_bounds__(256) void copy_stream_kernel(const char* __restrict__ x, char* __restrict__ y,
+                                                          int64_t nbytes) {
+    constexpr int64_t CHUNK = 256 * U * 16;
+    const int tid = threadIdx.x;
+    for (int64_t c = blockIdx.x; c * CHUNK < nbytes; c += gridDim.x) {
+        const int64_t left = nbytes - c * CHUNK;
+        const int nrec = left > CHUNK ? (int)CHUNK : (int)left;
+        const __amdgpu_buffer_rsrc_t rx =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(x + c * CHUNK), 0, nrec, 0x00020000);
+        const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(y + c * CHUNK, 0, nrec, 0x00020000);
+        u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = __builtin_amdgcn_raw_buffer_load_b128(rx, tid * 16 + u * 4096, 0, kLoadStreamAux);
+#pragma unroll
+        for (int u = 0; u < U; ++u) __builtin_amdgcn_raw_buffer_store_b128(v[u], ry, tid * 16 + u * 4096, 0, kStoreStreamAux);
+    }
 }
 
 // Dependent-chain latencies of the IntLSE pair steps (no counterpart in the
@@ -165,6 +191,26 @@ extern "C" int fl_diag_read_stream(const void* x, int64_t nbytes, int blocks, in
     case 4: read_stream_kernel<4><<<blocks, 256, 0, st>>>(static_cast<const char*>(x), nbytes, sink); break;
     case 8: read_stream_kernel<8><<<blocks, 256, 0, st>>>(static_cast<const char*>(x), nbytes, sink); break;
     default: return set_error(FL_EINVAL, "%s: unroll must be 1, 2, 4 or 8", name);
+    }
+    return launch_status(name);
+}
+
+extern "C" int fl_diag_copy_stream(const void* x, void* y, int64_t nbytes, int blocks, int unroll, void* stream) {
+    const char* name = "fl_diag_copy_stream";
+    FL_CHECK(nbytes >= 0 && nbytes % 16 == 0, "%s: nbytes must be a non-negative multiple of 16", name);
+    FL_CHECK((reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0,
+             "%s: x and y must be 16-byte aligned", name);
+    FL_CHECK(blocks > 0 && blocks <= (1 << 24), "%s: blocks out of range", name);
+    if (nbytes == 0) return ok();
+    FL_CHECK(x != nullptr && y != nullptr, "%s: x or y is NULL", name);
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const char* xs = static_cast<const char*>(x);
+    char* ys = static_cast<char*>(y);
+    switch (unroll) {
+    case 1: copy_stream_kernel<1><<<blocks, 256, 0, st>>>(xs, ys, nbytes); break;
+    case 2: copy_stream_kernel<2><<<blocks, 256, 0, st>>>(xs, ys, nbytes); break;
+    case 4: copy_stream_kernel<4><<<blocks, 256, 0, st>>>(xs, ys, nbytes); break;
+    default: return set_error(FL_EINVAL, "%s: unroll must be 1, 2 or 4", name);
     }
     return launch_status(name);
 }

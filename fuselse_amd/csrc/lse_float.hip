@@ -645,7 +645,11 @@ __device__ __forceinline__ void bwd_vec(const RowOut<T, BUF>& dst, const T* body
 
 // Long rows: grid = B * chunks_per_row blocks of 256 threads; a block covers
 // 256*U consecutive vectors of one row.  x and grad_x share their alignment.
-template <typename T, int U, typename GR, bool BUF>
+// With GRAN, the chunks of a row sit on absolute 256*U*16-byte boundaries of
+// x: chunk k covers the body vectors [k*256*U - ph, (k+1)*256*U - ph), ph
+// being the body's first vector's place in its granule, and the grid holds
+// one more chunk per row.
+template <typename T, int U, bool GRAN, typename GR, bool BUF>
 __global__ __launch_bounds__(256) void lse_bwd_row_chunks(const float* __restrict__ g, const T* __restrict__ x,
                                                           const float* __restrict__ lse, T* __restrict__ gx,
                                                           int64_t N, int64_t chunks_per_row, GR gr_t) {
@@ -668,14 +672,15 @@ __global__ __launch_bounds__(256) void lse_bwd_row_chunks(const float* __restric
     const T* xb = xr + sp.head;
     const RowOut<T, BUF> gb(gr + sp.head, sp.nvec);
     const bool fma_ok = __builtin_fabsf(lv) < 64.0f;
-    const int64_t i0 = chunk * 256 * U + tid;
+    const int64_t ph = GRAN ? (int64_t)((reinterpret_cast<uintptr_t>(xb) >> 4) & (256 * U - 1)) : 0;
+    const int64_t i0 = chunk * 256 * U + tid - ph;
     if constexpr (U == 1) {
-        if (i0 < sp.nvec) bwd_vec<T, GR>(gb, xb, i0, sp.head, gv, lv, fma_ok, t, g0);
+        if ((!GRAN || i0 >= 0) && i0 < sp.nvec) bwd_vec<T, GR>(gb, xb, i0, sp.head, gv, lv, fma_ok, t, g0);
     } else {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int64_t i = i0 + (int64_t)u * 256;
-            if (i < sp.nvec) bwd_vec<T, GR>(gb, xb, i, sp.head, gv, lv, fma_ok, t, g0);
+            if ((!GRAN || i >= 0) && i < sp.nvec) bwd_vec<T, GR>(gb, xb, i, sp.head, gv, lv, fma_ok, t, g0);
         }
     }
 }
@@ -729,9 +734,23 @@ static void launch_bwd_vec(const float* g, const T* x, const float* lse, T* gx, 
     if (vecs >= 1024) {
         // one 16-byte vector per lane: measured best for fp32 (with 128x2 and 1024x1)
         constexpr int U = 1;
-        const int64_t cpr = (vecs + 256 * U - 1) / (256 * U);
-        lse_bwd_row_chunks<T, U, GR, BUF>
-            <<<dim3((unsigned)(B * cpr)), dim3(256), 0, st>>>(g, x, lse, gx, N, cpr, gr_t);
+        // Rows of at least 32 chunks whose starts do not all fall on 4 KB
+        // boundaries take their chunks on absolute 4 KB boundaries: a chunk
+        // that straddles one streams slower (fp32 rows of 128257: 87.2 ->
+        // 81.3 us, (512, 128256) 79.8 -> 79.2, bf16 (2048, 128256) 162.2 ->
+        // 158.8).  Shorter rows pay more for the extra chunk per row than
+        // they gain (fp32 (8192, 8000) 79.0 -> 81.5).
+        const int64_t cpr0 = (vecs + 256 * U - 1) / (256 * U);
+        const bool granules =
+            cpr0 >= 32 && (((int64_t)N * (int64_t)sizeof(T)) % 4096 != 0 || (reinterpret_cast<uintptr_t>(x) & 4095u) != 0);
+        // (a run-time switch measured 1-3% slower on every shape: a wave
+        // handles one vector, so the kernel is two instantiations)
+        if (granules)
+            lse_bwd_row_chunks<T, U, true, GR, BUF>
+                <<<dim3((unsigned)(B * (cpr0 + 1))), dim3(256), 0, st>>>(g, x, lse, gx, N, cpr0 + 1, gr_t);
+        else
+            lse_bwd_row_chunks<T, U, false, GR, BUF>
+                <<<dim3((unsigned)(B * cpr0)), dim3(256), 0, st>>>(g, x, lse, gx, N, cpr0, gr_t);
         return;
     }
     int64_t lpr = pow2_ceil((vecs + 3) / 4);
