@@ -680,13 +680,15 @@ def main():
     read_us = min(read_shapes.values())
     # The copy ceiling of the backward's buffers: fl_diag_copy_stream, x into
     # the grad_x ring with the backward's load and store forms, best of a few
-    # launch shapes (the first is the backward's own: one 4 KB chunk per block).
+    # launch shapes (the backward's own, one 4 KB chunk per 256-thread block;
+    # one 1 KB chunk per one-wave block; grid-stride orders).
     copy_shapes = {}
-    for blocks, unroll in ((4 * B * N // 4096, 1), (2048, 4), (4096, 4), (8192, 2), (16384, 1)):
+    for blocks, threads, unroll in ((4 * B * N // 4096, 256, 1), (4 * B * N // 1024, 64, 1), (2048, 256, 4),
+                                    (8192, 256, 2), (16384, 64, 4)):
         cms = per_launch(lambda i: _lib.call("fl_diag_copy_stream", xs[i % NBUF].data_ptr(),
-                                             ring[(i + 1) % NBUF].data_ptr(), 4 * B * N, blocks, unroll,
+                                             ring[(i + 1) % NBUF].data_ptr(), 4 * B * N, blocks, threads, unroll,
                                              stream.cuda_stream))
-        copy_shapes[f"{blocks}x256_u{unroll}"] = round(cms * 1e3, 2)
+        copy_shapes[f"{blocks}x{threads}_u{unroll}"] = round(cms * 1e3, 2)
     copy_us = min(copy_shapes.values())
     stream_ceilings = {
         "read_gbps": round(4 * B * N / (read_us * 1e-6) / 1e9, 1),
@@ -778,7 +780,7 @@ def main():
         "bwd": {"us": round(bwd_ms * 1e3, 2), "gbps": round(bwd_gbps, 1),
                 "pct_peak": round(100 * bwd_gbps * 1e9 / HBM_PEAK, 2), "bytes": BWD_BYTES,
                 "pct_of_copy_ceiling": round(100 * copy_us / (bwd_ms * 1e3), 2)},
-        "roofline": {"bound": "hbm", "kernel": "lse_bwd_row_chunks<float, 1, LseGrad, true> (fused backward)",
+        "roofline": {"bound": "hbm", "kernel": "lse_bwd_flat<float, LseGrad> (fused backward)",
                      "achieved": round(bwd_gbps, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                      "frac": round(bwd_gbps * 1e9 / HBM_PEAK, 4), "traffic": traffic,
                      "traffic_source": "profiles/traffic_lse_f32_c2.json (two rocprofv3 --pmc passes, FETCH_SIZE "

@@ -43,13 +43,13 @@ __global__ __launch_bounds__(256) void read_stream_kernel(const char* __restrict
 
 // Read+write reference (no counterpart in the reference): copies a buffer
 // with the backward kernels' forms, 16-byte nontemporal buffer loads and
-// 16-byte buffer stores written through to memory (sc1 nt), in the same flat
-// grid-stride order as read_stream_kernel.  Its rate is the copy ceiling the
+// 16-byte buffer stores written through to memory (sc1 nt), in a flat
+// grid-stride order over chunks of TPB * U * 16 bytes.  Its rate is the copy ceiling the
 // fused backward (one read and one write of the row) is held against.
-template <int U>
-__global__ __launch_bounds__(256) void copy_stream_kernel(const char* __restrict__ x, char* __restrict__ y,
+template <int TPB, int U>
+__global__ __launch_bounds__(TPB) void copy_stream_kernel(const char* __restrict__ x, char* __restrict__ y,
                                                           int64_t nbytes) {
-    constexpr int64_t CHUNK = 256 * U * 16;
+    constexpr int64_t CHUNK = TPB * U * 16;
     const int tid = threadIdx.x;
     for (int64_t c = blockIdx.x; c * CHUNK < nbytes; c += gridDim.x) {
         const int64_t left = nbytes - c * CHUNK;
@@ -59,9 +59,9 @@ __global__ __launch_bounds__(256) void copy_stream_kernel(const char* __restrict
         const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(y + c * CHUNK, 0, nrec, 0x00020000);
         u32x4 v[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) v[u] = __builtin_amdgcn_raw_buffer_load_b128(rx, tid * 16 + u * 4096, 0, kLoadStreamAux);
+        for (int u = 0; u < U; ++u) v[u] = __builtin_amdgcn_raw_buffer_load_b128(rx, (tid + u * TPB) * 16, 0, kLoadStreamAux);
 #pragma unroll
-        for (int u = 0; u < U; ++u) __builtin_amdgcn_raw_buffer_store_b128(v[u], ry, tid * 16 + u * 4096, 0, kStoreStreamAux);
+        for (int u = 0; u < U; ++u) __builtin_amdgcn_raw_buffer_store_b128(v[u], ry, (tid + u * TPB) * 16, 0, kStoreStreamAux);
     }
 }
 
@@ -195,7 +195,8 @@ extern "C" int fl_diag_read_stream(const void* x, int64_t nbytes, int blocks, in
     return launch_status(name);
 }
 
-extern "C" int fl_diag_copy_stream(const void* x, void* y, int64_t nbytes, int blocks, int unroll, void* stream) {
+extern "C" int fl_diag_copy_stream(const void* x, void* y, int64_t nbytes, int blocks, int threads, int unroll,
+                                   void* stream) {
     const char* name = "fl_diag_copy_stream";
     FL_CHECK(nbytes >= 0 && nbytes % 16 == 0, "%s: nbytes must be a non-negative multiple of 16", name);
     FL_CHECK((reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0,
@@ -206,11 +207,20 @@ extern "C" int fl_diag_copy_stream(const void* x, void* y, int64_t nbytes, int b
     const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const char* xs = static_cast<const char*>(x);
     char* ys = static_cast<char*>(y);
-    switch (unroll) {
-    case 1: copy_stream_kernel<1><<<blocks, 256, 0, st>>>(xs, ys, nbytes); break;
-    case 2: copy_stream_kernel<2><<<blocks, 256, 0, st>>>(xs, ys, nbytes); break;
-    case 4: copy_stream_kernel<4><<<blocks, 256, 0, st>>>(xs, ys, nbytes); break;
-    default: return set_error(FL_EINVAL, "%s: unroll must be 1, 2 or 4", name);
+    FL_CHECK(threads == 64 || threads == 256, "%s: threads must be 64 or 256", name);
+    FL_CHECK(unroll == 1 || unroll == 2 || unroll == 4, "%s: unroll must be 1, 2 or 4", name);
+    if (threads == 64) {
+        switch (unroll) {
+        case 1: copy_stream_kernel<64, 1><<<blocks, 64, 0, st>>>(xs, ys, nbytes); break;
+        case 2: copy_stream_kernel<64, 2><<<blocks, 64, 0, st>>>(xs, ys, nbytes); break;
+        default: copy_stream_kernel<64, 4><<<blocks, 64, 0, st>>>(xs, ys, nbytes); break;
+        }
+    } else {
+        switch (unroll) {
+        case 1: copy_stream_kernel<256, 1><<<blocks, 256, 0, st>>>(xs, ys, nbytes); break;
+        case 2: copy_stream_kernel<256, 2><<<blocks, 256, 0, st>>>(xs, ys, nbytes); break;
+        default: copy_stream_kernel<256, 4><<<blocks, 256, 0, st>>>(xs, ys, nbytes); break;
+        }
     }
     return launch_status(name);
 }

@@ -685,6 +685,38 @@ __global__ __launch_bounds__(256) void lse_bwd_row_chunks(const float* __restric
     }
 }
 
+// Rows whose bytes are a multiple of 16, with x and grad_x 16-byte aligned:
+// the matrix is one flat run of 16-byte vectors, taken 64 at a time (1 KB) by
+// one-wave blocks in order.  With rows of at least 1 KB a block's vectors
+// span at most two rows, and each lane takes its own row's gradient, LSE and
+// target.
+template <typename T, typename GR>
+__global__ __launch_bounds__(64) void lse_bwd_flat(const float* __restrict__ g, const T* __restrict__ x,
+                                                   const float* __restrict__ lse, T* __restrict__ gx, int64_t N,
+                                                   int64_t total_vecs, GR gr_t) {
+    constexpr int VE = Elem<T>::kVec;
+    const int64_t v0 = (int64_t)blockIdx.x * 64;
+    const int64_t row0 = v0 * VE / N;
+    const int l = threadIdx.x;
+    const int64_t v = v0 + l;
+    if (v >= total_vecs) return;
+    const int64_t e = v * VE;
+    const int64_t row = e >= (row0 + 1) * N ? row0 + 1 : row0;
+    const float g0 = g[row];
+    const float gv = gr_t.coef(row, g0);
+    const int64_t t = gr_t.target(row);
+    const float lv = lse[row];
+    const int64_t left = total_vecs - v0;
+    const int nrec = (left < 64 ? (int)left : 64) * 16;
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(x + v0 * VE), 0, nrec, 0x00020000);
+    const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(gx + v0 * VE, 0, nrec, 0x00020000);
+    float vals[VE];
+    Elem<T>::cvt(__builtin_amdgcn_raw_buffer_load_b128(rx, l * 16, 0, kLoadStreamAux), vals);
+    bwd_vals<VE>(gv, lv, __builtin_fabsf(lv) < 64.0f, vals);
+    add_at<GR::kSel, VE>(vals, e - row * N, t, g0);
+    Elem<T>::put_vec_buf(ry, l * 16, vals);
+}
+
 // Short rows: LPR lanes per row, 256/LPR rows per block, grid-stride.
 template <typename T, int LPR, typename GR, bool BUF>
 __global__ __launch_bounds__(256) void lse_bwd_group_rows(const float* __restrict__ g, const T* __restrict__ x,
@@ -731,15 +763,27 @@ static void launch_bwd_vec(const float* g, const T* x, const float* lse, T* gx, 
                            hipStream_t st) {
     constexpr int VE = Elem<T>::kVec;
     const int64_t vecs = N / VE + 1;
+    const int64_t row_bytes = N * (int64_t)sizeof(T);
+    // Whole-vector rows of 1 KB or more: the flat kernel, in the order of the
+    // fastest plain copy of the same buffers.  Against the row-chunk kernels
+    // below: (512, 128256) 79.2 -> 78.3 us, bf16 (2048, 128256) 159.6 ->
+    // 155.8, fp16 (16384, 8000) 86.1 -> 78.5, (262144, 256) 83.4 -> 80.8.
+    if (row_bytes % 16 == 0 && row_bytes >= 1024 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0) {
+        const int64_t total_vecs = B * (N / VE);
+        lse_bwd_flat<T, GR><<<dim3((unsigned)((total_vecs + 63) / 64)), dim3(64), 0, st>>>(g, x, lse, gx, N,
+                                                                                          total_vecs, gr_t);
+        return;
+    }
     if (vecs >= 1024) {
-        // one 16-byte vector per lane: measured best for fp32 (with 128x2 and 1024x1)
+        // Rows that are not whole 16-byte vectors: one vector per lane, 256
+        // per block (measured best with 128x2 and 1024x1).
         constexpr int U = 1;
         // Rows of at least 32 chunks whose starts do not all fall on 4 KB
         // boundaries take their chunks on absolute 4 KB boundaries: a chunk
         // that straddles one streams slower (fp32 rows of 128257: 87.2 ->
-        // 81.3 us, (512, 128256) 79.8 -> 79.2, bf16 (2048, 128256) 162.2 ->
-        // 158.8).  Shorter rows pay more for the extra chunk per row than
-        // they gain (fp32 (8192, 8000) 79.0 -> 81.5).
+        // 81.3 us).  Shorter rows pay more for the extra chunk per row than
+        // they gain (whole-vector rows, before the flat kernel took them:
+        // fp32 (8192, 8000) 79.0 -> 81.5).
         const int64_t cpr0 = (vecs + 256 * U - 1) / (256 * U);
         const bool granules =
             cpr0 >= 32 && (((int64_t)N * (int64_t)sizeof(T)) % 4096 != 0 || (reinterpret_cast<uintptr_t>(x) & 4095u) != 0);

@@ -243,11 +243,12 @@ int fl_diag_read_stream(const void* x, int64_t nbytes, int blocks, int unroll, u
 /* Measurement aid (no counterpart in the reference): copies nbytes of x to y
  * (a multiple of 16, both 16-byte aligned, not overlapping) with the fused
  * backward's forms, 16-byte nontemporal buffer loads and 16-byte buffer
- * stores written through to memory, in the same flat grid-stride order over
- * `blocks` blocks of 256 threads with `unroll` (1, 2 or 4) vectors per lane.
- * The benchmark reports its rate over the backward's own buffers as their
- * copy ceiling. */
-int fl_diag_copy_stream(const void* x, void* y, int64_t nbytes, int blocks, int unroll, void* stream);
+ * stores written through to memory, in a flat grid-stride order over
+ * `blocks` blocks of `threads` (64 or 256) threads with `unroll` (1, 2 or 4)
+ * vectors per lane.  The benchmark reports its best rate over the backward's
+ * own buffers as their copy ceiling. */
+int fl_diag_copy_stream(const void* x, void* y, int64_t nbytes, int blocks, int threads, int unroll,
+                        void* stream);
 
 /* Measurement aid (no counterpart in the reference): one block of 64 * waves
  * threads (waves 1..16, on one CU) in which every wave runs `steps` (a

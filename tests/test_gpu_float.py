@@ -166,12 +166,29 @@ def test_bwd_f32_matches_fp64(cuda, B, N):
     np.testing.assert_allclose(gx.astype(np.float64).sum(1), g, rtol=1e-4, atol=1e-6)
 
 
-@pytest.mark.parametrize("N,off", [(131072, 0), (131072, 4), (131072, 516), (40000, 0), (40000, 260), (32780, 8)])
+@pytest.mark.parametrize("B,N,off", [(7, 256, 0), (5, 300, 0), (3, 1000, 4), (1, 4096, 0), (33, 260, 0),
+                                     (2, 262144, 516)])
+def test_bwd_f32_flat(cuda, B, N, off):
+    """Rows of 16-byte multiples from 1 KB up: the backward walks the matrix as
+    one flat run of 1 KB chunks, a chunk spanning two rows where rows are not
+    1 KB multiples, the last chunk partial."""
+    print(f"case bwd_f32 flat B={B} N={N} off={off}", flush=True)
+    rng = np.random.default_rng(B * 7 + N + off)
+    x = (rng.standard_normal((B, N)) * 2).astype(np.float32)
+    g = rng.standard_normal(B).astype(np.float32)
+    xd = _offset_view(torch.from_numpy(x), cuda, off)
+    ext = _ext()
+    lse = ext.onepass_lse_float_robust(xd)
+    gx = ext.onepass_lse_float_backward(torch.from_numpy(g).to(cuda), xd, lse).cpu().numpy()
+    np.testing.assert_allclose(gx, O.lse_bwd_fp64(g, x, O.lse_fp64(x)), rtol=RTOL32, atol=1e-30)
+
+
+@pytest.mark.parametrize("N,off", [(131073, 0), (131073, 4), (131073, 516), (40001, 0), (40001, 260), (32781, 8)])
 def test_bwd_f32_row_granules(cuda, N, off):
-    """Rows of at least 32 chunks whose 4 KB granules fall anywhere in the row
-    (x starts `off` elements past a 256-byte boundary, rows of any length):
-    the backward's chunks then follow absolute 4 KB boundaries, with a partial
-    chunk at both ends of each row."""
+    """Rows of at least 32 chunks that are not 16-byte multiples, so that
+    their 4 KB granules fall anywhere in the row (x starts `off` elements past
+    a 256-byte boundary): the backward's chunks follow absolute 4 KB
+    boundaries, with a partial chunk at both ends of each row."""
     print(f"case bwd_f32 granules N={N} off={off}", flush=True)
     B = 3
     rng = np.random.default_rng(N + off)
@@ -324,7 +341,8 @@ def _half_ulp(want: np.ndarray, dtype) -> np.ndarray:
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("B,N,off", [(5, 7, 0), (300, 1000, 0), (64, 50257, 0), (4, 128256, 0), (7, 4099, 3),
-                                     (3, 20001, 1), (3, 131072, 8), (2, 70000, 0), (2, 70000, 136)])
+                                     (3, 20001, 1), (3, 131072, 8), (2, 70001, 0), (2, 70001, 136), (7, 512, 0),
+                                     (33, 520, 0), (5, 600, 8)])
 def test_bwd_half_matches_fp64(cuda, dtype, B, N, off):
     """Within one half ulp of the fp64 value of g * exp(x - lse) on the half
     inputs (the rounding of the store), plus the fp32 arithmetic's 1e-5."""

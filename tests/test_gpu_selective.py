@@ -75,7 +75,7 @@ def test_selective_fwd_special_values_and_bad_index(cuda):
     assert np.isnan(lp[4]) and np.isnan(lp[5]) and np.isfinite(ls[4]) and np.isfinite(ls[5])
 
 
-@pytest.mark.parametrize("B,N", [(5, 7), (300, 1000), (64, 50257), (4, 128256), (7, 4099)])
+@pytest.mark.parametrize("B,N", [(5, 7), (300, 1000), (64, 50257), (4, 128256), (7, 4099), (33, 260)])
 def test_selective_bwd_matches_fp64(cuda, B, N):
     print(f"case sls_bwd B={B} N={N}", flush=True)
     rng = np.random.default_rng(B + 7 * N)
