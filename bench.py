@@ -230,16 +230,20 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
 
     def read_ceiling_us(bufs):
         """The read ceiling of the same buffers: fl_diag_read_stream (the
-        forward's load form, flat grid-stride order), best of three launch
-        shapes, timed like the kernels."""
+        forward's load form, flat order), best of four launch shapes, timed
+        like the kernels."""
         from fuselse_amd import _lib
 
         nb = len(bufs)
+        nbytes = bufs[0].numel() * bufs[0].element_size()
         best = None
-        for blocks, unroll in ((1024, 4), (2048, 4), (4096, 2)):
+        shapes = [(1024, 256, 4), (2048, 256, 4), (4096, 256, 2)]
+        if nbytes // 2048 <= (1 << 20):
+            shapes.append((max(1, nbytes // 2048), 64, 2))
+        for blocks, threads, unroll in shapes:
             ms = _time_calls(torch, stream, lambda i: _lib.call(
-                "fl_diag_read_stream", bufs[i % nb].data_ptr(), bufs[i % nb].numel() * bufs[i % nb].element_size(),
-                blocks, unroll, sink.data_ptr(), stream.cuda_stream), nb, iters)
+                "fl_diag_read_stream", bufs[i % nb].data_ptr(), nbytes, blocks, threads, unroll, sink.data_ptr(),
+                stream.cuda_stream), nb, iters)
             best = ms if best is None or ms < best else best
         return round(best * 1e3, 2)
 
@@ -673,10 +677,11 @@ def main():
     # shapes, each timed like the forward.
     sink = torch.zeros(1, dtype=torch.int32, device=dev)
     read_shapes = {}
-    for blocks, unroll in ((1024, 4), (2048, 4), (4096, 2), (4096, 4), (8192, 2)):
+    for blocks, threads, unroll in ((1024, 256, 4), (2048, 256, 4), (4096, 256, 2), (4096, 256, 4), (8192, 256, 2),
+                                    (4 * B * N // 2048, 64, 2)):
         rms = per_launch(lambda i: _lib.call("fl_diag_read_stream", xs[i % NBUF].data_ptr(), 4 * B * N, blocks,
-                                             unroll, sink.data_ptr(), stream.cuda_stream))
-        read_shapes[f"{blocks}x256_u{unroll}"] = round(rms * 1e3, 2)
+                                             threads, unroll, sink.data_ptr(), stream.cuda_stream))
+        read_shapes[f"{blocks}x{threads}_u{unroll}"] = round(rms * 1e3, 2)
     read_us = min(read_shapes.values())
     # The copy ceiling of the backward's buffers: fl_diag_copy_stream, x into
     # the grad_x ring with the backward's load and store forms, best of a few

@@ -40,7 +40,7 @@ SIGNATURES = {
     "fl_intlse_q16_f32": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _vp]),
     "fl_intlse_q16_i32": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _vp]),
     "fl_intlse_q10_6": (_int, [_vp, _vp, _vp, _i64, _i64, _vp]),
-    "fl_diag_read_stream": (_int, [_vp, _i64, _int, _int, _vp, _vp]),
+    "fl_diag_read_stream": (_int, [_vp, _i64, _int, _int, _int, _vp, _vp]),
     "fl_diag_copy_stream": (_int, [_vp, _vp, _i64, _int, _int, _int, _vp]),
     "fl_diag_chain_latency": (_int, [_int, _int, _int, _vp, _vp]),
     "fl_sparse_csr_fwd": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _int, _vp]),

@@ -16,15 +16,15 @@
 
 namespace fl {
 
-// Block b reads chunks b, b + gridDim.x, ... of 256 * U * 16 bytes; lane t of
-// the block reads bytes t * 16 + u * 4096 of a chunk (u < U), so each group of
-// U loads is issued back to back and every wave's loads are fully coalesced.
-// The xor of the words feeds a store that happens only when it equals a
-// constant no realistic input produces, which keeps the loads live.
-template <int U>
-__global__ __launch_bounds__(256) void read_stream_kernel(const char* __restrict__ x, int64_t nbytes,
+// Block b reads chunks b, b + gridDim.x, ... of TPB * U * 16 bytes; lane t
+// of the block reads bytes (t + u * TPB) * 16 of a chunk (u < U), so each
+// group of U loads is issued back to back and every wave's loads are fully
+// coalesced.  The xor of the words feeds a store that happens only when it
+// equals a constant no realistic input produces, which keeps the loads live.
+template <int TPB, int U>
+__global__ __launch_bounds__(TPB) void read_stream_kernel(const char* __restrict__ x, int64_t nbytes,
                                                           uint32_t* __restrict__ sink) {
-    constexpr int64_t CHUNK = 256 * U * 16;
+    constexpr int64_t CHUNK = TPB * U * 16;
     const int tid = threadIdx.x;
     uint32_t acc = 0;
     for (int64_t c = blockIdx.x; c * CHUNK < nbytes; c += gridDim.x) {
@@ -34,7 +34,7 @@ __global__ __launch_bounds__(256) void read_stream_kernel(const char* __restrict
             __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(x + c * CHUNK), 0, nrec, 0x00020000);
         u32x4 v[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) v[u] = __builtin_amdgcn_raw_buffer_load_b128(r, tid * 16 + u * 4096, 0, kLoadStreamAux);
+        for (int u = 0; u < U; ++u) v[u] = __builtin_amdgcn_raw_buffer_load_b128(r, (tid + u * TPB) * 16, 0, kLoadStreamAux);
 #pragma unroll
         for (int u = 0; u < U; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
     }
@@ -176,8 +176,8 @@ extern "C" int fl_diag_chain_latency(int kind, int steps, int waves, uint64_t* r
     return launch_status(name);
 }
 
-extern "C" int fl_diag_read_stream(const void* x, int64_t nbytes, int blocks, int unroll, uint32_t* sink,
-                                   void* stream) {
+extern "C" int fl_diag_read_stream(const void* x, int64_t nbytes, int blocks, int threads, int unroll,
+                                   uint32_t* sink, void* stream) {
     const char* name = "fl_diag_read_stream";
     FL_CHECK(nbytes >= 0 && nbytes % 16 == 0, "%s: nbytes must be a non-negative multiple of 16", name);
     FL_CHECK((reinterpret_cast<uintptr_t>(x) & 15u) == 0, "%s: x is not 16-byte aligned", name);
@@ -185,12 +185,24 @@ extern "C" int fl_diag_read_stream(const void* x, int64_t nbytes, int blocks, in
     FL_CHECK(sink != nullptr, "%s: sink is NULL", name);
     if (nbytes == 0) return ok();
     const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    switch (unroll) {
-    case 1: read_stream_kernel<1><<<blocks, 256, 0, st>>>(static_cast<const char*>(x), nbytes, sink); break;
-    case 2: read_stream_kernel<2><<<blocks, 256, 0, st>>>(static_cast<const char*>(x), nbytes, sink); break;
-    case 4: read_stream_kernel<4><<<blocks, 256, 0, st>>>(static_cast<const char*>(x), nbytes, sink); break;
-    case 8: read_stream_kernel<8><<<blocks, 256, 0, st>>>(static_cast<const char*>(x), nbytes, sink); break;
-    default: return set_error(FL_EINVAL, "%s: unroll must be 1, 2, 4 or 8", name);
+    FL_CHECK(threads == 64 || threads == 256, "%s: threads must be 64 or 256", name);
+    const char* xs = static_cast<const char*>(x);
+    if (threads == 64) {
+        switch (unroll) {
+        case 1: read_stream_kernel<64, 1><<<blocks, 64, 0, st>>>(xs, nbytes, sink); break;
+        case 2: read_stream_kernel<64, 2><<<blocks, 64, 0, st>>>(xs, nbytes, sink); break;
+        case 4: read_stream_kernel<64, 4><<<blocks, 64, 0, st>>>(xs, nbytes, sink); break;
+        case 8: read_stream_kernel<64, 8><<<blocks, 64, 0, st>>>(xs, nbytes, sink); break;
+        default: return set_error(FL_EINVAL, "%s: unroll must be 1, 2, 4 or 8", name);
+        }
+    } else {
+        switch (unroll) {
+        case 1: read_stream_kernel<256, 1><<<blocks, 256, 0, st>>>(xs, nbytes, sink); break;
+        case 2: read_stream_kernel<256, 2><<<blocks, 256, 0, st>>>(xs, nbytes, sink); break;
+        case 4: read_stream_kernel<256, 4><<<blocks, 256, 0, st>>>(xs, nbytes, sink); break;
+        case 8: read_stream_kernel<256, 8><<<blocks, 256, 0, st>>>(xs, nbytes, sink); break;
+        default: return set_error(FL_EINVAL, "%s: unroll must be 1, 2, 4 or 8", name);
+        }
     }
     return launch_status(name);
 }

@@ -232,13 +232,14 @@ int fl_sparse_blocked_bwd(const float* node_flows, const float* node_mars, const
  * Measurement aid (no counterpart in the reference): reads nbytes of x (a
  * multiple of 16, 16-byte aligned) from HBM with the forward kernels' load
  * form, 16-byte nontemporal buffer loads, in a flat grid-stride order over
- * `blocks` blocks of 256 threads with `unroll` (1, 2, 4 or 8) loads per lane
- * in flight, and nothing else.  The benchmark reports its rate over the
- * forward's own input buffers as their read ceiling.  sink: one uint32 of
- * device memory the kernel may write (it writes only for a value no
- * realistic input produces).
+ * `blocks` blocks of `threads` (64 or 256) threads with `unroll` (1, 2, 4 or
+ * 8) loads per lane in flight, and nothing else.  The benchmark reports its
+ * best rate over the forward's own input buffers as their read ceiling.
+ * sink: one uint32 of device memory the kernel may write (it writes only for
+ * a value no realistic input produces).
  * ------------------------------------------------------------------------- */
-int fl_diag_read_stream(const void* x, int64_t nbytes, int blocks, int unroll, uint32_t* sink, void* stream);
+int fl_diag_read_stream(const void* x, int64_t nbytes, int blocks, int threads, int unroll, uint32_t* sink,
+                        void* stream);
 
 /* Measurement aid (no counterpart in the reference): copies nbytes of x to y
  * (a multiple of 16, both 16-byte aligned, not overlapping) with the fused
