@@ -488,11 +488,16 @@ static void launch_fwd(const T* x, OUT out, int64_t B, int64_t N, hipStream_t st
     }
     if (vecs > 512) {
         // Many mid-length rows: fp32 takes a 256-thread block per row (4%
-        // ahead of a wave per row at 1024 vectors, 2% at 4000); fp16/bf16 a
-        // wave per row in batches of 4, or 32 lanes per row for 1025..2048
-        // vectors (3% ahead at 2000).
+        // ahead of a wave per row at 1024 vectors, 2% at 4000).  fp16/bf16:
+        // from 4096 rows of more than 2048 vectors, a 256-thread block per
+        // row in batches of 4 (2-3% ahead of a wave per row at (4096, 32000)
+        // and (8192, 24000), but 3% behind at (2048, 20000); 512 threads lose
+        // 19% at 3000 vectors); 32 lanes per row for 1025..2048 vectors (3%
+        // ahead at 2000); otherwise a wave per row.
         if constexpr (!kHalf)
             launch_block<T, ROBUST, 256, 2, true, OUT>(x, out, B, N, st);
+        else if (vecs > 2048 && B >= 4096)
+            launch_block<T, ROBUST, 256, 4, true, OUT>(x, out, B, N, st);
         else if (vecs > 1024 && vecs <= 2048)
             launch_group<T, ROBUST, 32, 4, true, OUT>(x, out, B, N, st);
         else

@@ -462,6 +462,29 @@ for _h in (_F16, _BF16):
     ]
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fwd_half_many_rows_block_geometry(cuda, dtype):
+    """fp16/bf16 rows of 2049..4096 vectors from 4096 rows take one 256-thread
+    block per row in batches of 1024 vectors: rows one vector past, on and
+    short of a batch boundary, on aligned and offset storage, robust and
+    plain, against float64 logsumexp of the same half values."""
+    ext = _ext()
+    fn = ext.batched_logsumexp_fp16 if dtype == torch.float16 else ext.batched_logsumexp_bf16
+    B = 4096
+    g = torch.Generator(device=cuda)
+    g.manual_seed(17)
+    for N in (2049 * 8 + 1, 3072 * 8 - 3, 3072 * 8, 3073 * 8 + 5, 32000):
+        for off in (0, 1):
+            print(f"case fwd_half_blk256x4 {dtype} B={B} N={N} off={off}", flush=True)
+            buf = torch.empty(B * N + off + 8, dtype=dtype, device=cuda)
+            xd = buf[off:off + B * N].view(B, N)
+            xd.copy_((torch.randn(B, N, device=cuda, generator=g) * 2).to(dtype))
+            want = torch.logsumexp(xd.double(), dim=1)
+            for robust in (False, True):
+                got = fn(xd, robust=robust).double()
+                torch.testing.assert_close(got, want, rtol=RTOL16, atol=1e-6)
+
+
 @pytest.mark.parametrize("dtype,label,B,vecs,step", GEOMETRIES)
 def test_fwd_pipelined_batch_boundaries(cuda, dtype, label, B, vecs, step):
     """Rows that end exactly on, one vector short of, and past a batch
