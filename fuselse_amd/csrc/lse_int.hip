@@ -340,6 +340,142 @@ __global__ __launch_bounds__(256) void intlse_q10_6_rows(const int16_t* __restri
     }
 }
 
+// Q10.6 rows whose bodies start on 16-byte boundaries (x 16-byte aligned, N a
+// multiple of 8): 128 threads per row, thread l holding the virtual threads
+// 2l and 2l+1 of the reference tree.  Their chunks are adjacent, so one
+// 16-byte load fetches both; the two chains are folded interleaved.  The
+// virtual-warp butterfly's distances 16, 8, 4, 2 become lane distances 8, 4,
+// 2, 1 and distance 1 is the pair within the thread.  Every virtual thread
+// folds the same elements in the same order as in tree_row, so the results
+// are the same bits.  With half the waves per row, a row's chains are hidden
+// behind fewer other waves, so the launcher takes this kernel only for many
+// short rows: (8192, 4096) 15.5 -> 12.8 us and (2048, 32000) 23.9 -> 22.9,
+// while (1024, 32000) measured the same and rows of 128256 elements 29-35%
+// slower.
+// chunk pairs per thread kept in flight ahead of the chains (2 measured ahead
+// of 3 and 4: 12.80 against 13.74 and 14.55 us at (8192, 4096))
+constexpr int kQ10PairedAhead = 2;
+
+template <int D>
+__global__ __launch_bounds__(128) void intlse_q10_6_rows_paired(const int16_t* __restrict__ x,
+                                                                float* __restrict__ out,
+                                                                int32_t* __restrict__ acc_out, int64_t N) {
+    __shared__ __align__(16) uint8_t gap[388];
+    __shared__ int sh_warp[8];
+    const int l = threadIdx.x;
+    const int va = 2 * l, vb = 2 * l + 1;
+    const int16_t* row = x + (int64_t)blockIdx.x * N;
+    // rows start 16-byte aligned, so the 8-byte alignment prefix is empty
+    const int64_t n4 = N / 4;
+    const int64_t tail = N - 4 * n4;
+    const int64_t kmain = n4 / 256;
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<int16_t*>(row), 0, (int)(n4 * 8), 0x00020000);
+    auto pairc = [&](int64_t k) {
+        return __builtin_amdgcn_raw_buffer_load_b128(rsrc, l * 16, (int)(k * 2048), kBufNT);
+    };
+    // the extra chunks (k = kmain) and the suffix elements, issued before the chain
+    const bool has_xa = va < n4 - kmain * 256, has_xb = vb < n4 - kmain * 256;
+    const u32x2 xa = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rsrc, va * 8, (int)(kmain * 2048), kBufNT));
+    const u32x2 xb = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rsrc, vb * 8, (int)(kmain * 2048), kBufNT));
+    const __amdgpu_buffer_rsrc_t rrow =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<int16_t*>(row), 0, (int)(N * 2), 0x00020000);
+    const bool has_sa = va < tail, has_sb = vb < tail;
+    const int16_t sa = SrcI16::sload(rrow, (int)((has_sa ? 4 * n4 + va : N) * 2));
+    const int16_t sb = SrcI16::sload(rrow, (int)((has_sb ? 4 * n4 + vb : N) * 2));
+    u32x4 bufa[D], bufb[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) bufa[d] = pairc(d);
+    // the gap table (as Q10Setup, 128 threads), after the first loads are issued
+    __builtin_amdgcn_sched_barrier(0);
+    {
+        const int lutv = lanes_table(kLutQ10);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int d = l + 128 * j;
+            const int dc = d <= 384 ? d : 384;
+            const int lv = __shfl(lutv, Q10Setup::m_of(dc) & 63, 64);
+            if (d <= 384)
+                gap[d] = (uint8_t)(Q10Setup::m_of(d) + lv);
+            else if (d == 385)
+                gap[d] = 0;
+        }
+        __syncthreads();
+    }
+    int a = kQNegInf, b = kQNegInf;
+    bool has = false;  // no prefix: chunk 0 seeds both chains
+    auto fold = [&](const u32x4& v, bool first) {
+        int qa[4], qb[4];
+        SrcI16::unpack(u32x2{v.x, v.y}, qa);
+        SrcI16::unpack(u32x2{v.z, v.w}, qb);
+        a = first ? qa[0] : q10_pair(a, qa[0], gap);
+        b = first ? qb[0] : q10_pair(b, qb[0], gap);
+#pragma unroll
+        for (int i = 1; i < 4; ++i) {
+            a = q10_pair(a, qa[i], gap);
+            b = q10_pair(b, qb[i], gap);
+        }
+    };
+    if (kmain > 0) {
+        int64_t k = 0;
+        for (;;) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) bufb[d] = pairc(k + D + d);
+#pragma unroll
+            for (int d = 0; d < D; ++d)
+                if (k + d < kmain) fold(bufa[d], d == 0 && k == 0);
+            k += D;
+            if (k >= kmain) break;
+#pragma unroll
+            for (int d = 0; d < D; ++d) bufa[d] = pairc(k + D + d);
+#pragma unroll
+            for (int d = 0; d < D; ++d)
+                if (k + d < kmain) fold(bufb[d], false);
+            k += D;
+            if (k >= kmain) break;
+        }
+        has = true;
+    }
+    // the extra chunk of each virtual thread, then its suffix element
+    auto fold_one = [&](int& acc, bool h, const u32x2& raw) {
+        int qq[4];
+        SrcI16::unpack(raw, qq);
+        acc = h ? q10_pair(acc, qq[0], gap) : qq[0];
+        acc = q10_pair(acc, qq[1], gap);
+        acc = q10_pair(acc, qq[2], gap);
+        acc = q10_pair(acc, qq[3], gap);
+    };
+    if (has_xa) fold_one(a, has, xa);
+    if (has_xb) fold_one(b, has, xb);
+    const bool ha = has || has_xa, hb = has || has_xb;
+    if (has_sa) a = ha ? q10_pair(a, (int)sa, gap) : (int)sa;
+    if (has_sb) b = hb ? q10_pair(b, (int)sb, gap) : (int)sb;
+    // virtual-warp butterfly: distances 16, 8, 4, 2 across lanes, 1 in-thread
+    a = q10_pair(a, exact_xor<8>(a), gap);
+    b = q10_pair(b, exact_xor<8>(b), gap);
+    a = q10_pair(a, exact_xor<4>(a), gap);
+    b = q10_pair(b, exact_xor<4>(b), gap);
+    a = q10_pair(a, exact_xor<2>(a), gap);
+    b = q10_pair(b, exact_xor<2>(b), gap);
+    a = q10_pair(a, exact_xor<1>(a), gap);
+    b = q10_pair(b, exact_xor<1>(b), gap);
+    a = q10_pair(a, b, gap);  // distance 1: both virtual threads end with pair(a, b)
+    if ((l & 15) == 0) sh_warp[l >> 4] = a;
+    __syncthreads();
+    if (l < 64) {
+        int v = (l & 31) < 8 ? sh_warp[l & 31] : kQNegInf;
+        v = q10_pair(v, exact_xor<16>(v), gap);
+        v = q10_pair(v, exact_xor<8>(v), gap);
+        v = q10_pair(v, exact_xor<4>(v), gap);
+        v = q10_pair(v, exact_xor<2>(v), gap);
+        v = q10_pair(v, exact_xor<1>(v), gap);
+        if (l == 0) {
+            out[blockIdx.x] = (float)v * kQ10Out;
+            if (acc_out) acc_out[blockIdx.x] = v;
+        }
+    }
+}
+
 // Calls launch(grid, x, out, acc) for consecutive chunks of at most 2^30 rows
 // (one block per row).
 template <typename T, typename LAUNCH>
@@ -430,8 +566,12 @@ extern "C" int fl_intlse_q10_6(const int16_t* q, float* out, int32_t* acc_out, i
     if (int rc = int_entry_check(name, q, out, B, N)) return rc;
     if (B == 0) return ok();
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const bool paired = (reinterpret_cast<uintptr_t>(q) & 15u) == 0 && N % 8 == 0 && N > 0 && N <= 32768 && B >= 2048;
     for_row_chunks(q, out, acc_out, B, N, [&](dim3 g, const int16_t* qc, float* oc, int32_t* ac) {
-        with_prefetch(g.x, 8, [&](auto d) { intlse_q10_6_rows<d.value><<<g, dim3(256), 0, st>>>(qc, oc, ac, N); });
+        if (paired)
+            intlse_q10_6_rows_paired<kQ10PairedAhead><<<g, dim3(128), 0, st>>>(qc, oc, ac, N);
+        else
+            with_prefetch(g.x, 8, [&](auto d) { intlse_q10_6_rows<d.value><<<g, dim3(256), 0, st>>>(qc, oc, ac, N); });
     });
     return launch_status(name);
 }

@@ -164,6 +164,28 @@ def test_q10_6_rows_and_prefixes(cuda, B, N, elem_offset):
     _assert_bits(out, acc, want, want_acc)
 
 
+@pytest.mark.parametrize("B,N", [(2048, 8), (2048, 1032), (2050, 2056), (4096, 4096), (2048, 32768), (2048, 32000)])
+@pytest.mark.parametrize("elem_offset", [0, 8, 4])
+def test_q10_6_many_short_rows(cuda, B, N, elem_offset):
+    """Many rows of at most 32768 elements, N a multiple of 8: on 16-byte
+    aligned storage (offsets 0 and 8 elements) these take the kernel whose
+    threads hold two virtual threads each; at 4 elements (8 bytes) the
+    one-virtual-thread kernel.  Rows with no whole 256-chunk round, with
+    extra chunks and with whole rounds only; saturated entries; against the
+    oracle's tree bit for bit."""
+    print(f"case q10_6 many rows B={B} N={N} off={elem_offset}", flush=True)
+    rng = np.random.default_rng(B * 7 + N + elem_offset)
+    x = (rng.standard_normal((B, N), dtype=np.float32) * np.float32(2.0))
+    q = O.to_q10_6(x)
+    q[0, ::5] = 32767
+    q[1, :] = -32768
+    q[2, 1::3] = -32768
+    qd = _offset_view(q, cuda, elem_offset) if elem_offset else torch.from_numpy(q).to(cuda)
+    out, acc = _run(_ext().batched_logsumexp_q10_6, qd)
+    want, want_acc = O.q10_6_rows(q, base_mod=qd.data_ptr() & 7, raw=True)
+    _assert_bits(out, acc, want, want_acc)
+
+
 def test_q10_6_published_shape(cuda):
     """The reference's published reduced-bit shape (512, 128256) with its
     U(-100, 0) inputs (reduced_bit/run_bench.py:58-71)."""
