@@ -33,15 +33,34 @@ __device__ __forceinline__ void fold_scalar(float& m, float& s, const T* p) {
     lse_fold<ROBUST, 1>(m, s, v);
 }
 
+// A wave-uniform 64-bit value in scalar registers.  Values the compiler
+// computes inside a divergent branch are treated as divergent even when every
+// lane holds the same; a buffer resource built from such a value would be
+// issued once per distinct value (a waterfall loop).
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)v >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 // Folds the vectors body[i], body[i + STRIDE], ... (i < nvec) into (m, s),
 // U vectors per rescale, one burst of U loads at a time: each iteration
 // issues its U loads and folds them once they land.  Where other waves cover
 // the load latency (fp32 rows, short rows) this beats the pipelined loop
-// below, whose extra loads in flight measured 2-10% slower there.
+// below, whose extra loads in flight measured 2-10% slower there.  `nfull`,
+// wave-uniform, counts the bursts that are whole for every lane of the wave;
+// the lanes' remaining vectors then come as masked bursts, their loads past
+// the end reading the lane's first remaining vector and folded as -inf (the
+// robust fold, as in fold_last).  With a per-lane loop bound instead, the
+// lanes of a row with whole and partial bursts ran them one after the other,
+// each waiting for its loads: rows of 200 fp16 elements took 12.6 us at 65536
+// rows against 8.0 us.
 template <typename T, bool ROBUST, int STRIDE, int U>
-__device__ __forceinline__ void fold_body_burst(float& m, float& s, const T* body, int64_t i, int64_t nvec) {
+__device__ __forceinline__ void fold_body_burst(float& m, float& s, const T* body, int64_t i, int64_t nvec,
+                                                int64_t nfull) {
     constexpr int VE = Elem<T>::kVec;
-    for (; i + (int64_t)(U - 1) * STRIDE < nvec; i += (int64_t)U * STRIDE) {
+    nfull = uniform64(nfull);
+    for (int64_t b = 0; b < nfull; ++b, i += (int64_t)U * STRIDE) {
         float v[U * VE];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -52,10 +71,23 @@ __device__ __forceinline__ void fold_body_burst(float& m, float& s, const T* bod
         }
         lse_fold<ROBUST, U * VE>(m, s, v);
     }
-    for (; i < nvec; i += STRIDE) {
-        float v[VE];
-        Elem<T>::vec(body + i * VE, v);
-        lse_fold<ROBUST, VE>(m, s, v);
+    for (; i < nvec; i += (int64_t)U * STRIDE) {
+        float v[U * VE];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t j = i + (int64_t)u * STRIDE;
+            const bool ok = j < nvec;
+            // select on the raw vector: selecting the widened floats holds
+            // both copies and costs a wave per SIMD of occupancy
+            u32x4 r = load_stream<u32x4>(body + (ok ? j : i) * VE);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) r[k] = ok ? r[k] : Elem<T>::kNegInfBits;
+            float t[VE];
+            Elem<T>::cvt(r, t);
+#pragma unroll
+            for (int k = 0; k < VE; ++k) v[u * VE + k] = t[k];
+        }
+        lse_fold<true, U * VE>(m, s, v);
     }
 }
 
@@ -122,15 +154,6 @@ __device__ __forceinline__ void fold_last(float& m, float& s, const u32x4 (&a)[U
 // sched_barrier after each issue keeps the scheduler from moving the fold
 // (and its wait) above the new loads; the uniform trip count keeps every
 // branch scalar.
-// A wave-uniform 64-bit value in scalar registers.  Values the compiler
-// computes inside a divergent branch are treated as divergent even when every
-// lane holds the same; a buffer resource built from such a value would be
-// issued once per distinct value (a waterfall loop).
-__device__ __forceinline__ int64_t uniform64(int64_t v) {
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)v >> 32));
-    return (int64_t)(((uint64_t)hi << 32) | lo);
-}
 
 template <typename T, bool ROBUST, int STRIDE, int U>
 __device__ __forceinline__ void fold_body(float& m, float& s, const char* base, int64_t region, int lane_off, int l,
@@ -230,7 +253,8 @@ __global__ __launch_bounds__(THREADS) void lse_fwd_block_rows(const T* __restric
             fold_body<T, ROBUST, THREADS, U>(m, s, reinterpret_cast<const char*>(p + sp.head), sp.nvec * 16, tid * 16,
                                              tid, sp.nvec, batches<(int64_t)U * THREADS>(sp.nvec));
         else
-            fold_body_burst<T, ROBUST, THREADS, U>(m, s, p + sp.head, tid, sp.nvec);
+            fold_body_burst<T, ROBUST, THREADS, U>(m, s, p + sp.head, tid, sp.nvec,
+                                                   sp.nvec / ((int64_t)U * THREADS));
         group_merge<64>(m, s);
         if ((tid & 63) == 0) {
             sh_m[tid >> 6] = m;
@@ -267,6 +291,12 @@ __global__ __launch_bounds__(256) void lse_fwd_group_rows(const T* __restrict__ 
     // bounds every row's count, and the masked last batch covers the
     // difference.
     const int64_t trips = batches<(int64_t)U * LPR>(N / VE);
+    // whole bursts for every lane of the wave: with x 16-byte aligned and rows
+    // of whole vectors every body holds N / VE vectors, otherwise at least
+    // (N - VE + 1) / VE whatever its alignment
+    const bool whole_rows = (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (N * E) % 16 == 0;
+    const int64_t nv_lo = whole_rows ? N / VE : (N >= VE - 1 ? (N - VE + 1) / VE : 0);
+    const int64_t nfull = nv_lo / ((int64_t)U * LPR);
     for (int64_t base = ((int64_t)blockIdx.x * WAVES + wave) * RPW; base < B; base += step) {
         const int64_t row = base + g;
         typename OUT::Row orow{};
@@ -288,7 +318,7 @@ __global__ __launch_bounds__(256) void lse_fwd_group_rows(const T* __restrict__ 
                 fold_body<T, ROBUST, LPR, U>(m, s, reinterpret_cast<const char*>(x + base * N), rows * N * E, lane_off,
                                              j, sp.nvec, trips);
             else
-                fold_body_burst<T, ROBUST, LPR, U>(m, s, p + sp.head, j, sp.nvec);
+                fold_body_burst<T, ROBUST, LPR, U>(m, s, p + sp.head, j, sp.nvec, nfull);
         }
         group_merge<LPR>(m, s);
         if (j == 0 && row < B) out.end(row, orow, lse_finish<ROBUST>(m, s));

@@ -485,6 +485,39 @@ def test_fwd_half_many_rows_block_geometry(cuda, dtype):
                 torch.testing.assert_close(got, want, rtol=RTOL16, atol=1e-6)
 
 
+@pytest.mark.parametrize("dtype", [_F32, _F16, _BF16])
+@pytest.mark.parametrize("lpr", [4, 8, 16, 32, 64])
+def test_fwd_short_rows_burst_boundaries(cuda, dtype, lpr):
+    """Short rows (16..512 vectors) take lpr lanes per row and bursts of 4
+    loads per lane: whole bursts for every lane of the wave, then masked
+    bursts.  Row lengths on, one vector under and one past a whole burst, and
+    lengths that are no multiple of the vector width (rows of one wave then
+    hold different vector counts), on aligned and offset storage, with a
+    ragged last row group; robust and plain against fp64."""
+    esize = torch.empty((), dtype=dtype).element_size()
+    ve = 16 // esize
+    burst = 4 * lpr  # vectors per whole burst of the wave's row group
+    vec_counts = sorted({v for v in (burst - 1, burst, burst + 1, burst // 2 + 1, 2 * burst - 3)
+                         if 16 <= v <= 512 and min(64, max(4, 1 << ((v + 3) // 4 - 1).bit_length())) == lpr})
+    assert vec_counts, lpr
+    ext = _ext()
+    rng = np.random.default_rng(lpr * esize)
+    B = 2051  # odd: the last row group of every lpr is ragged
+    for vecs in vec_counts:
+        for N, off in ((vecs * ve, 0), (vecs * ve, 1), (vecs * ve - 1, 0), (vecs * ve - ve // 2, 3)):
+            print(f"case fwd_short_burst {dtype} lpr={lpr} B={B} N={N} off={off}", flush=True)
+            xt = torch.from_numpy((rng.standard_normal((B, N)) * 2).astype(np.float32)).to(dtype)
+            xd = _offset_view(xt, cuda, off)
+            want = O.lse_fp64(xt.double().numpy())
+            for robust in (False, True):
+                if dtype == torch.float32:
+                    got = (ext.onepass_lse_float_robust if robust else ext.onepass_lse_float)(xd)
+                else:
+                    fn = ext.batched_logsumexp_fp16 if dtype == torch.float16 else ext.batched_logsumexp_bf16
+                    got = fn(xd, robust=robust)
+                _close(got.cpu().numpy(), want, RTOL32 if dtype == torch.float32 else RTOL16, atol=1e-6)
+
+
 @pytest.mark.parametrize("dtype,label,B,vecs,step", GEOMETRIES)
 def test_fwd_pipelined_batch_boundaries(cuda, dtype, label, B, vecs, step):
     """Rows that end exactly on, one vector short of, and past a batch
