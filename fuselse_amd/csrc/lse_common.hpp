@@ -15,6 +15,8 @@ constexpr float kInf = __builtin_huge_valf();
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
 
@@ -78,15 +80,14 @@ __device__ __forceinline__ void lse_merge(float& m, float& s, float m2, float s2
     m = mn;
 }
 
-// Fold K new values into (m, s) with one rescale. ROBUST keeps the base finite
-// so non-finite inputs follow the rules above; the plain variant assumes
-// finite inputs (as the reference's non-robust kernel does).
-template <bool ROBUST, int K>
-__device__ __forceinline__ void lse_fold(float& m, float& s, const float (&v)[K]) {
-    float cm = v[0];
-#pragma unroll
-    for (int k = 1; k < K; ++k) cm = fmaxf(cm, v[k]);
-    float mn = fmaxf(m, cm);
+// The rescale of a fold whose new values have maximum cm: moves (m, s) to
+// the maximum max(m, cm) and returns the base that the fold's exponents
+// subtract.  ROBUST keeps the base finite so non-finite inputs follow the
+// rules above; the plain variant assumes finite inputs (as the reference's
+// non-robust kernel does).
+template <bool ROBUST>
+__device__ __forceinline__ float lse_rebase(float& m, float& s, float cm) {
+    const float mn = fmaxf(m, cm);
     float b;
     if constexpr (ROBUST) {
         s *= lse_rescale(m, mn);
@@ -95,22 +96,36 @@ __device__ __forceinline__ void lse_fold(float& m, float& s, const float (&v)[K]
         s *= fexp2((m - mn) * kLog2e);
         b = mn;
     }
-    // exp(v - b) = exp2(v*log2e - b*log2e) as one FMA per element.  The
-    // rounding of b*log2e shifts every exponent of this fold by the same
-    // delta <= |b|*2^-23, i.e. a relative error of the result of the same
-    // order as fp32 rounding of b itself.  For |b| >= 2^24 that shift could
-    // reach the exp2 range, so those lanes take the exact-difference form.
+    m = mn;
+    return b;
+}
+
+// exp(v - b) = exp2(v*log2e - b*log2e) as one FMA per element.  The rounding
+// of b*log2e shifts every exponent of a fold by the same delta <= |b|*2^-23,
+// i.e. a relative error of the result of the same order as fp32 rounding of b
+// itself.  For |b| >= 2^24 that shift could reach the exp2 range, so those
+// lanes take the exact-difference form (lse_exp_exact).
+__device__ __forceinline__ bool lse_fused_exp_ok(float b) { return __builtin_fabsf(b) < 0x1p24f; }
+__device__ __forceinline__ float lse_exp_fused(float v, float nb) { return fexp2(__builtin_fmaf(v, kLog2e, nb)); }
+__device__ __forceinline__ float lse_exp_exact(float v, float b) { return fexp2((v - b) * kLog2e); }
+
+// Fold K new values into (m, s) with one rescale.
+template <bool ROBUST, int K>
+__device__ __forceinline__ void lse_fold(float& m, float& s, const float (&v)[K]) {
+    float cm = v[0];
+#pragma unroll
+    for (int k = 1; k < K; ++k) cm = fmaxf(cm, v[k]);
+    const float b = lse_rebase<ROBUST>(m, s, cm);
     float acc = 0.0f;
-    if (__builtin_fabsf(b) < 0x1p24f) {
+    if (lse_fused_exp_ok(b)) {
         const float nb = -b * kLog2e;
 #pragma unroll
-        for (int k = 0; k < K; ++k) acc += fexp2(__builtin_fmaf(v[k], kLog2e, nb));
+        for (int k = 0; k < K; ++k) acc += lse_exp_fused(v[k], nb);
     } else {
 #pragma unroll
-        for (int k = 0; k < K; ++k) acc += fexp2((v[k] - b) * kLog2e);
+        for (int k = 0; k < K; ++k) acc += lse_exp_exact(v[k], b);
     }
     s += acc;
-    m = mn;
 }
 
 template <bool ROBUST>

@@ -43,6 +43,55 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
     return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
+// fp16 fold of raw vectors: the same fp32 operations on the same values as
+// lse_fold over the widened elements, from the raw registers.  The maximum is
+// taken over the packed halves (exact: widening is monotonic) and each
+// exponent widens its element inside the FMA (v_fma_mix_f32).  A batch of 4
+// vectors then holds its 16 raw registers, not 32 widened floats beside them.
+template <bool ROBUST, int U>
+__device__ __forceinline__ void fold_raw_f16(float& m, float& s, const u32x4 (&a)[U]) {
+    f16x8 h[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) h[u] = __builtin_bit_cast(f16x8, a[u]);
+    f16x8 mx = h[0];
+#pragma unroll
+    for (int u = 1; u < U; ++u) mx = __builtin_elementwise_maximum(mx, h[u]);
+    const f16x4 m4 = __builtin_elementwise_maximum(__builtin_shufflevector(mx, mx, 0, 1, 2, 3),
+                                               __builtin_shufflevector(mx, mx, 4, 5, 6, 7));
+    const f16x2 m2 = __builtin_elementwise_maximum(__builtin_shufflevector(m4, m4, 0, 1),
+                                               __builtin_shufflevector(m4, m4, 2, 3));
+    const float b = lse_rebase<ROBUST>(m, s, fmaxf((float)m2[0], (float)m2[1]));
+    // Only the fused exponent: the base is an fp16 value (|b| <= 65504) or
+    // 0, or, in the plain fold of non-finite inputs, +-inf, where the fused
+    // and the exact forms give the same 0 or NaN for every element.
+    const float nb = -b * kLog2e;
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc += lse_exp_fused((float)h[u][k], nb);
+    s += acc;
+}
+
+// Folds the raw vectors a[0..U) into (m, s) with one rescale.
+template <typename T, bool ROBUST, int U>
+__device__ __forceinline__ void fold_raw(float& m, float& s, const u32x4 (&a)[U]) {
+    if constexpr (__is_same(T, _Float16)) {
+        fold_raw_f16<ROBUST, U>(m, s, a);
+    } else {
+        constexpr int VE = Elem<T>::kVec;
+        float v[U * VE];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float t[VE];
+            Elem<T>::cvt(a[u], t);
+#pragma unroll
+            for (int k = 0; k < VE; ++k) v[u * VE + k] = t[k];
+        }
+        lse_fold<ROBUST, U * VE>(m, s, v);
+    }
+}
+
 // Folds the vectors body[i], body[i + STRIDE], ... (i < nvec) into (m, s),
 // U vectors per rescale, one burst of U loads at a time: each iteration
 // issues its U loads and folds them once they land.  Where other waves cover
@@ -61,49 +110,25 @@ __device__ __forceinline__ void fold_body_burst(float& m, float& s, const T* bod
     constexpr int VE = Elem<T>::kVec;
     nfull = uniform64(nfull);
     for (int64_t b = 0; b < nfull; ++b, i += (int64_t)U * STRIDE) {
-        float v[U * VE];
+        u32x4 r[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            float t[VE];
-            Elem<T>::vec(body + (i + (int64_t)u * STRIDE) * VE, t);
-#pragma unroll
-            for (int k = 0; k < VE; ++k) v[u * VE + k] = t[k];
-        }
-        lse_fold<ROBUST, U * VE>(m, s, v);
+        for (int u = 0; u < U; ++u) r[u] = load_stream<u32x4>(body + (i + (int64_t)u * STRIDE) * VE);
+        fold_raw<T, ROBUST, U>(m, s, r);
     }
     for (; i < nvec; i += (int64_t)U * STRIDE) {
-        float v[U * VE];
+        u32x4 r[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int64_t j = i + (int64_t)u * STRIDE;
             const bool ok = j < nvec;
             // select on the raw vector: selecting the widened floats holds
             // both copies and costs a wave per SIMD of occupancy
-            u32x4 r = load_stream<u32x4>(body + (ok ? j : i) * VE);
+            r[u] = load_stream<u32x4>(body + (ok ? j : i) * VE);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) r[k] = ok ? r[k] : Elem<T>::kNegInfBits;
-            float t[VE];
-            Elem<T>::cvt(r, t);
-#pragma unroll
-            for (int k = 0; k < VE; ++k) v[u * VE + k] = t[k];
+            for (int k = 0; k < 4; ++k) r[u][k] = ok ? r[u][k] : Elem<T>::kNegInfBits;
         }
-        lse_fold<true, U * VE>(m, s, v);
+        fold_raw<T, true, U>(m, s, r);
     }
-}
-
-// Folds the raw vectors a[0..U) into (m, s) with one rescale.
-template <typename T, bool ROBUST, int U>
-__device__ __forceinline__ void fold_raw(float& m, float& s, const u32x4 (&a)[U]) {
-    constexpr int VE = Elem<T>::kVec;
-    float v[U * VE];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        float t[VE];
-        Elem<T>::cvt(a[u], t);
-#pragma unroll
-        for (int k = 0; k < VE; ++k) v[u * VE + k] = t[k];
-    }
-    lse_fold<ROBUST, U * VE>(m, s, v);
 }
 
 // Loads batch t of a lane: its vectors t * STEP + l + u * STRIDE (u < U).
