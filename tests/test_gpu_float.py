@@ -566,3 +566,40 @@ def test_fwd_pipelined_batch_boundaries(cuda, dtype, label, B, vecs, step):
                         fn = ext.batched_logsumexp_fp16 if dtype == torch.float16 else ext.batched_logsumexp_bf16
                         named = fn(xd, robust=robust)
                     assert torch.equal(named, got)
+
+
+def test_rows_of_zero_and_one_elements(cuda):
+    """N = 0: every forward gives -inf (torch.logsumexp over an empty dim), the
+    backward entries return without launching and the selective forward gives
+    NaN (no index is in range).  N = 1: lse = x and the gradient is g, up to
+    the rounding of x * log2(e) in the fused exponent (a few ulp)."""
+    print("case rows of 0 and 1 elements", flush=True)
+    ext = _ext()
+    B = 5
+    for N in (0, 1):
+        x = torch.randn(B, N, device=cuda) * 3
+        for robust in (False, True):
+            got = (ext.onepass_lse_float_robust if robust else ext.onepass_lse_float)(x)
+            torch.testing.assert_close(got, torch.logsumexp(x, -1), rtol=1e-6, atol=1e-6)
+            for dtype, fn in ((torch.float16, ext.batched_logsumexp_fp16), (torch.bfloat16, ext.batched_logsumexp_bf16)):
+                xh = x.to(dtype)
+                torch.testing.assert_close(fn(xh, robust=robust), torch.logsumexp(xh.float(), -1), rtol=1e-6, atol=1e-6)
+        if N == 0:
+            assert torch.isneginf(ext.onepass_lse_float(x)).all()
+        g = torch.randn(B, device=cuda)
+        lse = ext.onepass_lse_float_robust(x)
+        gx = ext.onepass_lse_float_backward(g, x, lse)
+        assert gx.shape == (B, N)
+        if N == 1:
+            torch.testing.assert_close(gx[:, 0], g, rtol=1e-6, atol=0.0)
+            gh = ext.onepass_lse_half_backward(g, x.half(), ext.batched_logsumexp_fp16(x.half()))
+            torch.testing.assert_close(gh[:, 0].float(), g.half().float(), rtol=2.0 ** -10, atol=0.0)
+        idx = torch.zeros(B, dtype=torch.int64, device=cuda)
+        logp, lse_s = ext.selective_log_softmax_float(x, idx)
+        if N == 0:
+            assert torch.isnan(logp).all() and torch.isneginf(lse_s).all()
+        else:
+            torch.testing.assert_close(logp, torch.zeros_like(logp), rtol=0.0, atol=1e-6)
+            torch.testing.assert_close(lse_s, x[:, 0], rtol=1e-6, atol=1e-6)
+            gs = ext.selective_log_softmax_float_backward(g, x, idx, lse_s)
+            torch.testing.assert_close(gs, torch.zeros_like(gs), rtol=0.0, atol=1e-6)

@@ -219,3 +219,24 @@ def test_acc_out_rejected_when_short(cuda):
     q = torch.zeros((8, 64), dtype=torch.int16, device=cuda)
     with pytest.raises(RuntimeError, match="acc_out must hold one int32 per row"):
         _ext().batched_logsumexp_q10_6(q, acc_out=torch.empty(3, dtype=torch.int32, device=cuda))
+
+
+@pytest.mark.parametrize("N", [0, 1])
+def test_rows_of_zero_and_one_elements(cuda, N):
+    """Rows of 0 and 1 elements: an empty row gives the tree of identities
+    (the chains start at the identity and nothing is folded), a single
+    element passes through the butterfly; bit for bit against the oracle."""
+    print(f"case intlse rows of {N}", flush=True)
+    rng = np.random.default_rng(40 + N)
+    x = (rng.standard_normal((5, N)) * 3).astype(np.float32)
+    xd = torch.from_numpy(x).to(cuda)
+    ext = _ext()
+    for fn, lut in ((ext.batched_logsumexp, True), (ext.batched_logsumexp_nolut, False)):
+        out, acc = _run(fn, xd)
+        want, want_acc = O.q16_gpu_rows(x, base_mod=xd.data_ptr() & 15, use_lut=lut, raw=True)
+        _assert_bits(out, acc, want, want_acc)
+    q = O.to_q10_6(x)
+    qd = torch.from_numpy(q).to(cuda)
+    out, acc = _run(ext.batched_logsumexp_q10_6, qd)
+    want, want_acc = O.q10_6_rows(q, base_mod=qd.data_ptr() & 15, raw=True)
+    _assert_bits(out, acc, want, want_acc)
