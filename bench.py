@@ -228,22 +228,40 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
 
     sink = torch.zeros(1, dtype=torch.int32, device=dev)
 
-    def read_ceiling_us(bufs):
+    def loop_or_graph_ms(call, nb, graph):
+        """Per-launch ms of call(i, stream): a stream loop of the calls
+        (graph=False), replays of a HIP graph of them (True), or the lower of
+        the two ("min").  A loop is paced by the host side of each call
+        (3.5-6.5 us) below about 16 MiB; a replay measured 1-2% slower than a
+        loop from 128 MiB up and the same at 32 MiB."""
+        res_ms = []
+        if graph in (True, "min"):
+            res_ms.append(_time_graph(torch, call, 4 * nb, lambda: None)[0])
+        if graph in (False, "min"):
+            res_ms.append(_time_calls(torch, stream, lambda i: call(i, stream.cuda_stream), nb, iters))
+        return min(res_ms)
+
+    def read_ceiling_us(bufs, graph=None):
         """The read ceiling of the same buffers: fl_diag_read_stream (the
         forward's load form, flat order), best of four launch shapes, timed
-        like the kernels."""
+        like the kernels: launches of under 64 MiB replayed from a HIP graph
+        (graph=None), since a launch of a few us is no longer than the host
+        side of a call; `graph` as in loop_or_graph_ms otherwise."""
         from fuselse_amd import _lib
 
         nb = len(bufs)
         nbytes = bufs[0].numel() * bufs[0].element_size()
+        if graph is None:
+            graph = nbytes < (64 << 20)
         best = None
         shapes = [(1024, 256, 4), (2048, 256, 4), (4096, 256, 2)]
         if nbytes // 2048 <= (1 << 20):
             shapes.append((max(1, nbytes // 2048), 64, 2))
         for blocks, threads, unroll in shapes:
-            ms = _time_calls(torch, stream, lambda i: _lib.call(
-                "fl_diag_read_stream", bufs[i % nb].data_ptr(), nbytes, blocks, threads, unroll, sink.data_ptr(),
-                stream.cuda_stream), nb, iters)
+            def call(i, s, blocks=blocks, threads=threads, unroll=unroll):
+                _lib.call("fl_diag_read_stream", bufs[i % nb].data_ptr(), nbytes, blocks, threads, unroll,
+                          sink.data_ptr(), s)
+            ms = loop_or_graph_ms(call, nb, graph)
             best = ms if best is None or ms < best else best
         return round(best * 1e3, 2)
 
@@ -262,8 +280,23 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
                                 (torch.bfloat16, ext.batched_logsumexp_bf16, "bf16")]:
                 nb = nbuf_for(2 * b * n)
                 bufs = [(torch.randn(b, n, device=dev, generator=gen) * 2).to(dt) for _ in range(nb)]
-                ms = _time_calls(torch, stream, lambda i: fn(bufs[i % nb]), nb, iters)
-                rec(f"C3_{tag}_fwd_{b}x{n}", ms, 2 * b * n + 4 * b, read_ceiling_us=read_ceiling_us(bufs))
+                if 2 * b * n < (64 << 20):
+                    # A launch of a few us is as long as the Python side of a
+                    # call (about 6 us), which would then set the pace: these
+                    # launches go through the same C entry the shim calls,
+                    # replayed from a HIP graph.
+                    from fuselse_amd import _lib
+
+                    outg = torch.empty(b, device=dev)
+                    entry = "fl_lse_fwd_f16" if dt == torch.float16 else "fl_lse_fwd_bf16"
+                    ms, _ = _time_graph(torch, lambda i, s: _lib.call(entry, bufs[i % nb].data_ptr(), outg.data_ptr(),
+                                                                      b, n, 0, s), 4 * nb, lambda: None)
+                    loop_ms = _time_calls(torch, stream, lambda i: fn(bufs[i % nb]), nb, iters)
+                    rec(f"C3_{tag}_fwd_{b}x{n}", ms, 2 * b * n + 4 * b, read_ceiling_us=read_ceiling_us(bufs),
+                        python_loop_us=round(loop_ms * 1e3, 2))
+                else:
+                    ms = _time_calls(torch, stream, lambda i: fn(bufs[i % nb]), nb, iters)
+                    rec(f"C3_{tag}_fwd_{b}x{n}", ms, 2 * b * n + 4 * b, read_ceiling_us=read_ceiling_us(bufs))
                 if n > 256:
                     # the fused half backward (fp32 grad and lse, half x and grad_x)
                     gsv = torch.randn(b, device=dev, generator=gen)
@@ -374,6 +407,8 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
         # Infinity Cache; a least-squares fit t = a + bytes / bw per kernel.
         import numpy as np
 
+        from fuselse_amd import _lib
+
         sizes = [8 << 20, 16 << 20, 32 << 20, 64 << 20, 128 << 20, 256 << 20, 512 << 20]
         big = torch.empty(3 * (512 << 20) // 2, dtype=torch.float16, device=dev)
         big.normal_(0.0, 2.0, generator=gen)
@@ -382,8 +417,12 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
             nreg = max(2, int(np.ceil(2 * 256e6 / sz)) + 1)
             nreg = min(nreg, (big.numel() * 2) // sz)
             regs = [big[k * (sz // 2):(k + 1) * (sz // 2)].view(-1, 256) for k in range(nreg)]
-            t_read = read_ceiling_us(regs)
-            ms = _time_calls(torch, stream, lambda i: ext.batched_logsumexp_fp16(regs[i % nreg]), nreg, iters)
+            # every point the lower of a loop of C calls and graph replays:
+            # the host side of a call is as long as the smallest launches
+            t_read = read_ceiling_us(regs, graph="min")
+            outr = torch.empty(regs[0].shape[0], device=dev)
+            ms = loop_or_graph_ms(lambda i, s: _lib.call("fl_lse_fwd_f16", regs[i % nreg].data_ptr(), outr.data_ptr(),
+                                                         regs[i % nreg].shape[0], 256, 0, s), nreg, "min")
             pts["read"].append((sz, t_read))
             pts["fp16_fwd_rows_of_256"].append((sz, round(ms * 1e3, 2)))
             log(f"ramp {sz >> 20} MB: read {t_read:.2f} us, fp16 rows of 256 {ms * 1e3:.2f} us")

@@ -59,12 +59,29 @@ def _on_device(t: torch.Tensor):
     return torch.cuda.device(idx)
 
 
+_ws_cache = {}
+
+
+def _workspace_bytes(B: int, N: int, elem_bytes: int) -> int:
+    """Bytes of split-row workspace the library's plan asks for at (B, N)
+    (0: the one-pass kernels).  The plan is a fixed function of the shape, so
+    each shape is asked once: the query is a second foreign call, about as
+    long as the launch itself."""
+    key = (B, N, elem_bytes)
+    nbytes = _ws_cache.get(key)
+    if nbytes is None:
+        if len(_ws_cache) >= 4096:
+            _ws_cache.clear()
+        nbytes = _ws_cache[key] = _lib.load().fl_lse_fwd_workspace_bytes(B, N, elem_bytes)
+    return nbytes
+
+
 def _launch_fwd(entry: str, x: torch.Tensor, out: torch.Tensor, elem_bytes: int, robust: bool) -> None:
     """One-pass kernels, or the split-row kernels (entry + "_ws") for few long
     rows, where the library asks for a workspace."""
     B, N = x.shape
     with _on_device(x):
-        nbytes = _lib.load().fl_lse_fwd_workspace_bytes(B, N, elem_bytes)
+        nbytes = _workspace_bytes(B, N, elem_bytes)
         if nbytes:
             # partials between the two split kernels; stream-ordered reuse by
             # torch's caching allocator keeps it valid until they have run
@@ -157,7 +174,7 @@ def selective_log_softmax_float(logits: torch.Tensor, index: torch.Tensor, robus
     if B == 0:
         return logp, lse
     with _on_device(logits):
-        nbytes = _lib.load().fl_lse_fwd_workspace_bytes(B, N, 4)
+        nbytes = _workspace_bytes(B, N, 4)
         ws = torch.empty(nbytes, dtype=torch.uint8, device=logits.device) if nbytes else None
         _lib.call("fl_selective_logsoftmax_f32", logits.data_ptr(), index.data_ptr(), logp.data_ptr(),
                   lse.data_ptr(), B, N, int(robust), ws.data_ptr() if ws is not None else None, nbytes,
