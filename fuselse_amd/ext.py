@@ -21,6 +21,15 @@ def _check(cond: bool, msg: str) -> None:
         raise RuntimeError(msg)
 
 
+def _check_device(ref: torch.Tensor, ref_name: str, **others) -> None:
+    """Every tensor of `others` (name=tensor; None is skipped) is on ref's
+    GPU: the kernels dereference every pointer on the launching device, where
+    another GPU's memory is not an operand."""
+    for name, t in others.items():
+        if t is not None:
+            _check(t.device == ref.device, f"{name} must be on the same device as {ref_name}")
+
+
 # torch's raw current-stream query (what its own compiled kernels use) costs
 # a fraction of building a torch.cuda.Stream object; the public form is the
 # fallback.
@@ -134,6 +143,7 @@ def onepass_lse_float_backward(grad_output: torch.Tensor, x: torch.Tensor, lse_o
     _check(lse_output.is_contiguous(), "lse_output must be contiguous")
     _check(grad_output.size(0) == x.size(0), "grad_output batch dimension must match x")
     _check(lse_output.size(0) == x.size(0), "lse_output batch dimension must match x")
+    _check_device(x, "x", grad_output=grad_output, lse_output=lse_output)
     B, N = x.shape
     grad_input = torch.empty_like(x)
     if B * N == 0:
@@ -162,6 +172,7 @@ def selective_log_softmax_float(logits: torch.Tensor, index: torch.Tensor, robus
     _check(logits.is_contiguous(), "logits must be contiguous")
     _check(index.is_contiguous(), "index must be contiguous")
     _check(index.size(0) == logits.size(0), "index batch dimension must match logits")
+    _check_device(logits, "logits", index=index)
     B, N = logits.shape
     if out is None:
         logp = torch.empty((B,), dtype=torch.float32, device=logits.device)
@@ -198,6 +209,7 @@ def selective_log_softmax_float_backward(grad_output: torch.Tensor, logits: torc
     B, N = logits.shape
     _check(grad_output.size(0) == B and index.size(0) == B and lse.size(0) == B,
            "grad_output, index and lse batch dimensions must match logits")
+    _check_device(logits, "logits", grad_output=grad_output, index=index, lse=lse)
     if out is None:
         grad = torch.empty_like(logits)
     else:
@@ -242,6 +254,7 @@ def onepass_lse_half_backward(grad_output: torch.Tensor, x: torch.Tensor, lse_ou
            "inputs must be contiguous")
     _check(grad_output.size(0) == x.size(0) and lse_output.size(0) == x.size(0),
            "grad_output and lse_output batch dimensions must match x")
+    _check_device(x, "x", grad_output=grad_output, lse_output=lse_output)
     B, N = x.shape
     grad_input = torch.empty_like(x)
     if B * N == 0:
@@ -360,6 +373,7 @@ def _sparse_blocked(node_mars, element_mars, params, nids, cids, pids, block_siz
         _check(t.is_cuda and t.dtype == torch.int64 and t.is_contiguous(), f"{name} must be a contiguous CUDA int64 tensor")
     _check(cids.dim() == 2 and pids.shape == cids.shape and nids.dim() == 1 and nids.size(0) == cids.size(0),
            "nids [nblocks], cids and pids [nblocks, num_edges] shapes disagree")
+    _check_device(node_mars, "node_mars", element_mars=element_mars, params=params, nids=nids, cids=cids, pids=pids)
     batch = node_mars.size(1)
     num_nblocks = nids.size(0)
     num_edges = cids.size(1)
@@ -407,6 +421,7 @@ def sparse_blocked_transpose(nids, cids, pids, block_size, num_elements):
         _check(t.is_cuda and t.dtype == torch.int64 and t.is_contiguous(), f"{name} must be a contiguous CUDA int64 tensor")
     _check(cids.dim() == 2 and pids.shape == cids.shape and nids.dim() == 1 and nids.size(0) == cids.size(0),
            "nids [nblocks], cids and pids [nblocks, num_edges] shapes disagree")
+    _check_device(cids, "cids", nids=nids, pids=pids)
     return _blocked_plan(nids, cids, pids, block_size, num_elements)
 
 
@@ -469,6 +484,8 @@ def sparse_blocked_backward(node_flows, element_flows, node_mars, element_mars, 
         _check(t.is_cuda and t.dtype == torch.int64 and t.is_contiguous(), f"{name} must be a contiguous CUDA int64 tensor")
     _check(cids.dim() == 2 and pids.shape == cids.shape and nids.dim() == 1 and nids.size(0) == cids.size(0),
            "nids [nblocks], cids and pids [nblocks, num_edges] shapes disagree")
+    _check_device(node_mars, "node_mars", node_flows=node_flows, element_flows=element_flows,
+                  element_mars=element_mars, params=params, param_flows=param_flows, nids=nids, cids=cids, pids=pids)
     nb, ne = cids.shape
     bs = int(block_size)
     num_el, batch = element_mars.shape
@@ -479,6 +496,7 @@ def sparse_blocked_backward(node_flows, element_flows, node_mars, element_mars, 
     if plan is None:
         plan = sparse_blocked_transpose(nids, cids, pids, bs, num_el)
     csc_off, csc_edge, csc_node, q = plan
+    _check_device(node_mars, "node_mars", csc_offsets=csc_off, csc_edges=csc_edge, csc_nodes=csc_node, param_ids=q)
     _check(csc_off.dtype == torch.int64 and csc_off.numel() == num_el + 1 and csc_edge.dtype == torch.int32
            and csc_edge.numel() == nb * ne and (bs != 1 or (csc_node is not None and q is not None
                                                              and csc_node.numel() == nb * ne and q.numel() == nb * ne)),
@@ -517,6 +535,7 @@ def sparse_csr_forward(child, offsets, child_ids, logparams, q16=False, out=None
            "child_ids must be a contiguous CUDA int32 tensor")
     _check(logparams.is_cuda and logparams.dtype == torch.float32 and logparams.is_contiguous()
            and logparams.numel() == child_ids.numel(), "logparams must be contiguous CUDA float32, one per edge")
+    _check_device(child, "child", offsets=offsets, child_ids=child_ids, logparams=logparams, out=out)
     num_nodes = offsets.numel() - 1
     batch = child.size(1)
     if out is None:
@@ -540,6 +559,7 @@ def sparse_csr_transpose(offsets, child_ids, num_children):
     _check(offsets.is_cuda and offsets.dtype == torch.int64 and offsets.dim() == 1,
            "offsets must be a CUDA int64 [num_nodes + 1] tensor")
     _check(child_ids.is_cuda and child_ids.dtype == torch.int32, "child_ids must be a CUDA int32 tensor")
+    _check_device(child_ids, "child_ids", offsets=offsets)
     nnz = child_ids.numel()
     _check(nnz < 2 ** 31 and num_children < 2 ** 31, "CSC ids are int32: nnz and num_children must be < 2^31")
     num_nodes = offsets.numel() - 1
@@ -571,6 +591,8 @@ def sparse_csr_backward(child, out, grad_out, offsets, child_ids, logparams, csc
     if csc is None:
         csc = sparse_csr_transpose(offsets, child_ids, num_children)
     csc_off, csc_edge, csc_node = csc
+    _check_device(child, "child", out=out, grad_out=grad_out, logparams=logparams, csc_offsets=csc_off,
+                  csc_edges=csc_edge, csc_nodes=csc_node)
     _check(csc_off.dtype == torch.int64 and csc_off.numel() == num_children + 1 and csc_edge.dtype == torch.int32
            and csc_node.dtype == torch.int32 and csc_edge.numel() == child_ids.numel(), "csc does not fit this layer")
     grad_child = torch.empty_like(child)

@@ -94,3 +94,57 @@ def test_split_entry_rejects_small_workspace_without_launch():
     unaligned = ctypes.c_void_p((1 << 40) + 4)
     assert lib.fl_lse_fwd_f32_ws(fake, fake, 8, 128256, 1, unaligned, need, None) == 1
     assert b"8-byte aligned" in lib.fl_last_error()
+
+
+class _OnGpu(torch.Tensor):
+    """A CPU tensor that reports itself CUDA on device `_idx` (set per
+    subclass), so the shim's checks run without a GPU."""
+    _idx = 0
+
+    @property
+    def is_cuda(self):
+        return True
+
+    @property
+    def device(self):
+        return torch.device("cuda", self._idx)
+
+
+class _OnGpu1(_OnGpu):
+    _idx = 1
+
+
+def _gpu(t, idx=0):
+    return t.as_subclass(_OnGpu1 if idx else _OnGpu)
+
+
+@pytest.mark.parametrize("fn,make,msg", [
+    ("onepass_lse_float_backward",
+     lambda: (_gpu(torch.zeros(2), 1), _gpu(torch.zeros(2, 3)), _gpu(torch.zeros(2))),
+     "grad_output must be on the same device as x"),
+    ("onepass_lse_float_backward",
+     lambda: (_gpu(torch.zeros(2)), _gpu(torch.zeros(2, 3)), _gpu(torch.zeros(2), 1)),
+     "lse_output must be on the same device as x"),
+    ("onepass_lse_half_backward",
+     lambda: (_gpu(torch.zeros(2)), _gpu(torch.zeros(2, 3, dtype=torch.float16)), _gpu(torch.zeros(2), 1)),
+     "lse_output must be on the same device as x"),
+    ("selective_log_softmax_float",
+     lambda: (_gpu(torch.zeros(2, 3)), _gpu(torch.zeros(2, dtype=torch.int64), 1)),
+     "index must be on the same device as logits"),
+    ("selective_log_softmax_float_backward",
+     lambda: (_gpu(torch.zeros(2)), _gpu(torch.zeros(2, 3)), _gpu(torch.zeros(2, dtype=torch.int64)),
+              _gpu(torch.zeros(2), 1)),
+     "lse must be on the same device as logits"),
+    ("sparse_csr_forward",
+     lambda: (_gpu(torch.zeros(4, 8)), _gpu(torch.tensor([0, 1], dtype=torch.int64), 1),
+              _gpu(torch.zeros(1, dtype=torch.int32)), _gpu(torch.zeros(1))),
+     "offsets must be on the same device as child"),
+])
+def test_shim_rejects_operands_on_another_gpu(fn, make, msg):
+    """Every operand of a multi-tensor entry must live on the launching GPU:
+    the check raises before any launch (a pointer into another GPU's memory
+    is not an operand of the kernel)."""
+    import fuselse_amd
+
+    with pytest.raises(RuntimeError, match=msg):
+        getattr(fuselse_amd.ext, fn)(*make())
