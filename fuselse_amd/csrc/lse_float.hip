@@ -970,12 +970,20 @@ struct ScratchSlot {
 };
 static ScratchSlot g_scratch[kMaxDevices];
 
-// Device address of `scratch` on the current device.
-static int scratch_address(const char* name, void** ptr) {
+// Device address of `scratch` on the current device, which must be the
+// device of `stream` (the address is only valid there).
+static int scratch_address(const char* name, hipStream_t stream, void** ptr) {
     int dev = -1;
     const hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return set_error(FL_ELAUNCH, "%s: hipGetDevice failed: %s", name, hipGetErrorString(e));
     FL_CHECK(dev >= 0 && dev < kMaxDevices, "%s: device %d beyond the %d the library tracks", name, dev, kMaxDevices);
+    if (stream != nullptr) {  // the null stream is the current device's
+        int sdev = -1;
+        const hipError_t se = hipStreamGetDevice(stream, &sdev);
+        if (se != hipSuccess)
+            return set_error(FL_EINVAL, "%s: hipStreamGetDevice failed: %s", name, hipGetErrorString(se));
+        FL_CHECK(sdev == dev, "%s: the stream belongs to device %d, the current device is %d", name, sdev, dev);
+    }
     ScratchSlot& slot = g_scratch[dev];
     std::call_once(slot.once, [&slot] { slot.err = hipGetSymbolAddress(&slot.ptr, HIP_SYMBOL(scratch)); });
     if (slot.err != hipSuccess || slot.ptr == nullptr)
@@ -997,7 +1005,7 @@ extern "C" int fl_lse_fwd_f32_noalloc(const float* x, float* out, int64_t B, int
                          (long long)need, (long long)sizeof(scratch));
     void* ws = nullptr;
     if (need > 0) {
-        const int rc = scratch_address(name, &ws);
+        const int rc = scratch_address(name, reinterpret_cast<hipStream_t>(stream), &ws);
         if (rc != FL_OK) return rc;
     }
     return fwd_launch<float>(name, x, LseOut{out}, B, N, robust, ws, sizeof(scratch),

@@ -128,7 +128,9 @@ int fl_lse_fwd_bf16_ws(const void* x, float* out, int64_t B, int64_t N, int robu
  * split plan fits (B < 320 rows, at most 64 segments), and a shape needing
  * more is rejected with FL_ERANGE.  The first call on a device takes the
  * array's address on that device (hipGetSymbolAddress), so make it once
- * outside graph capture.  All calls on one GPU share the array: calls that
+ * outside graph capture.  The array's address is per device, so a call whose
+ * split plan uses it checks that `stream` belongs to the current device
+ * (FL_EINVAL otherwise).  All calls on one GPU share the array: calls that
  * can run concurrently on one GPU (different streams) race and must not
  * overlap.
  * ------------------------------------------------------------------------- */
