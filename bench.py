@@ -374,7 +374,25 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
             rec(f"sls_fwd_{name}_{bt}x1023x{v}", ms, 4 * rows * v + 16 * rows, trl_torch_us=round(ms_trl * 1e3, 1),
                 trl_with_fuselse_lse_us=round(ms_trl_fl * 1e3, 1), trl_slice_us=round(ms_slice * 1e3, 1),
                 trl_slice_copied_us=round(ms_copy * 1e3, 1))
-            del bufs
+            # the fused backward, grad_logits = g * (onehot(index) - softmax(logits)):
+            # one read of the logits and one write of the gradient, into a
+            # preallocated output; checked once against torch autograd of trl's
+            # algorithm
+            flat = [b.view(rows, v) for b in bufs]
+            idx1 = idx.reshape(rows)
+            gr = torch.randn(rows, device=dev, generator=gen)
+            lses = [ext.selective_log_softmax_float(f, idx1)[1] for f in flat]
+            gx = torch.empty(rows, v, device=dev)
+            ms_b = _time_calls(torch, stream,
+                               lambda i: ext.selective_log_softmax_float_backward(gr, flat[i % 2], idx1, lses[i % 2],
+                                                                                  out=gx), 2, 20)
+            ext.selective_log_softmax_float_backward(gr, flat[0], idx1, lses[0], out=gx)
+            xr = bufs[0].detach().clone().requires_grad_(True)
+            (_trl_algorithm(xr, idx).reshape(rows) * gr).sum().backward()
+            assert torch.allclose(gx, xr.grad.view(rows, v), rtol=1e-4, atol=1e-6), "selective backward mismatch"
+            del xr
+            rec(f"sls_bwd_{name}_{bt}x1023x{v}", ms_b, 8 * rows * v + 16 * rows)
+            del bufs, flat, gx, lses
     if want("published"):
         # The reference's own published shape for its reduced-precision kernels,
         # (512, 128256) with x ~ U(-100, 0) (experiment_microbenchmark/reduced_bit/

@@ -745,12 +745,14 @@ __global__ __launch_bounds__(256) void lse_bwd_row_chunks(const float* __restric
     }
 }
 
-// Rows whose bytes are a multiple of 16, with x and grad_x 16-byte aligned:
-// the matrix is one flat run of 16-byte vectors, taken 64 at a time (1 KB) by
-// one-wave blocks in order.  With rows of at least 1 KB a block's vectors
-// span at most two rows, and each lane takes its own row's gradient, LSE and
-// target.
-template <typename T, typename GR>
+// Rows of at least 1 KB, x and grad_x 16-byte aligned: the matrix is one
+// flat run of 16-byte vectors, taken 64 at a time (1 KB) by one-wave blocks
+// in order.  A block's vectors span at most two rows, and each lane takes its
+// own row's gradient, LSE and target.  STRADDLE, for rows that are not whole
+// vectors (the element count of the matrix still a multiple of the vector's):
+// a vector may end one row and start the next, and its lane computes the
+// elements of each row with that row's values.
+template <typename T, typename GR, bool STRADDLE>
 __global__ __launch_bounds__(64) void lse_bwd_flat(const float* __restrict__ g, const T* __restrict__ x,
                                                    const float* __restrict__ lse, T* __restrict__ gx, int64_t N,
                                                    int64_t total_vecs, GR gr_t) {
@@ -772,6 +774,26 @@ __global__ __launch_bounds__(64) void lse_bwd_flat(const float* __restrict__ g, 
     const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(gx + v0 * VE, 0, nrec, 0x00020000);
     float vals[VE];
     Elem<T>::cvt(__builtin_amdgcn_raw_buffer_load_b128(rx, l * 16, 0, kLoadStreamAux), vals);
+    if constexpr (STRADDLE) {
+        // elements of this vector in `row`; the rest start row + 1, which
+        // exists: the vector lies inside the matrix
+        const int64_t k0 = (row + 1) * N - e;
+        if (k0 < VE) {
+            float nxt[VE];
+#pragma unroll
+            for (int k = 0; k < VE; ++k) nxt[k] = vals[k];
+            const float g1 = g[row + 1];
+            const float lv1 = lse[row + 1];
+            bwd_vals<VE>(gr_t.coef(row + 1, g1), lv1, __builtin_fabsf(lv1) < 64.0f, nxt);
+            add_at<GR::kSel, VE>(nxt, -k0, gr_t.target(row + 1), g1);
+            bwd_vals<VE>(gv, lv, __builtin_fabsf(lv) < 64.0f, vals);
+            add_at<GR::kSel, VE>(vals, e - row * N, t, g0);
+#pragma unroll
+            for (int k = 0; k < VE; ++k) vals[k] = k < k0 ? vals[k] : nxt[k];
+            Elem<T>::put_vec_buf(ry, l * 16, vals);
+            return;
+        }
+    }
     bwd_vals<VE>(gv, lv, __builtin_fabsf(lv) < 64.0f, vals);
     add_at<GR::kSel, VE>(vals, e - row * N, t, g0);
     Elem<T>::put_vec_buf(ry, l * 16, vals);
@@ -828,11 +850,21 @@ static void launch_bwd_vec(const float* g, const T* x, const float* lse, T* gx, 
     // fastest plain copy of the same buffers.  Against the row-chunk kernels
     // below: (512, 128256) 79.2 -> 78.3 us, bf16 (2048, 128256) 159.6 ->
     // 155.8, fp16 (16384, 8000) 86.1 -> 78.5, (262144, 256) 83.4 -> 80.8.
-    if (row_bytes % 16 == 0 && row_bytes >= 1024 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0) {
-        const int64_t total_vecs = B * (N / VE);
-        lse_bwd_flat<T, GR><<<dim3((unsigned)((total_vecs + 63) / 64)), dim3(64), 0, st>>>(g, x, lse, gx, N,
-                                                                                          total_vecs, gr_t);
-        return;
+    // Rows that are not whole vectors take the flat kernel too when the
+    // matrix is a whole number of vectors (some vectors then straddle two
+    // rows): gpt-2's vocabulary, fp32 (8184, 50257), 514.8 -> 489.1 us (a
+    // copy of the same bytes: 490.9), the selective backward 512.8 -> 489.6.
+    if (row_bytes >= 1024 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0) {
+        const int64_t total_vecs = B * N / VE;
+        const dim3 grid((unsigned)((total_vecs + 63) / 64));
+        if (row_bytes % 16 == 0) {
+            lse_bwd_flat<T, GR, false><<<grid, dim3(64), 0, st>>>(g, x, lse, gx, N, total_vecs, gr_t);
+            return;
+        }
+        if ((B * N) % VE == 0) {
+            lse_bwd_flat<T, GR, true><<<grid, dim3(64), 0, st>>>(g, x, lse, gx, N, total_vecs, gr_t);
+            return;
+        }
     }
     if (vecs >= 1024) {
         // Rows that are not whole 16-byte vectors: one vector per lane, 256

@@ -183,6 +183,26 @@ def test_bwd_f32_flat(cuda, B, N, off):
     np.testing.assert_allclose(gx, O.lse_bwd_fp64(g, x, O.lse_fp64(x)), rtol=RTOL32, atol=1e-30)
 
 
+@pytest.mark.parametrize("B,N", [(16, 257), (8, 1023), (4, 50257), (12, 32001), (6, 4098)])
+def test_bwd_f32_flat_vectors_straddling_rows(cuda, B, N):
+    """Rows of 1 KB or more that are not whole 16-byte vectors, over a matrix
+    that is: the flat backward's vectors then hold the end of one row and the
+    start of the next, and each element takes its own row's gradient and LSE
+    (rows of 257 put a boundary inside almost every block)."""
+    print(f"case bwd_f32 straddling B={B} N={N}", flush=True)
+    assert (B * N) % 4 == 0 and N % 4 != 0 and N * 4 >= 1024
+    rng = np.random.default_rng(B * 5 + N)
+    x = (rng.standard_normal((B, N)) * 2).astype(np.float32)
+    x[1::2] += 40.0  # neighbouring rows at very different LSE levels
+    g = rng.standard_normal(B).astype(np.float32)
+    xd = torch.from_numpy(x).to(cuda)
+    ext = _ext()
+    lse = ext.onepass_lse_float_robust(xd)
+    gx = ext.onepass_lse_float_backward(torch.from_numpy(g).to(cuda), xd, lse).cpu().numpy()
+    np.testing.assert_allclose(gx, O.lse_bwd_fp64(g, x, O.lse_fp64(x)), rtol=RTOL32, atol=1e-30)
+    np.testing.assert_allclose(gx.astype(np.float64).sum(1), g, rtol=1e-4, atol=1e-6)
+
+
 @pytest.mark.parametrize("N,off", [(131073, 0), (131073, 4), (131073, 516), (40001, 0), (40001, 260), (32781, 8)])
 def test_bwd_f32_row_granules(cuda, N, off):
     """Rows of at least 32 chunks that are not 16-byte multiples, so that
@@ -357,6 +377,30 @@ def test_bwd_half_matches_fp64(cuda, dtype, B, N, off):
     got = ext.onepass_lse_half_backward(torch.from_numpy(g).to(cuda), xd, lse)
     assert got.dtype == dtype
     got = got.double().cpu().numpy()
+    want = O.lse_bwd_fp64(g, x64, O.lse_fp64(x64))
+    err = np.abs(got - want)
+    bound = _half_ulp(want, dtype) + 1e-5 * np.abs(want)
+    assert (err <= bound).all(), (err / bound).max()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("B,N", [(16, 513), (8, 1001), (8, 50257), (4, 4098)])
+def test_bwd_half_flat_vectors_straddling_rows(cuda, dtype, B, N):
+    """Half rows of 1 KB or more that are not whole 16-byte vectors, the
+    matrix a whole number of them: vectors straddle row ends in the flat
+    backward.  Bound as in test_bwd_half_matches_fp64."""
+    print(f"case bwd_half straddling {dtype} B={B} N={N}", flush=True)
+    assert (B * N) % 8 == 0 and N % 8 != 0 and N * 2 >= 1024
+    rng = np.random.default_rng(B * 17 + N)
+    x32 = (rng.standard_normal((B, N)) * 2).astype(np.float32)
+    x32[1::2] += 30.0
+    xh = torch.from_numpy(x32).to(dtype)
+    g = rng.standard_normal(B).astype(np.float32)
+    x64 = xh.double().numpy()
+    ext = _ext()
+    xd = xh.to(cuda)
+    lse = (ext.batched_logsumexp_fp16 if dtype == torch.float16 else ext.batched_logsumexp_bf16)(xd)
+    got = ext.onepass_lse_half_backward(torch.from_numpy(g).to(cuda), xd, lse).double().cpu().numpy()
     want = O.lse_bwd_fp64(g, x64, O.lse_fp64(x64))
     err = np.abs(got - want)
     bound = _half_ulp(want, dtype) + 1e-5 * np.abs(want)

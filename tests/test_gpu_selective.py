@@ -97,6 +97,30 @@ def test_selective_bwd_matches_fp64(cuda, B, N):
     np.testing.assert_allclose(got.astype(np.float64).sum(axis=1), 0.0, atol=2e-5 * np.abs(g).max() + 1e-6)
 
 
+@pytest.mark.parametrize("B,N", [(16, 257), (8, 50257), (6, 4098)])
+def test_selective_bwd_vectors_straddling_rows(cuda, B, N):
+    """Rows that are not whole 16-byte vectors over a matrix that is: the
+    flat backward's vectors straddle row ends.  Targets sit at the last and
+    first column of neighbouring rows, so the one-hot term lands in the
+    straddling vectors on both sides."""
+    print(f"case sls_bwd straddling B={B} N={N}", flush=True)
+    assert (B * N) % 4 == 0 and N % 4 != 0
+    rng = np.random.default_rng(B * 3 + N)
+    x = (rng.standard_normal((B, N)) * 3).astype(np.float32)
+    idx = np.where(np.arange(B) % 2 == 0, N - 1, 0).astype(np.int64)
+    idx[-1] = rng.integers(0, N)
+    g = rng.standard_normal(B).astype(np.float32)
+    ext = _ext()
+    xd, id_ = torch.from_numpy(x).to(cuda), torch.from_numpy(idx).to(cuda)
+    _, lse = ext.selective_log_softmax_float(xd, id_)
+    got = ext.selective_log_softmax_float_backward(torch.from_numpy(g).to(cuda), xd, id_, lse).cpu().numpy()
+    want = O.selective_logsoftmax_bwd_fp64(g, x, idx, O.lse_fp64(x))
+    atol = 1e-6 * np.abs(g)[:, None] * np.ones_like(want)
+    err = np.abs(got - want)
+    assert (err <= 1e-5 * np.abs(want) + atol).all(), err.max()
+    np.testing.assert_allclose(got.astype(np.float64).sum(axis=1), 0.0, atol=2e-5 * np.abs(g).max() + 1e-6)
+
+
 def test_selective_bwd_unaligned_offsets(cuda):
     """Rows of odd length (scalar head and tail) and an x / grad_x pair of
     different 16-byte alignment (scalar kernel)."""
