@@ -481,6 +481,58 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
                     "cycles_per_step": round(sorted(per)[1], 2), "shader_clock_mhz": round(mhz, 0)}
                 log(f"latency {kname} {waves} waves: {sorted(per)[1]:.2f} cycles per step at {mhz:.0f} MHz")
         res["chain_latency"] = lat
+    if want("sweep"):
+        # The reference's own microbenchmark (experiment_microbenchmark/microbench/
+        # run_microbenchmark.py:88-90,109,215-240): B = 512 rows, N from 2 to
+        # 128256, x ~ U(-100, 0), its fp32 FuseLSE forward (onepass_lse_float),
+        # IntLSE Q16.16 (batched_logsumexp) and torch.logsumexp.  The library's
+        # calls are replayed from a HIP graph (most take a few us, under the
+        # host side of a call); torch's run in a stream loop; all over enough
+        # buffers to exceed twice the Infinity Cache.  The
+        # published V100 times of the same protocol (outputs/
+        # benchmark_results.json, range U(-100,0), gpu_timing) ride along.
+        from fuselse_amd import _lib
+
+        b = 512
+        v100 = {2: (0.005545, 0.005444, 0.058627), 4: (0.005206, 0.005383, 0.058729),
+                8: (0.005531, 0.005460, 0.058406), 16: (0.005336, 0.005493, 0.058678),
+                32: (0.005513, 0.005445, 0.058194), 64: (0.005526, 0.005471, 0.058818),
+                128: (0.005541, 0.005603, 0.058598), 256: (0.005428, 0.005702, 0.058865),
+                512: (0.005566, 0.006075, 0.057874), 1024: (0.005272, 0.005970, 0.059235),
+                2048: (0.005883, 0.007553, 0.058442), 4096: (0.014102, 0.016119, 0.107630),
+                8192: (0.024192, 0.026077, 0.156808), 16384: (0.043576, 0.045199, 0.278026),
+                32000: (0.080755, 0.084037, 0.510945), 50257: (0.127028, 0.129809, 0.785721),
+                65536: (0.158884, 0.162411, 1.006734), 128256: (0.310394, 0.313315, 1.935665)}
+        rows = []
+        for n in sorted(v100):
+            # at most 32 buffers and 256 captured calls: below N = 4096 the
+            # rotation fits in the Infinity Cache anyway (the reference reused
+            # one buffer throughout), and those launches are launch-bound
+            nb = min(nbuf_for(4 * b * n), 32)
+            bufs = [torch.rand(b, n, device=dev, generator=gen) * 100.0 - 100.0 for _ in range(nb)]
+            outg = torch.empty(b, device=dev)
+            calls = min(max(iters, 4 * nb), 256)
+            fl_ms, fl_out = _time_graph(
+                torch, lambda i, s: _lib.call("fl_lse_fwd_f32", bufs[i % nb].data_ptr(), outg.data_ptr(), b, n, 0, s),
+                calls, lambda: outg.clone())
+            q_ms, _ = _time_graph(
+                torch, lambda i, s: _lib.call("fl_intlse_q16_f32", bufs[i % nb].data_ptr(), outg.data_ptr(), None, b,
+                                              n, 1, s), calls, lambda: None)
+            # torch's reduction in a plain stream loop, as the reference timed it
+            # (a captured graph could hold the memset nodes torch's reductions record)
+            t_ms = _time_calls(torch, stream, lambda i: torch.logsumexp(bufs[i % nb], dim=-1), nb, calls)
+            want_lse = torch.logsumexp(bufs[(calls - 1) % nb].double(), dim=-1).float()
+            assert torch.allclose(fl_out, want_lse, rtol=1e-5, atol=1e-5), f"sweep N={n} mismatch"
+            pf, pq, pt = v100[n]
+            rows.append({"N": n, "cache_resident": nb * 4 * b * n < 512e6,
+                         "fuselse_us": round(fl_ms * 1e3, 2), "intlse_q16_us": round(q_ms * 1e3, 2),
+                         "torch_us": round(t_ms * 1e3, 2),
+                         "fuselse_pct_peak": round(100 * (4 * b * n + 4 * b) / (fl_ms * 1e-3) / HBM_PEAK, 1),
+                         "v100_fuselse_us": round(pf * 1e3, 2), "v100_intlse_us": round(pq * 1e3, 2),
+                         "v100_torch_us": round(pt * 1e3, 2)})
+            log(f"sweep N={n}: fuselse {fl_ms * 1e3:.2f} us, intlse {q_ms * 1e3:.2f} us, torch {t_ms * 1e3:.2f} us")
+            del bufs
+        res["microbench_sweep_512xN_u100"] = {"B": b, "data": "U(-100,0)", "rows": rows}
     if want("C4"):
         # C4: IntLSE fixed point
         b, n = 512, 128256
@@ -605,7 +657,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-configs", action="store_true", help="skip the other BASELINE configs")
     ap.add_argument("--only", default=None,
-                    help="comma-separated config groups (C3, split, sls, published, ramp, latency, C4, C5) to run alone, "
+                    help="comma-separated config groups (C3, split, sls, sweep, published, ramp, latency, C4, C5) to run alone, "
                          "without the C2 "
                          "step; for profiling passes over one group")
     ap.add_argument("--copy-calib", action="store_true",
@@ -624,7 +676,7 @@ def main():
         import fuselse_amd
 
         groups = set(args.only.split(","))
-        unknown = groups - {"C3", "split", "sls", "published", "ramp", "latency", "C4", "C5"}
+        unknown = groups - {"C3", "split", "sls", "sweep", "published", "ramp", "latency", "C4", "C5"}
         if unknown:
             log(f"bench.py: unknown config groups {sorted(unknown)}")
             sys.exit(2)
