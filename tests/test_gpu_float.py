@@ -233,10 +233,13 @@ def test_bwd_f32_unaligned_and_mismatched(cuda):
         np.testing.assert_allclose(gx, O.lse_bwd_fp64(g, x, O.lse_fp64(x)), rtol=RTOL32, atol=1e-30)
 
 
-def test_bwd_f32_special_rows(cuda):
-    """All -inf row -> NaN gradient (torch's grad*exp(x-result)); +inf row."""
-    print("case bwd_f32 special rows", flush=True)
-    x = O.make_robust_rows(O.make_c2_input(8, 300, seed=5), seed=8)
+@pytest.mark.parametrize("N", [300, 257, 1023])
+def test_bwd_f32_special_rows(cuda, N):
+    """All -inf row -> NaN gradient (torch's grad*exp(x-result)); +inf row.
+    N = 257 and 1023 run the flat backward with vectors straddling rows, so
+    special rows meet ordinary ones inside one vector."""
+    print(f"case bwd_f32 special rows N={N}", flush=True)
+    x = O.make_robust_rows(O.make_c2_input(8, N, seed=5), seed=8)
     g = np.ones(8, np.float32)
     xd = torch.from_numpy(x).to(cuda)
     lse = _ext().onepass_lse_float_robust(xd)
