@@ -25,6 +25,21 @@ def test_abi_version_and_error_string():
     assert isinstance(lib.fl_last_error(), bytes)
 
 
+@pytest.mark.parametrize("contents", [None, b"not an ELF object"])
+def test_missing_library_raises(monkeypatch, tmp_path, contents):
+    """An absent or unloadable library raises NativeLibraryMissing from the
+    first call: there is no CPU path to fall back on."""
+    path = tmp_path / "libfuselse_amd.so"
+    if contents is not None:
+        path.write_bytes(contents)
+    monkeypatch.setattr(_lib, "LIB_PATH", str(path))
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "_bound", {})
+    with pytest.raises(_lib.NativeLibraryMissing, match="not built" if contents is None else "cannot load"):
+        _lib.call("fl_lse_fwd_f32", None, None, 2, 3, 1, None)
+    assert issubclass(_lib.NativeLibraryMissing, RuntimeError)
+
+
 def test_invalid_arguments_rejected_without_launch():
     """Negative shapes and NULL outputs are refused on the host (no kernel)."""
     lib = _lib.load()
