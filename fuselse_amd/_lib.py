@@ -28,6 +28,9 @@ SIGNATURES = {
     "fl_lse_bwd_f32": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _vp]),
     "fl_lse_fwd_f16": (_int, [_vp, _vp, _i64, _i64, _int, _vp]),
     "fl_lse_fwd_bf16": (_int, [_vp, _vp, _i64, _i64, _int, _vp]),
+    "fl_lse_fwd_f32_keep": (_int, [_vp, _vp, _i64, _i64, _int, _vp]),
+    "fl_lse_fwd_f16_keep": (_int, [_vp, _vp, _i64, _i64, _int, _vp]),
+    "fl_lse_fwd_bf16_keep": (_int, [_vp, _vp, _i64, _i64, _int, _vp]),
     "fl_selective_logsoftmax_f32": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _int, _vp, ctypes.c_size_t, _vp]),
     "fl_selective_logsoftmax_bwd_f32": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp]),
     "fl_lse_bwd_f16": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _vp]),

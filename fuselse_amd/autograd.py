@@ -12,7 +12,10 @@ contract (fuselse/gpu/autograd.py:6-61):
   else;
 * with grad enabled and ``input.requires_grad`` it goes through an autograd
   Function whose backward is the fused ``grad * exp(x - lse)`` kernel (no
-  double backward);
+  double backward).  Its forward calls ``ext.onepass_lse_float[_robust]_keep``
+  where the ext has it (this package's does; the reference's does not): the
+  same result, with part of x left in the Infinity Cache for the backward's
+  read of it;
 * a contiguous 2-D input without grad calls the kernel directly; other shapes
   are flattened to (rows, N), made contiguous, and reshaped back;
 * ``keepdim`` unsqueezes the last dimension.
@@ -30,12 +33,19 @@ import torch
 
 def make_fuselse_logsumexp(ext, robust: bool = True, half_inputs: bool = False):
     fwd = ext.onepass_lse_float_robust if robust else ext.onepass_lse_float
+    # the forward whose backward follows (autograd): the keeping variant where
+    # the ext provides one
+    fwd_grad = getattr(ext, ("onepass_lse_float_robust" if robust else "onepass_lse_float") + "_keep", fwd)
     bwd = ext.onepass_lse_float_backward
     torch_logsumexp = torch.logsumexp
     half_fwd = {}
+    half_fwd_grad = {}
     if half_inputs:
         half_fwd = {torch.float16: lambda x: ext.batched_logsumexp_fp16(x, robust),
                     torch.bfloat16: lambda x: ext.batched_logsumexp_bf16(x, robust)}
+        f16k = getattr(ext, "batched_logsumexp_fp16_keep", ext.batched_logsumexp_fp16)
+        bf16k = getattr(ext, "batched_logsumexp_bf16_keep", ext.batched_logsumexp_bf16)
+        half_fwd_grad = {torch.float16: lambda x: f16k(x, robust), torch.bfloat16: lambda x: bf16k(x, robust)}
         half_bwd = ext.onepass_lse_half_backward
 
     class _RowLSE(torch.autograd.Function):
@@ -43,7 +53,7 @@ def make_fuselse_logsumexp(ext, robust: bool = True, half_inputs: bool = False):
         def forward(ctx, inp):
             n = inp.shape[-1]
             rows = inp.reshape(-1, n).contiguous()
-            lse = fwd(rows)
+            lse = fwd_grad(rows)
             ctx.save_for_backward(rows, lse)
             ctx.in_shape = tuple(inp.shape)
             return lse.reshape(inp.shape[:-1])
@@ -63,7 +73,7 @@ def make_fuselse_logsumexp(ext, robust: bool = True, half_inputs: bool = False):
         def forward(ctx, inp):
             n = inp.shape[-1]
             rows = inp.reshape(-1, n).contiguous()
-            lse = half_fwd[inp.dtype](rows)
+            lse = half_fwd_grad[inp.dtype](rows)
             ctx.save_for_backward(rows, lse)
             ctx.in_shape = tuple(inp.shape)
             return lse.to(inp.dtype).reshape(inp.shape[:-1])

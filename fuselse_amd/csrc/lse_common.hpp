@@ -185,6 +185,11 @@ struct bf16_t { uint16_t bits; };
 constexpr int kStoreStreamAux = 16 | 2;
 // Streamed loads through a buffer resource: nontemporal (nt), as load_stream.
 constexpr int kLoadStreamAux = 2;
+// Loads of the rows a forward leaves for the backward that follows it: plain
+// (no nt), so part of what they bring in stays in the Infinity Cache, the
+// memory-side cache in front of HBM.  nt loads leave nothing there that a
+// following read finds.
+constexpr int kLoadKeepAux = 0;
 
 // fp32 -> bfloat16 pairs with gfx950's v_cvt_pk_bf16_f32 (round to nearest
 // even, NaN stays NaN): lo in bits 0-15, hi in bits 16-31.

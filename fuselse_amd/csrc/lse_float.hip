@@ -136,7 +136,7 @@ __device__ __forceinline__ void fold_body_burst(float& m, float& s, const T* bod
 // (wave-uniform, so it lives in scalar registers), which keeps the 32-bit
 // offsets small for rows of any length; the resource's range check returns
 // zeros, without a memory access, for the bytes past `region`.
-template <int STRIDE, int U>
+template <int STRIDE, int U, int AUX = kLoadStreamAux>
 __device__ __forceinline__ void load_batch(u32x4 (&a)[U], const char* base, int64_t region, int lane_off,
                                            int64_t t) {
     constexpr int64_t STEP_BYTES = (int64_t)U * STRIDE * 16;
@@ -145,7 +145,7 @@ __device__ __forceinline__ void load_batch(u32x4 (&a)[U], const char* base, int6
     const __amdgpu_buffer_rsrc_t r =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base + t * STEP_BYTES), 0, nrec, 0x00020000);
 #pragma unroll
-    for (int u = 0; u < U; ++u) a[u] = __builtin_amdgcn_raw_buffer_load_b128(r, lane_off + u * STRIDE * 16, 0, kLoadStreamAux);
+    for (int u = 0; u < U; ++u) a[u] = __builtin_amdgcn_raw_buffer_load_b128(r, lane_off + u * STRIDE * 16, 0, AUX);
 }
 
 // Folds the last batch: the lane's vectors at or past `count` (counted from
@@ -178,9 +178,9 @@ __device__ __forceinline__ void fold_last(float& m, float& s, const u32x4 (&a)[U
 // flight and each lane keeps 2U loads outstanding while it computes.  The
 // sched_barrier after each issue keeps the scheduler from moving the fold
 // (and its wait) above the new loads; the uniform trip count keeps every
-// branch scalar.
+// branch scalar.  AUX is the loads' cache policy.
 
-template <typename T, bool ROBUST, int STRIDE, int U>
+template <typename T, bool ROBUST, int STRIDE, int U, int AUX = kLoadStreamAux>
 __device__ __forceinline__ void fold_body(float& m, float& s, const char* base, int64_t region, int lane_off, int l,
                                           int64_t end, int64_t trips) {
     constexpr int64_t STEP = (int64_t)U * STRIDE;
@@ -190,7 +190,7 @@ __device__ __forceinline__ void fold_body(float& m, float& s, const char* base, 
     if (trips <= 0) return;
     const int64_t count = end - (trips - 1) * STEP;
     u32x4 a[U], c[U];
-    load_batch<STRIDE, U>(a, base, region, lane_off, 0);
+    load_batch<STRIDE, U, AUX>(a, base, region, lane_off, 0);
     __builtin_amdgcn_sched_barrier(0);
     if (trips == 1) {
         fold_last<T, STRIDE, U>(m, s, a, l, count);
@@ -198,7 +198,7 @@ __device__ __forceinline__ void fold_body(float& m, float& s, const char* base, 
     }
     int64_t t = 1;  // batches issued
     while (true) {
-        load_batch<STRIDE, U>(c, base, region, lane_off, t);
+        load_batch<STRIDE, U, AUX>(c, base, region, lane_off, t);
         __builtin_amdgcn_sched_barrier(0);
         fold_raw<T, ROBUST, U>(m, s, a);
         if (t == trips - 1) {
@@ -206,7 +206,7 @@ __device__ __forceinline__ void fold_body(float& m, float& s, const char* base, 
             return;
         }
         ++t;
-        load_batch<STRIDE, U>(a, base, region, lane_off, t);
+        load_batch<STRIDE, U, AUX>(a, base, region, lane_off, t);
         __builtin_amdgcn_sched_barrier(0);
         fold_raw<T, ROBUST, U>(m, s, c);
         if (t == trips - 1) {
@@ -258,10 +258,12 @@ struct SelectOut {
     }
 };
 
-// One block per row (grid-stride over rows).
-template <typename T, bool ROBUST, int THREADS, int U, bool PIPE, typename OUT>
+// One block per row (grid-stride over rows).  KEEP: rows below keep_rows load
+// with kLoadKeepAux instead of nt, for a backward that reads x next (a
+// separate instantiation, so the other kernels are unchanged).
+template <typename T, bool ROBUST, int THREADS, int U, bool PIPE, typename OUT, bool KEEP = false>
 __global__ __launch_bounds__(THREADS) void lse_fwd_block_rows(const T* __restrict__ x, OUT out, int64_t B,
-                                                              int64_t N) {
+                                                              int64_t N, int64_t keep_rows) {
     constexpr int VE = Elem<T>::kVec;
     constexpr int WAVES = THREADS / 64;
     __shared__ float sh_m[WAVES], sh_s[WAVES];
@@ -274,7 +276,15 @@ __global__ __launch_bounds__(THREADS) void lse_fwd_block_rows(const T* __restric
         float m = -kInf, s = 0.0f;
         if (tid < sp.head) fold_scalar<T, ROBUST>(m, s, p + tid);
         if (tid < sp.tail) fold_scalar<T, ROBUST>(m, s, p + sp.head + sp.nvec * VE + tid);
-        if constexpr (PIPE)
+        if constexpr (PIPE && KEEP) {
+            if (row < keep_rows)
+                fold_body<T, ROBUST, THREADS, U, kLoadKeepAux>(m, s, reinterpret_cast<const char*>(p + sp.head),
+                                                               sp.nvec * 16, tid * 16, tid, sp.nvec,
+                                                               batches<(int64_t)U * THREADS>(sp.nvec));
+            else
+                fold_body<T, ROBUST, THREADS, U>(m, s, reinterpret_cast<const char*>(p + sp.head), sp.nvec * 16,
+                                                 tid * 16, tid, sp.nvec, batches<(int64_t)U * THREADS>(sp.nvec));
+        } else if constexpr (PIPE)
             fold_body<T, ROBUST, THREADS, U>(m, s, reinterpret_cast<const char*>(p + sp.head), sp.nvec * 16, tid * 16,
                                              tid, sp.nvec, batches<(int64_t)U * THREADS>(sp.nvec));
         else
@@ -498,9 +508,14 @@ static void launch_group(const T* x, OUT out, int64_t B, int64_t N, hipStream_t 
 }
 
 template <typename T, bool ROBUST, int THREADS, int U, bool PIPE, typename OUT>
-static void launch_block(const T* x, OUT out, int64_t B, int64_t N, hipStream_t st) {
+static void launch_block(const T* x, OUT out, int64_t B, int64_t N, hipStream_t st, int64_t keep_rows) {
     const int64_t grid = B < ((int64_t)1 << 30) ? B : ((int64_t)1 << 30);
-    lse_fwd_block_rows<T, ROBUST, THREADS, U, PIPE, OUT><<<dim3((unsigned)grid), dim3(THREADS), 0, st>>>(x, out, B, N);
+    if (keep_rows > 0)
+        lse_fwd_block_rows<T, ROBUST, THREADS, U, PIPE, OUT, true>
+            <<<dim3((unsigned)grid), dim3(THREADS), 0, st>>>(x, out, B, N, keep_rows);
+    else
+        lse_fwd_block_rows<T, ROBUST, THREADS, U, PIPE, OUT>
+            <<<dim3((unsigned)grid), dim3(THREADS), 0, st>>>(x, out, B, N, 0);
 }
 
 // Geometry and loop per shape ("vectors" = 16-byte vectors per row), from
@@ -509,8 +524,10 @@ static void launch_block(const T* x, OUT out, int64_t B, int64_t N, hipStream_t 
 // than a few hundred vectors long: for fp16 / bf16, whose fold costs twice
 // the ALU work per byte, by 3-10% on many rows and by up to 39% on few
 // mid-length rows.  Short rows keep the burst loop, 2-10% ahead there.
+// keep_rows > 0: the one-block-per-row launches load rows below it with
+// kLoadKeepAux (the row-group launches keep nt).
 template <typename T, bool ROBUST, typename OUT>
-static void launch_fwd(const T* x, OUT out, int64_t B, int64_t N, hipStream_t st) {
+static void launch_fwd(const T* x, OUT out, int64_t B, int64_t N, hipStream_t st, int64_t keep_rows) {
     constexpr int VE = Elem<T>::kVec;
     constexpr bool kHalf = VE == 8;
     const int64_t vecs = (N + VE - 1) / VE;
@@ -522,13 +539,13 @@ static void launch_fwd(const T* x, OUT out, int64_t B, int64_t N, hipStream_t st
         // (best from 768 to 8184 rows, 1.5-4% ahead of 256 x 2 at 1024 and
         // of the burst loop at (2046, 256128) and (8184, 50257)).
         if constexpr (kHalf)
-            launch_block<T, ROBUST, 512, 4, true, OUT>(x, out, B, N, st);
+            launch_block<T, ROBUST, 512, 4, true, OUT>(x, out, B, N, st, keep_rows);
         else if (B < 512)
-            launch_block<T, ROBUST, 512, 2, true, OUT>(x, out, B, N, st);
+            launch_block<T, ROBUST, 512, 2, true, OUT>(x, out, B, N, st, keep_rows);
         else if (B < 768)
-            launch_block<T, ROBUST, 256, 2, true, OUT>(x, out, B, N, st);
+            launch_block<T, ROBUST, 256, 2, true, OUT>(x, out, B, N, st, keep_rows);
         else
-            launch_block<T, ROBUST, 1024, 1, true, OUT>(x, out, B, N, st);
+            launch_block<T, ROBUST, 1024, 1, true, OUT>(x, out, B, N, st, keep_rows);
         return;
     }
     if (vecs > 1024 && B <= 1024) {
@@ -536,9 +553,9 @@ static void launch_fwd(const T* x, OUT out, int64_t B, int64_t N, hipStream_t st
         // under-filled, so one block per row; 128 threads for fp16/bf16 up
         // to 2048 vectors (2-8% ahead of 256), 256 otherwise.
         if (kHalf && vecs <= 2048)
-            launch_block<T, ROBUST, 128, 2, true, OUT>(x, out, B, N, st);
+            launch_block<T, ROBUST, 128, 2, true, OUT>(x, out, B, N, st, keep_rows);
         else
-            launch_block<T, ROBUST, 256, 2, true, OUT>(x, out, B, N, st);
+            launch_block<T, ROBUST, 256, 2, true, OUT>(x, out, B, N, st, keep_rows);
         return;
     }
     if (vecs > 512) {
@@ -550,9 +567,9 @@ static void launch_fwd(const T* x, OUT out, int64_t B, int64_t N, hipStream_t st
         // 19% at 3000 vectors); 32 lanes per row for 1025..2048 vectors (3%
         // ahead at 2000); otherwise a wave per row.
         if constexpr (!kHalf)
-            launch_block<T, ROBUST, 256, 2, true, OUT>(x, out, B, N, st);
+            launch_block<T, ROBUST, 256, 2, true, OUT>(x, out, B, N, st, keep_rows);
         else if (vecs > 2048 && B >= 4096)
-            launch_block<T, ROBUST, 256, 4, true, OUT>(x, out, B, N, st);
+            launch_block<T, ROBUST, 256, 4, true, OUT>(x, out, B, N, st, keep_rows);
         else if (vecs > 1024 && vecs <= 2048)
             launch_group<T, ROBUST, 32, 4, true, OUT>(x, out, B, N, st);
         else
@@ -582,9 +599,26 @@ static void launch_fwd(const T* x, OUT out, int64_t B, int64_t N, hipStream_t st
 // kernels where default_split_plan() chooses them, with ws_bytes checked
 // against what that plan needs.  Argument checks other than x's are the
 // caller's.
+// Rows the keeping forward loads with kLoadKeepAux: the first three quarters
+// of x, at most 240 MiB.  Same-process sweeps of the forward then the backward
+// on the same batch (backward after the keeping forward, against after the nt
+// forward): fp32 (512, 128256) 123.8 -> 118.6 us with 384 of 512 rows (all
+// 512: 120.7, the forward alone 11% slower), fp32 (256, 128256) 67.1 ->
+// 64.1 us with 192 of 256, bf16 (2048, 128256) 238.6 -> 232.8 us with 1024 of
+// 2048 (250 MiB; 1536 rows: 235.5).  The backward's gain grows with the rows
+// kept, the forward's cost faster beyond about three quarters of x.
+constexpr int64_t kKeepMaxBytes = (int64_t)240 << 20;
+
+static int64_t keep_rows_for(int64_t B, int64_t row_bytes) {
+    if (row_bytes <= 0) return 0;
+    int64_t budget = B * row_bytes / 4 * 3;
+    if (budget > kKeepMaxBytes) budget = kKeepMaxBytes;
+    return budget / row_bytes;
+}
+
 template <typename T, typename OUT>
 static int fwd_launch(const char* name, const T* x, OUT out, int64_t B, int64_t N, int robust, void* ws,
-                      size_t ws_bytes, hipStream_t st) {
+                      size_t ws_bytes, hipStream_t st, bool keep = false) {
     FL_CHECK(x != nullptr || N == 0, "%s: x is NULL", name);
     FL_CHECK((reinterpret_cast<uintptr_t>(x) % sizeof(T)) == 0, "%s: x is not element-aligned", name);
     const SplitPlan pl = ws ? default_split_plan(B, N, (int64_t)sizeof(T)) : SplitPlan{1, 0};
@@ -597,21 +631,24 @@ static int fwd_launch(const char* name, const T* x, OUT out, int64_t B, int64_t 
             launch_split<T, true, kSplitThreads, kSplitU>(x, out, B, N, pl, ws, st);
         else
             launch_split<T, false, kSplitThreads, kSplitU>(x, out, B, N, pl, ws, st);
-    } else if (robust) {
-        launch_fwd<T, true>(x, out, B, N, st);
     } else {
-        launch_fwd<T, false>(x, out, B, N, st);
+        const int64_t keep_rows = keep ? keep_rows_for(B, N * (int64_t)sizeof(T)) : 0;
+        if (robust)
+            launch_fwd<T, true>(x, out, B, N, st, keep_rows);
+        else
+            launch_fwd<T, false>(x, out, B, N, st, keep_rows);
     }
     return launch_status(name);
 }
 
 template <typename T>
 static int fwd_entry(const char* name, const T* x, float* out, int64_t B, int64_t N, int robust, void* ws,
-                     size_t ws_bytes, void* stream) {
+                     size_t ws_bytes, void* stream, bool keep = false) {
     FL_CHECK(B >= 0 && N >= 0, "%s: negative shape (B=%lld, N=%lld)", name, (long long)B, (long long)N);
     if (B == 0) return ok();
     FL_CHECK(out != nullptr, "%s: out is NULL", name);
-    return fwd_launch<T>(name, x, LseOut{out}, B, N, robust, ws, ws_bytes, reinterpret_cast<hipStream_t>(stream));
+    return fwd_launch<T>(name, x, LseOut{out}, B, N, robust, ws, ws_bytes, reinterpret_cast<hipStream_t>(stream),
+                         keep);
 }
 
 // ---------------------------------------------------------------------------
@@ -954,6 +991,20 @@ extern "C" int fl_lse_fwd_f16(const void* x, float* out, int64_t B, int64_t N, i
 extern "C" int fl_lse_fwd_bf16(const void* x, float* out, int64_t B, int64_t N, int robust, void* stream) {
     return fwd_entry<bf16_t>("fl_lse_fwd_bf16", static_cast<const bf16_t*>(x), out, B, N, robust, nullptr, 0,
                              stream);
+}
+
+extern "C" int fl_lse_fwd_f32_keep(const float* x, float* out, int64_t B, int64_t N, int robust, void* stream) {
+    return fwd_entry<float>("fl_lse_fwd_f32_keep", x, out, B, N, robust, nullptr, 0, stream, true);
+}
+
+extern "C" int fl_lse_fwd_f16_keep(const void* x, float* out, int64_t B, int64_t N, int robust, void* stream) {
+    return fwd_entry<_Float16>("fl_lse_fwd_f16_keep", static_cast<const _Float16*>(x), out, B, N, robust, nullptr,
+                               0, stream, true);
+}
+
+extern "C" int fl_lse_fwd_bf16_keep(const void* x, float* out, int64_t B, int64_t N, int robust, void* stream) {
+    return fwd_entry<bf16_t>("fl_lse_fwd_bf16_keep", static_cast<const bf16_t*>(x), out, B, N, robust, nullptr, 0,
+                             stream, true);
 }
 
 extern "C" size_t fl_lse_fwd_workspace_bytes(int64_t B, int64_t N, int elem_bytes) {

@@ -85,9 +85,11 @@ def _workspace_bytes(B: int, N: int, elem_bytes: int) -> int:
     return nbytes
 
 
-def _launch_fwd(entry: str, x: torch.Tensor, out: torch.Tensor, elem_bytes: int, robust: bool) -> None:
-    """One-pass kernels, or the split-row kernels (entry + "_ws") for few long
-    rows, where the library asks for a workspace."""
+def _launch_fwd(entry: str, x: torch.Tensor, out: torch.Tensor, elem_bytes: int, robust: bool,
+                keep: bool = False) -> None:
+    """One-pass kernels (entry + "_keep" with keep: x partly left in the
+    Infinity Cache for the backward), or the split-row kernels (entry +
+    "_ws") for few long rows, where the library asks for a workspace."""
     B, N = x.shape
     with _on_device(x):
         nbytes = _workspace_bytes(B, N, elem_bytes)
@@ -98,10 +100,11 @@ def _launch_fwd(entry: str, x: torch.Tensor, out: torch.Tensor, elem_bytes: int,
             _lib.call(entry + "_ws", x.data_ptr(), out.data_ptr(), B, N, int(robust), ws.data_ptr(), ws.numel(),
                       _stream(x))
         else:
-            _lib.call(entry, x.data_ptr(), out.data_ptr(), B, N, int(robust), _stream(x))
+            _lib.call(entry + "_keep" if keep else entry, x.data_ptr(), out.data_ptr(), B, N, int(robust),
+                      _stream(x))
 
 
-def _fwd_f32(x: torch.Tensor, robust: bool) -> torch.Tensor:
+def _fwd_f32(x: torch.Tensor, robust: bool, keep: bool = False) -> torch.Tensor:
     # fused_fp32_kernel.cu:155-158 / :176-179
     _check(x.is_cuda, "x must be CUDA")
     _check(x.dtype == torch.float32, "x must be float32")
@@ -111,7 +114,7 @@ def _fwd_f32(x: torch.Tensor, robust: bool) -> torch.Tensor:
     out = torch.empty((B,), dtype=torch.float32, device=x.device)
     if B == 0:
         return out
-    _launch_fwd("fl_lse_fwd_f32", x, out, 4, robust)
+    _launch_fwd("fl_lse_fwd_f32", x, out, 4, robust, keep)
     return out
 
 
@@ -124,6 +127,19 @@ def onepass_lse_float(x: torch.Tensor) -> torch.Tensor:
 def onepass_lse_float_robust(x: torch.Tensor) -> torch.Tensor:
     """Row LSE with -inf/+inf/NaN semantics (fused_fp32_kernel.cu:175-194)."""
     return _fwd_f32(x, robust=True)
+
+
+def onepass_lse_float_keep(x: torch.Tensor) -> torch.Tensor:
+    """onepass_lse_float for a backward that reads x next: the same result,
+    with part of x left in the Infinity Cache for that read
+    (fl_lse_fwd_f32_keep; no reference counterpart)."""
+    return _fwd_f32(x, robust=False, keep=True)
+
+
+def onepass_lse_float_robust_keep(x: torch.Tensor) -> torch.Tensor:
+    """onepass_lse_float_robust for a backward that reads x next
+    (fl_lse_fwd_f32_keep; no reference counterpart)."""
+    return _fwd_f32(x, robust=True, keep=True)
 
 
 def onepass_lse_float_backward(grad_output: torch.Tensor, x: torch.Tensor, lse_output: torch.Tensor) -> torch.Tensor:
@@ -225,7 +241,8 @@ def selective_log_softmax_float_backward(grad_output: torch.Tensor, logits: torc
     return grad
 
 
-def _fwd_half(x: torch.Tensor, dtype: torch.dtype, entry: str, dtype_msg: str, robust: bool) -> torch.Tensor:
+def _fwd_half(x: torch.Tensor, dtype: torch.dtype, entry: str, dtype_msg: str, robust: bool,
+              keep: bool = False) -> torch.Tensor:
     # fused_fp16_kernel.cu:113-116
     _check(x.dim() == 2, "Expected 2-D tensor (B, N)")
     _check(x.is_cuda and x.dtype == dtype, dtype_msg)
@@ -234,7 +251,7 @@ def _fwd_half(x: torch.Tensor, dtype: torch.dtype, entry: str, dtype_msg: str, r
     out = torch.empty((B,), dtype=torch.float32, device=x.device)
     if B == 0:
         return out
-    _launch_fwd(entry, x, out, 2, robust)
+    _launch_fwd(entry, x, out, 2, robust, keep)
     return out
 
 
@@ -276,6 +293,18 @@ def batched_logsumexp_bf16(x: torch.Tensor, robust: bool = False) -> torch.Tenso
     """bf16 (B, N) -> fp32 (B,) LSE with fp32 accumulation (no reference
     counterpart; the fp16 entry's contract with bf16 storage)."""
     return _fwd_half(x, torch.bfloat16, "fl_lse_fwd_bf16", "Input must be CUDA bf16", robust)
+
+
+def batched_logsumexp_fp16_keep(x: torch.Tensor, robust: bool = False) -> torch.Tensor:
+    """batched_logsumexp_fp16 for a backward that reads x next
+    (fl_lse_fwd_f16_keep; no reference counterpart)."""
+    return _fwd_half(x, torch.float16, "fl_lse_fwd_f16", "Input must be CUDA fp16", robust, keep=True)
+
+
+def batched_logsumexp_bf16_keep(x: torch.Tensor, robust: bool = False) -> torch.Tensor:
+    """batched_logsumexp_bf16 for a backward that reads x next
+    (fl_lse_fwd_bf16_keep; no reference counterpart)."""
+    return _fwd_half(x, torch.bfloat16, "fl_lse_fwd_bf16", "Input must be CUDA bf16", robust, keep=True)
 
 
 # ---------------------------------------------------------------------------

@@ -80,6 +80,23 @@ int fl_lse_fwd_f16(const void* x, float* out, int64_t B, int64_t N, int robust, 
 int fl_lse_fwd_bf16(const void* x, float* out, int64_t B, int64_t N, int robust, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Forward for a backward that follows: the arguments, kernels and results of
+ * fl_lse_fwd_f32 / _f16 / _bf16 (bit-identical), but the long-row kernels
+ * load the first three quarters of x (at most 240 MiB) without the
+ * nontemporal hint, so part of x stays in the Infinity Cache (MI355X's 256 MB
+ * memory-side cache) for the backward's read of the same rows.  For
+ * training, where the backward (fl_lse_bwd_*) runs next on the same x: the
+ * pair takes 2-4% less time at (512, 128256) fp32, (256, 128256) fp32 and
+ * (2048, 128256) bf16, while this forward alone takes 2-5% more than
+ * fl_lse_fwd_*.  No counterpart in the reference (whose autograd forward
+ * calls onepass_lse_float_robust, fused_fp32_kernel.cu:175); the drop-in
+ * logsumexp uses it when autograd will run the backward.
+ * ------------------------------------------------------------------------- */
+int fl_lse_fwd_f32_keep(const float* x, float* out, int64_t B, int64_t N, int robust, void* stream);
+int fl_lse_fwd_f16_keep(const void* x, float* out, int64_t B, int64_t N, int robust, void* stream);
+int fl_lse_fwd_bf16_keep(const void* x, float* out, int64_t B, int64_t N, int robust, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Half-precision backward: grad_x[r, i] = grad[r] * exp(x[r, i] - lse[r]),
  * computed in fp32 and rounded to nearest even into the input type.  grad
  * and lse are fp32 [B] (lse as the half forward above returns it), x and

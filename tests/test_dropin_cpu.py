@@ -150,6 +150,60 @@ def test_no_grad_uses_direct_path():
     assert [c[0] for c in ext.calls] == ["fwd_robust"]
 
 
+class FakeKeepExt(FakeExt):
+    """An ext with the keeping forwards (this package's has them)."""
+
+    def onepass_lse_float_keep(self, x):
+        self._rec("fwd_keep", x)
+        return torch.logsumexp(x.as_subclass(torch.Tensor), -1).as_subclass(FakeCuda)
+
+    def onepass_lse_float_robust_keep(self, x):
+        self._rec("fwd_robust_keep", x)
+        return torch.logsumexp(x.as_subclass(torch.Tensor), -1).as_subclass(FakeCuda)
+
+    def batched_logsumexp_fp16_keep(self, x, robust=False):
+        self._rec("fwd_fp16_keep", x)
+        return torch.logsumexp(x.as_subclass(torch.Tensor).float(), -1).as_subclass(FakeCuda)
+
+    def batched_logsumexp_bf16_keep(self, x, robust=False):
+        self._rec("fwd_bf16_keep", x)
+        return torch.logsumexp(x.as_subclass(torch.Tensor).float(), -1).as_subclass(FakeCuda)
+
+
+@pytest.mark.parametrize("robust", [True, False])
+def test_autograd_forward_keeps_x_for_the_backward(robust):
+    """With grad the forward is the keeping variant, where the ext has one;
+    without grad (nothing reads x again) it is the plain forward.  An ext
+    without the keeping variants (the reference's) gets the plain forward
+    both ways."""
+    ext = FakeKeepExt()
+    lse = make_fuselse_logsumexp(ext, robust=robust)
+    x = torch.randn(4, 7, requires_grad=True)
+    y = lse(fake(x))
+    y.as_subclass(torch.Tensor).sum().backward()
+    assert [c[0] for c in ext.calls] == ["fwd_robust_keep" if robust else "fwd_keep", "bwd"]
+    ext.calls.clear()
+    with torch.no_grad():
+        lse(fake(x))
+    lse(fake(x.detach()))
+    assert [c[0] for c in ext.calls] == ["fwd_robust" if robust else "fwd"] * 2
+    plain = FakeExt()
+    y = make_fuselse_logsumexp(plain, robust=robust)(fake(x))
+    y.as_subclass(torch.Tensor).sum().backward()
+    assert [c[0] for c in plain.calls] == ["fwd_robust" if robust else "fwd", "bwd"]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_half_autograd_forward_keeps_x(dtype):
+    ext = FakeKeepExt()
+    lse = make_fuselse_logsumexp(ext, half_inputs=True)
+    x = torch.randn(3, 9).to(dtype).requires_grad_(True)
+    y = lse(fake(x))
+    y.as_subclass(torch.Tensor).float().sum().backward()
+    tag = "fwd_fp16_keep" if dtype == torch.float16 else "fwd_bf16_keep"
+    assert [c[0] for c in ext.calls] == [tag, "bwd_half"]
+
+
 # ---------------------------------------------------------------------------
 # make_selective_log_softmax (trl.trainer.utils.selective_log_softmax drop-in)
 # ---------------------------------------------------------------------------

@@ -582,9 +582,9 @@ def test_fwd_pipelined_batch_boundaries(cuda, dtype, label, B, vecs, step):
     entry = {torch.float32: "fl_lse_fwd_f32", torch.float16: "fl_lse_fwd_f16",
              torch.bfloat16: "fl_lse_fwd_bf16"}[dtype]
 
-    def one_pass(xd, robust):
+    def one_pass(xd, robust, name=entry):
         out = torch.empty(xd.shape[0], device=xd.device)
-        _lib.call(entry, xd.data_ptr(), out.data_ptr(), xd.shape[0], xd.shape[1], int(robust),
+        _lib.call(name, xd.data_ptr(), out.data_ptr(), xd.shape[0], xd.shape[1], int(robust),
                   torch.cuda.current_stream().cuda_stream)
         return out
 
@@ -606,6 +606,8 @@ def test_fwd_pipelined_batch_boundaries(cuda, dtype, label, B, vecs, step):
             for robust in (False, True):
                 got = one_pass(xd, robust)
                 _close(got.cpu().numpy(), want, RTOL32 if dtype == torch.float32 else RTOL16, atol=1e-6)
+                # the keeping forward: same kernels but for the loads' cache policy
+                assert torch.equal(one_pass(xd, robust, entry + "_keep"), got)
                 if lib.fl_lse_fwd_workspace_bytes(B, N, esize) == 0:
                     if dtype == torch.float32:
                         named = (ext.onepass_lse_float_robust if robust else ext.onepass_lse_float)(xd)
@@ -650,3 +652,43 @@ def test_rows_of_zero_and_one_elements(cuda):
             torch.testing.assert_close(lse_s, x[:, 0], rtol=1e-6, atol=1e-6)
             gs = ext.selective_log_softmax_float_backward(g, x, idx, lse_s)
             torch.testing.assert_close(gs, torch.zeros_like(gs), rtol=0.0, atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype,B,N", [(torch.float32, 512, 128256), (torch.float32, 256, 128256),
+                                       (torch.float32, 1024, 20000), (torch.float32, 700, 3001),
+                                       (torch.float32, 4096, 1000), (torch.bfloat16, 2048, 128256),
+                                       (torch.float16, 4096, 32000), (torch.float16, 64, 3000)])
+def test_fwd_keep_bit_identical(cuda, dtype, B, N):
+    """fl_lse_fwd_*_keep (rows below the kept-row count load without the
+    nontemporal hint) gives the bits of fl_lse_fwd_* on both sides of that
+    count, robust on the BASELINE robust set and plain on finite rows, at
+    C2, the bf16 C3 shape and the other one-block-per-row geometries (and a
+    row-group shape, where the entries run the same kernel)."""
+    from fuselse_amd import _lib
+
+    print(f"case fwd_keep {dtype} B={B} N={N}", flush=True)
+    entry = {torch.float32: "fl_lse_fwd_f32", torch.float16: "fl_lse_fwd_f16",
+             torch.bfloat16: "fl_lse_fwd_bf16"}[dtype]
+    finite = O.make_c2_input(B, N, seed=B + N)
+    special = O.make_robust_rows(finite, seed=7)
+    st = torch.cuda.current_stream().cuda_stream
+    for data, robust in ((finite, False), (finite, True), (special, True)):
+        xd = torch.from_numpy(data).to(cuda).to(dtype)
+        outs = []
+        for name in (entry, entry + "_keep"):
+            out = torch.empty(B, device=cuda)
+            _lib.call(name, xd.data_ptr(), out.data_ptr(), B, N, int(robust), st)
+            outs.append(out)
+        torch.testing.assert_close(outs[1], outs[0], rtol=0, atol=0, equal_nan=True)
+        if data is special:
+            got = outs[1].cpu().numpy()
+            assert np.isneginf(got[0]) and np.isposinf(got[1]) and np.isnan(got[2]) and np.isposinf(got[3])
+    ext = _ext()
+    xd = torch.from_numpy(finite).to(cuda).to(dtype)
+    if dtype == torch.float32:
+        assert torch.equal(ext.onepass_lse_float_robust_keep(xd), ext.onepass_lse_float_robust(xd))
+        assert torch.equal(ext.onepass_lse_float_keep(xd), ext.onepass_lse_float(xd))
+    else:
+        f, fk = ((ext.batched_logsumexp_fp16, ext.batched_logsumexp_fp16_keep) if dtype == torch.float16
+                 else (ext.batched_logsumexp_bf16, ext.batched_logsumexp_bf16_keep))
+        assert torch.equal(fk(xd, robust=True), f(xd, robust=True))
