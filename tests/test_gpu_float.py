@@ -336,6 +336,33 @@ def test_dropin_autograd_matches_torch(cuda):
         assert lse(torch.empty(0, 8, device=cuda), -1).shape == (0,)
 
 
+@pytest.mark.parametrize("B,N", [(512, 128256), (1024, 20000)])
+def test_dropin_autograd_keeping_forward_at_size(cuda, B, N):
+    """Under autograd the drop-in's forward is the keeping variant; at C2
+    (256-thread blocks) and at 1024 rows of 20000 (1024-thread blocks), where
+    it keeps part of x for the backward, the forward and the gradient equal
+    the plain ext calls bit for bit, and the gradient's first 64 rows match
+    fp64."""
+    import fuselse_amd
+
+    print(f"case dropin autograd keep B={B} N={N}", flush=True)
+    ext = fuselse_amd.ext
+    x = O.make_c2_input(B, N, seed=11)
+    g = np.random.default_rng(12).standard_normal(B).astype(np.float32)
+    xd = torch.from_numpy(x).to(cuda)
+    gd = torch.from_numpy(g).to(cuda)
+    lse = fuselse_amd.make_fuselse_logsumexp(ext, robust=True)
+    a = xd.clone().requires_grad_(True)
+    y = lse(a, dim=-1)
+    y.backward(gd)
+    want_lse = ext.onepass_lse_float_robust(xd)
+    assert torch.equal(y.detach(), want_lse)
+    assert torch.equal(a.grad, ext.onepass_lse_float_backward(gd, xd, want_lse))
+    rows = slice(0, 64)
+    np.testing.assert_allclose(a.grad[rows].cpu().numpy(), O.lse_bwd_fp64(g[rows], x[rows], O.lse_fp64(x[rows])),
+                               rtol=RTOL32, atol=1e-30)
+
+
 def test_dropin_is_native(cuda):
     """The GPU drop-in path runs the native library (it is loaded in-process)."""
     import fuselse_amd
