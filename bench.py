@@ -314,6 +314,18 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
                     ms = _time_calls(torch, stream,
                                      lambda i: ext.onepass_lse_half_backward(gsv, bufs[i % nb], lses[i % nb]), nb, iters)
                     rec(f"C3_{tag}_bwd_{b}x{n}", ms, 4 * b * n + 8 * b)
+                    # forward then backward on the same batch, as autograd runs
+                    # them: the keeping forward (the drop-in's choice there)
+                    # against the nt forward
+                    fk = ext.batched_logsumexp_fp16_keep if dt == torch.float16 else ext.batched_logsumexp_bf16_keep
+
+                    def pair(i, f):
+                        x = bufs[i % nb]
+                        ext.onepass_lse_half_backward(gsv, x, f(x))
+
+                    ms_nt = _time_calls(torch, stream, lambda i: pair(i, fn), nb, iters)
+                    ms_keep = _time_calls(torch, stream, lambda i: pair(i, fk), nb, iters)
+                    rec(f"C3_{tag}_step_{b}x{n}", ms_keep, 6 * b * n + 12 * b, nt_forward_us=round(ms_nt * 1e3, 2))
                 del bufs
     if want("split"):
         # Few long rows (fp32, robust): the split-row path (fl_lse_fwd_f32_ws, the
