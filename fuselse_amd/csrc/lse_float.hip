@@ -595,10 +595,6 @@ static void launch_fwd(const T* x, OUT out, int64_t B, int64_t N, hipStream_t st
     }
 }
 
-// ws == nullptr: the one-pass kernels for every shape.  Otherwise the split
-// kernels where default_split_plan() chooses them, with ws_bytes checked
-// against what that plan needs.  Argument checks other than x's are the
-// caller's.
 // Rows the keeping forward loads with kLoadKeepAux: the first three quarters
 // of x, at most 240 MiB.  Same-process sweeps of the forward then the backward
 // on the same batch (backward after the keeping forward, against after the nt
@@ -616,6 +612,11 @@ static int64_t keep_rows_for(int64_t B, int64_t row_bytes) {
     return budget / row_bytes;
 }
 
+// ws == nullptr: the one-pass kernels for every shape.  Otherwise the split
+// kernels where default_split_plan() chooses them, with ws_bytes checked
+// against what that plan needs.  keep: the one-pass kernels load the rows
+// keep_rows_for() gives with kLoadKeepAux (the split kernels ignore it).
+// Argument checks other than x's are the caller's.
 template <typename T, typename OUT>
 static int fwd_launch(const char* name, const T* x, OUT out, int64_t B, int64_t N, int robust, void* ws,
                       size_t ws_bytes, hipStream_t st, bool keep = false) {
