@@ -6,12 +6,16 @@ One step = one robust forward (lse = onepass_lse_float_robust(x)) and one
 fused backward (grad_x = onepass_lse_float_backward(g, x, lse)) over full
 (512, 128256) batches, through the same extension functions the drop-in uses.
 The backward of step i runs on batch i-1, so no kernel re-reads the buffer the
-kernel before it just streamed.  Inputs are resident in HBM before the timed
-region; three input buffers (3 x 263 MB) and four output buffers rotate so the
-working set exceeds twice the 256 MB Infinity Cache and the numbers are HBM
-numbers.  The step time comes from HIP events at both ends of the timed region;
+kernel before it just streamed: every launch reads HBM, and `value`,
+`hbm_gbps` and `pct_hbm_peak` are HBM figures.  Inputs are resident in HBM
+before the timed region; four input buffers (4 x 263 MB) and four output
+buffers rotate so the working set exceeds twice the 256 MB Infinity Cache.
+The step time comes from HIP events at both ends of the timed region;
 per-kernel average durations (the roofline figures) from K back-to-back
 launches of each kernel with HIP events on the stream the kernels run on.
+Beside it, `step` holds the same pair in autograd's order (the backward on the
+batch its forward just read), with the nt forward and with the keeping
+forward, each also with 512 MB of other traffic between the two.
 
 Prints ONE JSON line on stdout; progress goes to stderr.
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
@@ -58,9 +62,10 @@ def cpu_baseline(max_rows=512):
     benchmark.py:36-44), at all cores.  Also reports: the port and
     torch.logsumexp fwd+bwd at 1 thread (64-row sample, scaled); the C1 shapes
     (32, 256) and (200, 1000) forward at 1 thread and all cores; torch's
-    fwd+bwd at all cores; when it was built, the reference's own AVX2 IntLSE
-    (single thread as in the reference, 32 rows, also scaled to B); the
-    affinity core count and the CPU model."""
+    fwd+bwd at all cores; the repo's C restatement of the reference's AVX2
+    IntLSE (single thread as in the reference, 32 rows, also scaled to B); the
+    affinity core count and the CPU model.  No reference code runs here: every
+    CPU path timed is torch or this repo's own C port."""
     import numpy as np
     import torch
 
@@ -146,11 +151,17 @@ def cpu_baseline(max_rows=512):
         torch.set_num_threads(cores)
     except Exception as e:  # pragma: no cover - reported, not fatal
         extra["torch_cpu_error"] = repr(e)
-    if O.ref_available():
-        x32 = np.ascontiguousarray(x[:32])
-        t32 = med(lambda: O.ref_intlse_cpu_rows(x32, True), 1, 3)
-        extra["intlse_avx2_ref_fwd_ms_1thread_32rows"] = round(t32, 3)
-        extra["intlse_avx2_ref_fwd_ms_1thread_scaled_to_B"] = round(t32 * B / 32, 3)
+    # IntLSE-AVX2 (lse_kernel_simd.c), the repo's bit-pinned C restatement,
+    # single-threaded as the reference runs it (lse_kernel_simd.c:232-236), on a
+    # 32-row sample scaled to B
+    x32 = np.ascontiguousarray(x[:32])
+    O.set_omp_threads(1)
+    try:
+        t32 = med(lambda: O.intlse_cpu_rows(x32, True), 1, 3)
+    finally:
+        O.set_omp_threads(cores)
+    extra["intlse_avx2_port_fwd_ms_1thread_32rows"] = round(t32, 3)
+    extra["intlse_avx2_port_fwd_ms_1thread_scaled_to_B"] = round(t32 * B / 32, 3)
     cpu = ""
     try:
         for ln in open("/proc/cpuinfo"):
@@ -185,9 +196,18 @@ def _time_calls(torch, stream, fn, nbuf, iters):
     return a.elapsed_time(b) / iters
 
 
+# The most calls one captured graph may hold.  An uncapped sweep once asked for
+# about 500k captured calls over 125k buffers (a rotation sized for the
+# Infinity Cache at N = 2, where each buffer is 4 KB) and the process died with
+# SIGSEGV during capture; every group now sizes its rotation and call count
+# below this.
+MAX_GRAPH_CALLS = 1024
+
+
 def _time_graph(torch, fn, iters, result):
     """Average per-call duration (ms) of fn(i, stream), i < iters, captured in
     one HIP graph and replayed three times; and result() after the replays."""
+    assert 0 < iters <= MAX_GRAPH_CALLS, f"{iters} captured calls asked for, at most {MAX_GRAPH_CALLS}"
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -729,19 +749,17 @@ def main():
     if args.copy_calib:
         _copy_calibration(torch, dev)
 
-    # A step is one forward and one backward over a full (512, 128256) batch,
-    # in autograd's order: the forward, then the backward on the batch it just
-    # read.  The forward is the one the drop-in runs when autograd will run the
-    # backward (onepass_lse_float_robust_keep): it leaves part of x in the
-    # Infinity Cache, where the backward finds it.  Batches rotate over NBUF
-    # buffers, so each step starts with its x in HBM only (the three steps in
-    # between move about 2 GB through the 256 MB cache).
+    # A step is one forward and one backward over full (512, 128256) batches.
+    # The backward of step i runs on batch i-1 (lse of each batch computed once
+    # here), so every launch streams a buffer that the launch before it did not
+    # touch: all reads come from HBM.  Batches rotate over NBUF buffers.
     ring = [None] * NBUF  # keeps NBUF grad_x outputs alive so outputs rotate too
+    lses = [ext.onepass_lse_float_robust(x) for x in xs]
 
     def step(i):
-        x = xs[i % NBUF]
-        lse = ext.onepass_lse_float_robust_keep(x)
-        ring[i % NBUF] = ext.onepass_lse_float_backward(gs[i % NBUF], x, lse)
+        j = (i - 1) % NBUF
+        ext.onepass_lse_float_robust(xs[i % NBUF])
+        ring[i % NBUF] = ext.onepass_lse_float_backward(gs[j], xs[j], lses[j])
 
     stream = torch.cuda.current_stream(dev)
     for i in range(args.warmup):
@@ -776,7 +794,6 @@ def main():
         torch.cuda.synchronize()
         return a.elapsed_time(b) / K
 
-    lses = [ext.onepass_lse_float_robust(x) for x in xs]
     fwd_ms = per_launch(lambda i: ext.onepass_lse_float_robust(xs[i % NBUF]))
     fwd_plain_ms = per_launch(lambda i: ext.onepass_lse_float(xs[i % NBUF]))
     fwd_keep_ms = per_launch(lambda i: ext.onepass_lse_float_robust_keep(xs[i % NBUF]))
@@ -788,24 +805,31 @@ def main():
     log(f"per launch: fwd {fwd_ms * 1e3:.1f} us (plain {fwd_plain_ms * 1e3:.1f}, keeping x {fwd_keep_ms * 1e3:.1f}), "
         f"bwd {bwd_ms * 1e3:.1f} us")
 
-    # The same step with the nt forward (onepass_lse_float_robust), and with
-    # each backward on the previous step's batch instead, so that no kernel
-    # re-reads what the kernel before it streamed and every launch reads HBM.
-    def same_batch_nt(i):
+    # The same pair in autograd's order, the backward on the batch its forward
+    # just read: with the nt forward (the drop-in's default) and with the
+    # keeping forward (make_fuselse_logsumexp(keep=True)), which leaves part of
+    # x in the Infinity Cache for the backward.  Then each with 512 MB of other
+    # traffic between the forward and its backward (a 256 MB device copy, as the
+    # rest of a training step would stream), which flushes that cache.
+    def same_batch(i, fwd, flush):
         x = xs[i % NBUF]
-        lse = ext.onepass_lse_float_robust(x)
+        lse = fwd(x)
+        if flush:
+            flush_dst.copy_(flush_src)
         ring[i % NBUF] = ext.onepass_lse_float_backward(gs[i % NBUF], x, lse)
 
-    same_batch_nt_ms = per_launch(same_batch_nt)
-
-    def cross_batch(i):
-        j = (i - 1) % NBUF
-        ext.onepass_lse_float_robust(xs[i % NBUF])
-        ring[i % NBUF] = ext.onepass_lse_float_backward(gs[j], xs[j], lses[j])
-
-    cross_batch_ms = per_launch(cross_batch)
-    log(f"step variants: keeping forward {ms_step * 1e3:.1f} us, nt forward {same_batch_nt_ms * 1e3:.1f} us, "
-        f"backward on the previous batch {cross_batch_ms * 1e3:.1f} us")
+    same_batch_nt_ms = per_launch(lambda i: same_batch(i, ext.onepass_lse_float_robust, False))
+    same_batch_keep_ms = per_launch(lambda i: same_batch(i, ext.onepass_lse_float_robust_keep, False))
+    flush_src = torch.empty(64 << 20, dtype=torch.float32, device=dev)
+    flush_dst = torch.empty_like(flush_src)
+    flush_src.normal_()
+    flush_ms = per_launch(lambda i: flush_dst.copy_(flush_src))
+    flushed_nt_ms = per_launch(lambda i: same_batch(i, ext.onepass_lse_float_robust, True))
+    flushed_keep_ms = per_launch(lambda i: same_batch(i, ext.onepass_lse_float_robust_keep, True))
+    del flush_src, flush_dst
+    log(f"step variants: every launch from HBM {ms_step * 1e3:.1f} us; autograd order nt {same_batch_nt_ms * 1e3:.1f}, "
+        f"keeping {same_batch_keep_ms * 1e3:.1f} us; with a 512 MB copy between (copy alone "
+        f"{flush_ms * 1e3:.1f} us) nt {flushed_nt_ms * 1e3:.1f}, keeping {flushed_keep_ms * 1e3:.1f} us")
 
     # Reference streams over the same 263 MB buffers, for the roofline's
     # context: torch's own elementwise read+write (mul with out=) and its
@@ -923,13 +947,18 @@ def main():
                    "robust": True},
         "hbm_gbps": round(gbps, 1),
         "pct_hbm_peak": round(100 * gbps * 1e9 / HBM_PEAK, 2),
-        "step": {"order": "forward (onepass_lse_float_robust_keep), then the backward on the same batch, as autograd "
-                          "runs them; x partly re-read from the Infinity Cache, so hbm_gbps counts algorithmic bytes",
+        "step": {"order": "value: forward of batch i, then the backward of batch i-1, every launch from HBM; "
+                          "autograd_*: the backward right after the forward on the same batch",
                  "us": round(ms_step * 1e3, 2),
-                 "same_batch_nt_forward_us": round(same_batch_nt_ms * 1e3, 2),
-                 "cross_batch_us": round(cross_batch_ms * 1e3, 2),
-                 "cross_batch_pct_peak": round(100 * (FWD_BYTES + BWD_BYTES) / (cross_batch_ms * 1e-3) / HBM_PEAK, 2),
-                 "keep_gain_pct": round(100 * (1 - ms_step / same_batch_nt_ms), 2)},
+                 "autograd_nt_forward_us": round(same_batch_nt_ms * 1e3, 2),
+                 "autograd_keeping_forward_us": round(same_batch_keep_ms * 1e3, 2),
+                 "keep_gain_pct": round(100 * (1 - same_batch_keep_ms / same_batch_nt_ms), 2),
+                 "with_512mb_between": {"copy_alone_us": round(flush_ms * 1e3, 2),
+                                        "nt_forward_step_us": round((flushed_nt_ms - flush_ms) * 1e3, 2),
+                                        "keeping_forward_step_us": round((flushed_keep_ms - flush_ms) * 1e3, 2),
+                                        "nt_total_us": round(flushed_nt_ms * 1e3, 2),
+                                        "keeping_total_us": round(flushed_keep_ms * 1e3, 2),
+                                        "keep_gain_pct": round(100 * (1 - flushed_keep_ms / flushed_nt_ms), 2)}},
         "stream_ceilings": stream_ceilings,
         "fwd": {"us": round(fwd_ms * 1e3, 2), "gbps": round(fwd_gbps, 1),
                 "pct_peak": round(100 * fwd_gbps * 1e9 / HBM_PEAK, 2), "bytes": FWD_BYTES,

@@ -12,10 +12,8 @@ contract (fuselse/gpu/autograd.py:6-61):
   else;
 * with grad enabled and ``input.requires_grad`` it goes through an autograd
   Function whose backward is the fused ``grad * exp(x - lse)`` kernel (no
-  double backward).  Its forward calls ``ext.onepass_lse_float[_robust]_keep``
-  where the ext has it (this package's does; the reference's does not): the
-  same result, with part of x left in the Infinity Cache for the backward's
-  read of it;
+  double backward); its forward is the same kernel as without grad, as in the
+  reference (autograd.py:15-34);
 * a contiguous 2-D input without grad calls the kernel directly; other shapes
   are flattened to (rows, N), made contiguous, and reshaped back;
 * ``keepdim`` unsqueezes the last dimension.
@@ -24,6 +22,14 @@ contract (fuselse/gpu/autograd.py:6-61):
 autograd.py:40) also routes CUDA fp16 / bf16 tensors to the kernels: fp32
 accumulation, the result rounded to the input dtype as ``torch.logsumexp``
 returns it, and a fused half backward from the fp32 LSE.
+
+``keep=True`` (not in the reference) makes the forward under autograd call
+``ext.onepass_lse_float[_robust]_keep`` (and its half twins): the same result,
+with part of x left in the Infinity Cache for a backward that reads x right
+after the forward.  It is off by default: the keeping forward alone is about
+4% slower than the plain one, and its gain is gone once other work moves a few
+hundred MB through the cache between the forward and its backward, as the rest
+of a training step does.
 """
 
 from __future__ import annotations
@@ -31,11 +37,13 @@ from __future__ import annotations
 import torch
 
 
-def make_fuselse_logsumexp(ext, robust: bool = True, half_inputs: bool = False):
+def make_fuselse_logsumexp(ext, robust: bool = True, half_inputs: bool = False, keep: bool = False):
     fwd = ext.onepass_lse_float_robust if robust else ext.onepass_lse_float
-    # the forward whose backward follows (autograd): the keeping variant where
-    # the ext provides one
-    fwd_grad = getattr(ext, ("onepass_lse_float_robust" if robust else "onepass_lse_float") + "_keep", fwd)
+    # the forward whose backward follows (autograd): with keep, the keeping
+    # variant where the ext provides one
+    fwd_grad = fwd
+    if keep:
+        fwd_grad = getattr(ext, ("onepass_lse_float_robust" if robust else "onepass_lse_float") + "_keep", fwd)
     bwd = ext.onepass_lse_float_backward
     torch_logsumexp = torch.logsumexp
     half_fwd = {}
@@ -43,8 +51,10 @@ def make_fuselse_logsumexp(ext, robust: bool = True, half_inputs: bool = False):
     if half_inputs:
         half_fwd = {torch.float16: lambda x: ext.batched_logsumexp_fp16(x, robust),
                     torch.bfloat16: lambda x: ext.batched_logsumexp_bf16(x, robust)}
-        f16k = getattr(ext, "batched_logsumexp_fp16_keep", ext.batched_logsumexp_fp16)
-        bf16k = getattr(ext, "batched_logsumexp_bf16_keep", ext.batched_logsumexp_bf16)
+        f16k = getattr(ext, "batched_logsumexp_fp16_keep", ext.batched_logsumexp_fp16) if keep else \
+            ext.batched_logsumexp_fp16
+        bf16k = getattr(ext, "batched_logsumexp_bf16_keep", ext.batched_logsumexp_bf16) if keep else \
+            ext.batched_logsumexp_bf16
         half_fwd_grad = {torch.float16: lambda x: f16k(x, robust), torch.bfloat16: lambda x: bf16k(x, robust)}
         half_bwd = ext.onepass_lse_half_backward
 
@@ -101,4 +111,5 @@ def make_fuselse_logsumexp(ext, robust: bool = True, half_inputs: bool = False):
 
     logsumexp.fuselse_robust = robust
     logsumexp.fuselse_half_inputs = half_inputs
+    logsumexp.fuselse_keep = keep
     return logsumexp

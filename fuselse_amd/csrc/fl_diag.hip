@@ -184,6 +184,7 @@ extern "C" int fl_diag_read_stream(const void* x, int64_t nbytes, int blocks, in
     FL_CHECK(blocks > 0 && blocks <= (1 << 20), "%s: blocks out of range", name);
     FL_CHECK(sink != nullptr, "%s: sink is NULL", name);
     if (nbytes == 0) return ok();
+    FL_CHECK(x != nullptr, "%s: x is NULL", name);
     const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     FL_CHECK(threads == 64 || threads == 256, "%s: threads must be 64 or 256", name);
     const char* xs = static_cast<const char*>(x);

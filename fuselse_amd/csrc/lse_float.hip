@@ -1035,11 +1035,13 @@ extern "C" int fl_lse_fwd_bf16_ws(const void* x, float* out, int64_t B, int64_t 
 // B < kSplitMaxRows and S <= 64, at most 319 * 64 * 8 = 163,328 bytes, so one
 // static 160 KiB array per GPU holds every plan's partials.  Host code never
 // uses the array's name as an address (on the host it is only a stand-in for
-// the symbol): each device's address comes from hipGetSymbolAddress, taken
-// once per device on the first call made with that device current.  Every
-// partial is written by the partials kernel before the merge kernel reads it,
-// so the array needs no clearing between calls.  Calls on one GPU share the
-// array: calls whose work can overlap (different streams of one device) race.
+// the symbol): each device's address comes from hipGetSymbolAddress, taken on
+// the first call with a split shape made with that device current and kept
+// only once it succeeded, so a call that failed (for instance one made under
+// graph capture) leaves the next call to try again.  Every partial is written
+// by the partials kernel before the merge kernel reads it, so the array needs
+// no clearing between calls.  Calls on one GPU share the array: calls whose
+// work can overlap (different streams of one device) race.
 // ---------------------------------------------------------------------------
 namespace fl {
 constexpr int64_t kNoAllocPairs = 20480;  // 160 KiB of float2
@@ -1047,12 +1049,8 @@ static_assert((kSplitMaxRows - 1) * 64 <= kNoAllocPairs, "static scratch smaller
 static __device__ __align__(256) float2 scratch[kNoAllocPairs];
 
 constexpr int kMaxDevices = 64;
-struct ScratchSlot {
-    std::once_flag once;
-    void* ptr = nullptr;
-    hipError_t err = hipSuccess;
-};
-static ScratchSlot g_scratch[kMaxDevices];
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];  // guarded by g_scratch_mu; NULL until an address was taken
 
 // Device address of `scratch` on the current device, which must be the
 // device of `stream` (the address is only valid there).
@@ -1068,12 +1066,16 @@ static int scratch_address(const char* name, hipStream_t stream, void** ptr) {
             return set_error(FL_EINVAL, "%s: hipStreamGetDevice failed: %s", name, hipGetErrorString(se));
         FL_CHECK(sdev == dev, "%s: the stream belongs to device %d, the current device is %d", name, sdev, dev);
     }
-    ScratchSlot& slot = g_scratch[dev];
-    std::call_once(slot.once, [&slot] { slot.err = hipGetSymbolAddress(&slot.ptr, HIP_SYMBOL(scratch)); });
-    if (slot.err != hipSuccess || slot.ptr == nullptr)
-        return set_error(FL_ELAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", name, dev,
-                         hipGetErrorString(slot.err));
-    *ptr = slot.ptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t ge = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (ge != hipSuccess || p == nullptr)
+            return set_error(FL_ELAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", name, dev,
+                             hipGetErrorString(ge));
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
     return FL_OK;
 }
 }  // namespace fl

@@ -143,9 +143,12 @@ int fl_lse_fwd_bf16_ws(const void* x, float* out, int64_t B, int64_t N, int robu
  * plan and results as fl_lse_fwd_f32_ws (bit-identical).
  * Limit: the array holds 160 KiB per GPU (held until the process ends); every
  * split plan fits (B < 320 rows, at most 64 segments), and a shape needing
- * more is rejected with FL_ERANGE.  The first call on a device takes the
- * array's address on that device (hipGetSymbolAddress), so make it once
- * outside graph capture.  The array's address is per device, so a call whose
+ * more is rejected with FL_ERANGE.  The first call on a device whose shape
+ * takes the split plan (few long rows; other shapes never touch the array)
+ * takes the array's address on that device (hipGetSymbolAddress), so make
+ * one such call outside graph capture first.  The address is kept only once
+ * it was taken; a call that failed to take it returns FL_ELAUNCH and the next
+ * call tries again.  The array's address is per device, so a call whose
  * split plan uses it checks that `stream` belongs to the current device
  * (FL_EINVAL otherwise).  All calls on one GPU share the array: calls that
  * can run concurrently on one GPU (different streams) race and must not

@@ -53,6 +53,10 @@ def test_invalid_arguments_rejected_without_launch():
     assert b"negative shape" in lib.fl_last_error()
     assert lib.fl_lse_fwd_f32_noalloc(None, None, 3, 4, 1, None) == 1
     assert b"out is NULL" in lib.fl_last_error()
+    # the read-ceiling kernel refuses a NULL buffer before building a resource
+    # over it (the sink pointer is only checked for NULL on the host)
+    assert lib.fl_diag_read_stream(None, 256, 4, 64, 2, ctypes.c_void_p(256), None) == 1
+    assert b"x is NULL" in lib.fl_last_error()
     # B == 0 is a no-op success
     assert lib.fl_lse_fwd_f32_noalloc(None, None, 0, 4, 1, None) == 0
     assert lib.fl_lse_fwd_f32(None, None, 0, 4, 1, None) == 0

@@ -171,13 +171,26 @@ class FakeKeepExt(FakeExt):
 
 
 @pytest.mark.parametrize("robust", [True, False])
-def test_autograd_forward_keeps_x_for_the_backward(robust):
-    """With grad the forward is the keeping variant, where the ext has one;
-    without grad (nothing reads x again) it is the plain forward.  An ext
-    without the keeping variants (the reference's) gets the plain forward
-    both ways."""
+def test_autograd_forward_is_the_plain_forward_by_default(robust):
+    """By default the forward under autograd is the plain forward, as in the
+    reference (autograd.py:15-34), even where the ext has a keeping variant."""
     ext = FakeKeepExt()
     lse = make_fuselse_logsumexp(ext, robust=robust)
+    assert lse.fuselse_keep is False
+    x = torch.randn(4, 7, requires_grad=True)
+    y = lse(fake(x))
+    y.as_subclass(torch.Tensor).sum().backward()
+    assert [c[0] for c in ext.calls] == ["fwd_robust" if robust else "fwd", "bwd"]
+
+
+@pytest.mark.parametrize("robust", [True, False])
+def test_autograd_forward_keeps_x_for_the_backward(robust):
+    """With keep=True and grad the forward is the keeping variant, where the ext
+    has one; without grad (nothing reads x again) it is the plain forward.  An
+    ext without the keeping variants (the reference's) gets the plain forward
+    both ways."""
+    ext = FakeKeepExt()
+    lse = make_fuselse_logsumexp(ext, robust=robust, keep=True)
     x = torch.randn(4, 7, requires_grad=True)
     y = lse(fake(x))
     y.as_subclass(torch.Tensor).sum().backward()
@@ -188,20 +201,21 @@ def test_autograd_forward_keeps_x_for_the_backward(robust):
     lse(fake(x.detach()))
     assert [c[0] for c in ext.calls] == ["fwd_robust" if robust else "fwd"] * 2
     plain = FakeExt()
-    y = make_fuselse_logsumexp(plain, robust=robust)(fake(x))
+    y = make_fuselse_logsumexp(plain, robust=robust, keep=True)(fake(x))
     y.as_subclass(torch.Tensor).sum().backward()
     assert [c[0] for c in plain.calls] == ["fwd_robust" if robust else "fwd", "bwd"]
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_half_autograd_forward_keeps_x(dtype):
+@pytest.mark.parametrize("keep", [False, True])
+def test_half_autograd_forward_keeps_x_only_when_asked(dtype, keep):
     ext = FakeKeepExt()
-    lse = make_fuselse_logsumexp(ext, half_inputs=True)
+    lse = make_fuselse_logsumexp(ext, half_inputs=True, keep=keep)
     x = torch.randn(3, 9).to(dtype).requires_grad_(True)
     y = lse(fake(x))
     y.as_subclass(torch.Tensor).float().sum().backward()
-    tag = "fwd_fp16_keep" if dtype == torch.float16 else "fwd_bf16_keep"
-    assert [c[0] for c in ext.calls] == [tag, "bwd_half"]
+    tag = "fwd_fp16" if dtype == torch.float16 else "fwd_bf16"
+    assert [c[0] for c in ext.calls] == [tag + ("_keep" if keep else ""), "bwd_half"]
 
 
 # ---------------------------------------------------------------------------

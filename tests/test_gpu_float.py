@@ -337,21 +337,22 @@ def test_dropin_autograd_matches_torch(cuda):
 
 
 @pytest.mark.parametrize("B,N", [(512, 128256), (1024, 20000)])
-def test_dropin_autograd_keeping_forward_at_size(cuda, B, N):
-    """Under autograd the drop-in's forward is the keeping variant; at C2
-    (256-thread blocks) and at 1024 rows of 20000 (1024-thread blocks), where
-    it keeps part of x for the backward, the forward and the gradient equal
-    the plain ext calls bit for bit, and the gradient's first 64 rows match
-    fp64."""
+@pytest.mark.parametrize("keep", [False, True])
+def test_dropin_autograd_at_size(cuda, B, N, keep):
+    """The drop-in under autograd, with the plain forward (the default) and
+    with keep=True (the keeping variant, which at C2, 256-thread blocks, and at
+    1024 rows of 20000, 1024-thread blocks, leaves part of x for the backward):
+    the forward and the gradient equal the plain ext calls bit for bit, and the
+    gradient's first 64 rows match fp64."""
     import fuselse_amd
 
-    print(f"case dropin autograd keep B={B} N={N}", flush=True)
+    print(f"case dropin autograd keep={keep} B={B} N={N}", flush=True)
     ext = fuselse_amd.ext
     x = O.make_c2_input(B, N, seed=11)
     g = np.random.default_rng(12).standard_normal(B).astype(np.float32)
     xd = torch.from_numpy(x).to(cuda)
     gd = torch.from_numpy(g).to(cuda)
-    lse = fuselse_amd.make_fuselse_logsumexp(ext, robust=True)
+    lse = fuselse_amd.make_fuselse_logsumexp(ext, robust=True, keep=keep)
     a = xd.clone().requires_grad_(True)
     y = lse(a, dim=-1)
     y.backward(gd)
