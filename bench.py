@@ -240,6 +240,32 @@ def _copy_calibration(torch, dev):
     del a, b
 
 
+def c5_csr_layer(torch, dev, nodes=1_000_000, batch=512, seed=11):
+    """The C5 CSR sum layer: fan-in k ~ p(k) proportional to k^-2 on [2, 256]
+    per node, child ids uniform over `nodes` child rows, log-parameters a
+    per-node log-softmax of N(0, 1), child log-probabilities log(U(0, 1)).
+    Returns the host offsets and log-parameters (float64) and the device child
+    matrix, offsets, child ids (int32) and log-parameters (fp32)."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    ks = np.arange(2, 257)
+    pk = ks.astype(np.float64) ** -2.0
+    fan = rng.choice(ks, size=nodes, p=pk / pk.sum())
+    off = np.concatenate([[0], np.cumsum(fan)]).astype(np.int64)
+    nnz = int(off[-1])
+    lp = rng.standard_normal(nnz)
+    seg = np.maximum.reduceat(lp, off[:-1])
+    lp = lp - np.repeat(seg + np.log(np.add.reduceat(np.exp(lp - np.repeat(seg, fan)), off[:-1])), fan)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    child = torch.log(torch.rand(nodes, batch, device=dev, generator=gen).clamp_min_(1e-30))
+    d_off = torch.from_numpy(off).to(dev)
+    d_cid = torch.randint(0, nodes, (nnz,), device=dev, generator=gen, dtype=torch.int32)
+    d_lp = torch.from_numpy(lp.astype(np.float32)).to(dev)
+    return off, lp, child, d_off, d_cid, d_lp
+
+
 def measure_configs(torch, ext, dev, stream, iters=50, only=None):
     """The other BASELINE configs: fp16/bf16 forward (C3), IntLSE Q16.16 fp32 /
     int32 and Q10.6 int16 (C4), sparse PC at 1M nodes (C5); beside them the
@@ -598,21 +624,9 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
         del q6
     if want("C5"):
         # C5: sparse PC, 1M sum nodes, power-law fan-in (alpha = 2) on [2, 256], batch 512
-        sys.path.insert(0, ROOT)
         nodes, batch = 1_000_000, 512
-        rng = np.random.default_rng(11)
-        ks = np.arange(2, 257)
-        pk = ks.astype(np.float64) ** -2.0
-        fan = rng.choice(ks, size=nodes, p=pk / pk.sum())
-        off = np.concatenate([[0], np.cumsum(fan)]).astype(np.int64)
+        off, lp_np, child, d_off, d_cid, d_lp = c5_csr_layer(torch, dev, nodes, batch)
         nnz = int(off[-1])
-        lp = rng.standard_normal(nnz)
-        seg = np.maximum.reduceat(lp, off[:-1])
-        lp = lp - np.repeat(seg + np.log(np.add.reduceat(np.exp(lp - np.repeat(seg, fan)), off[:-1])), fan)
-        child = torch.log(torch.rand(nodes, batch, device=dev, generator=gen).clamp_min_(1e-30))
-        d_off = torch.from_numpy(off).to(dev)
-        d_cid = torch.randint(0, nodes, (nnz,), device=dev, generator=gen, dtype=torch.int32)
-        d_lp = torch.from_numpy(lp.astype(np.float32)).to(dev)
         out = torch.empty(nodes, batch, device=dev)
         sbytes = nnz * batch * 4 + nnz * 8 + (nodes + 1) * 8 + nodes * batch * 4
         for q16, tag in [(False, "fp32"), (True, "q16")]:

@@ -217,6 +217,8 @@ extern "C" int fl_diag_copy_stream(const void* x, void* y, int64_t nbytes, int b
     FL_CHECK(blocks > 0 && blocks <= (1 << 24), "%s: blocks out of range", name);
     if (nbytes == 0) return ok();
     FL_CHECK(x != nullptr && y != nullptr, "%s: x or y is NULL", name);
+    FL_CHECK(blocks <= max_grid_blocks(threads), "%s: %d blocks of %d threads exceed one dispatch", name, blocks,
+             threads);
     const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const char* xs = static_cast<const char*>(x);
     char* ys = static_cast<char*>(y);

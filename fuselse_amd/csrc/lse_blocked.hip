@@ -330,7 +330,7 @@ static void launch_k(float* node_mars, const float* child, const float* params, 
     const int64_t ctiles = (batch + 16 * NT - 1) / (16 * NT);
     const int64_t pgroups = (bs + 16 * MT - 1) / (16 * MT);
     const int64_t items = nblocks * pgroups * ctiles;
-    constexpr int64_t kMax = (int64_t)1 << 30;  // workgroups per launch, a multiple of 8
+    constexpr int64_t kMax = max_grid_blocks(64);  // workgroups per launch, a multiple of 8
     for (int64_t id0 = 0; id0 < items; id0 += kMax) {
         const int64_t n = items - id0 < kMax ? items - id0 : kMax;
         const unsigned grid = (unsigned)((n + 7) / 8 * 8);

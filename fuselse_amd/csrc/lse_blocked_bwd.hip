@@ -904,8 +904,8 @@ __global__ __launch_bounds__(256) void blocked_bwd_elements(float* __restrict__ 
                                                             const float* __restrict__ edge_flows,
                                                             const int64_t* __restrict__ csc_offsets,
                                                             const int32_t* __restrict__ csc_edges, int64_t nel,
-                                                            int64_t batch) {
-    const int64_t c = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+                                                            int64_t batch, int64_t block0) {
+    const int64_t c = (block0 + (int64_t)blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (c >= nel) return;
     const int64_t k0 = csc_offsets[c];
     const int64_t k1 = csc_offsets[c + 1];
@@ -935,7 +935,7 @@ __global__ __launch_bounds__(256) void blocked_bwd_elements(float* __restrict__ 
 
 namespace {
 
-constexpr int64_t kMaxGroups = (int64_t)1 << 30;  // workgroups per launch, a multiple of 8
+constexpr int64_t kMaxGroups = max_grid_blocks(64);  // workgroups per launch, a multiple of 8
 // Columns per lane per pass of the parameter-flow product, and parent K-steps
 // per chunk of the edge-flow product (at most).  Measured at 8192 blocks of
 // 32 parents, 32 edges, batch 512: 16 columns and 8 K-steps 1280 us; 8 and 4
@@ -1088,13 +1088,14 @@ extern "C" int fl_sparse_blocked_bwd(const float* node_flows, const float* node_
                                              nids, cids, pids, nb, ne, bs, batch, st);
     }
     if (num_elements > 0) {
-        const dim3 grid((unsigned)((num_elements + 3) / 4));
-        if (vec)
-            sparse::blocked_bwd_elements<true><<<grid, dim3(256), 0, st>>>(element_flows, edge_flows, csc_offsets,
-                                                                          csc_edges, num_elements, batch);
-        else
-            sparse::blocked_bwd_elements<false><<<grid, dim3(256), 0, st>>>(element_flows, edge_flows, csc_offsets,
-                                                                           csc_edges, num_elements, batch);
+        for_grid_chunks((num_elements + 3) / 4, 256, [&](int64_t b0, int64_t nb) {
+            if (vec)
+                sparse::blocked_bwd_elements<true><<<dim3((unsigned)nb), dim3(256), 0, st>>>(
+                    element_flows, edge_flows, csc_offsets, csc_edges, num_elements, batch, b0);
+            else
+                sparse::blocked_bwd_elements<false><<<dim3((unsigned)nb), dim3(256), 0, st>>>(
+                    element_flows, edge_flows, csc_offsets, csc_edges, num_elements, batch, b0);
+        });
     }
     return launch_status(name);
 }

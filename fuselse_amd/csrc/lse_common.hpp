@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "fl_grid.hpp"
+
 namespace fl {
 
 constexpr float kLog2e = 1.4426950408889634f;

@@ -502,14 +502,13 @@ static int64_t pow2_ceil(int64_t v) {
 template <typename T, bool ROBUST, int LPR, int U, bool PIPE, typename OUT>
 static void launch_group(const T* x, OUT out, int64_t B, int64_t N, hipStream_t st) {
     const int64_t rows_per_block = 4 * (64 / LPR);
-    int64_t grid = (B + rows_per_block - 1) / rows_per_block;
-    if (grid > (int64_t)1 << 30) grid = (int64_t)1 << 30;
+    const int64_t grid = grid_stride_blocks((B + rows_per_block - 1) / rows_per_block, 256);
     lse_fwd_group_rows<T, ROBUST, LPR, U, PIPE, OUT><<<dim3((unsigned)grid), dim3(256), 0, st>>>(x, out, B, N);
 }
 
 template <typename T, bool ROBUST, int THREADS, int U, bool PIPE, typename OUT>
 static void launch_block(const T* x, OUT out, int64_t B, int64_t N, hipStream_t st, int64_t keep_rows) {
-    const int64_t grid = B < ((int64_t)1 << 30) ? B : ((int64_t)1 << 30);
+    const int64_t grid = grid_stride_blocks(B, THREADS);
     if (keep_rows > 0)
         lse_fwd_block_rows<T, ROBUST, THREADS, U, PIPE, OUT, true>
             <<<dim3((unsigned)grid), dim3(THREADS), 0, st>>>(x, out, B, N, keep_rows);
@@ -750,9 +749,10 @@ __device__ __forceinline__ void bwd_vec(const RowOut<T, BUF>& dst, const T* body
 template <typename T, int U, bool GRAN, typename GR, bool BUF>
 __global__ __launch_bounds__(256) void lse_bwd_row_chunks(const float* __restrict__ g, const T* __restrict__ x,
                                                           const float* __restrict__ lse, T* __restrict__ gx,
-                                                          int64_t N, int64_t chunks_per_row, GR gr_t) {
+                                                          int64_t N, int64_t chunks_per_row, GR gr_t,
+                                                          int64_t block0) {
     constexpr int VE = Elem<T>::kVec;
-    const int64_t blk = blockIdx.x;
+    const int64_t blk = block0 + blockIdx.x;
     const int64_t row = blk / chunks_per_row;
     const int64_t chunk = blk - row * chunks_per_row;
     const int tid = threadIdx.x;
@@ -793,9 +793,9 @@ __global__ __launch_bounds__(256) void lse_bwd_row_chunks(const float* __restric
 template <typename T, typename GR, bool STRADDLE>
 __global__ __launch_bounds__(64) void lse_bwd_flat(const float* __restrict__ g, const T* __restrict__ x,
                                                    const float* __restrict__ lse, T* __restrict__ gx, int64_t N,
-                                                   int64_t total_vecs, GR gr_t) {
+                                                   int64_t total_vecs, GR gr_t, int64_t block0) {
     constexpr int VE = Elem<T>::kVec;
-    const int64_t v0 = (int64_t)blockIdx.x * 64;
+    const int64_t v0 = (block0 + (int64_t)blockIdx.x) * 64;
     const int64_t row0 = v0 * VE / N;
     const int l = threadIdx.x;
     const int64_t v = v0 + l;
@@ -894,13 +894,19 @@ static void launch_bwd_vec(const float* g, const T* x, const float* lse, T* gx, 
     // copy of the same bytes: 490.9), the selective backward 512.8 -> 489.6.
     if (row_bytes >= 1024 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0) {
         const int64_t total_vecs = B * N / VE;
-        const dim3 grid((unsigned)((total_vecs + 63) / 64));
+        const int64_t blocks = (total_vecs + 63) / 64;
         if (row_bytes % 16 == 0) {
-            lse_bwd_flat<T, GR, false><<<grid, dim3(64), 0, st>>>(g, x, lse, gx, N, total_vecs, gr_t);
+            for_grid_chunks(blocks, 64, [&](int64_t b0, int64_t nb) {
+                lse_bwd_flat<T, GR, false><<<dim3((unsigned)nb), dim3(64), 0, st>>>(g, x, lse, gx, N, total_vecs, gr_t,
+                                                                                    b0);
+            });
             return;
         }
         if ((B * N) % VE == 0) {
-            lse_bwd_flat<T, GR, true><<<grid, dim3(64), 0, st>>>(g, x, lse, gx, N, total_vecs, gr_t);
+            for_grid_chunks(blocks, 64, [&](int64_t b0, int64_t nb) {
+                lse_bwd_flat<T, GR, true><<<dim3((unsigned)nb), dim3(64), 0, st>>>(g, x, lse, gx, N, total_vecs, gr_t,
+                                                                                   b0);
+            });
             return;
         }
     }
@@ -920,18 +926,21 @@ static void launch_bwd_vec(const float* g, const T* x, const float* lse, T* gx, 
         // (a run-time switch measured 1-3% slower on every shape: a wave
         // handles one vector, so the kernel is two instantiations)
         if (granules)
-            lse_bwd_row_chunks<T, U, true, GR, BUF>
-                <<<dim3((unsigned)(B * (cpr0 + 1))), dim3(256), 0, st>>>(g, x, lse, gx, N, cpr0 + 1, gr_t);
+            for_grid_chunks(B * (cpr0 + 1), 256, [&](int64_t b0, int64_t nb) {
+                lse_bwd_row_chunks<T, U, true, GR, BUF>
+                    <<<dim3((unsigned)nb), dim3(256), 0, st>>>(g, x, lse, gx, N, cpr0 + 1, gr_t, b0);
+            });
         else
-            lse_bwd_row_chunks<T, U, false, GR, BUF>
-                <<<dim3((unsigned)(B * cpr0)), dim3(256), 0, st>>>(g, x, lse, gx, N, cpr0, gr_t);
+            for_grid_chunks(B * cpr0, 256, [&](int64_t b0, int64_t nb) {
+                lse_bwd_row_chunks<T, U, false, GR, BUF>
+                    <<<dim3((unsigned)nb), dim3(256), 0, st>>>(g, x, lse, gx, N, cpr0, gr_t, b0);
+            });
         return;
     }
     int64_t lpr = pow2_ceil((vecs + 3) / 4);
     if (lpr < 4) lpr = 4;
     const int64_t rpb = 256 / lpr;
-    int64_t grid = (B + rpb - 1) / rpb;
-    if (grid > (int64_t)1 << 30) grid = (int64_t)1 << 30;
+    const int64_t grid = grid_stride_blocks((B + rpb - 1) / rpb, 256);
     const dim3 gd((unsigned)grid), blk(256);
     switch (lpr) {
     case 4: lse_bwd_group_rows<T, 4, GR, BUF><<<gd, blk, 0, st>>>(g, x, lse, gx, B, N, gr_t); break;
@@ -965,13 +974,11 @@ static void launch_bwd(const float* g, const T* x, const float* lse, T* gx, int6
 template <typename T, typename GR>
 static int bwd_entry(const char* name, const float* grad, const T* x, const float* lse, T* grad_x, int64_t B,
                      int64_t N, GR gr_t, void* stream) {
-    constexpr int VE = Elem<T>::kVec;
     FL_CHECK(B >= 0 && N >= 0, "%s: negative shape (B=%lld, N=%lld)", name, (long long)B, (long long)N);
     if (B == 0 || N == 0) return ok();
     FL_CHECK(grad && x && lse && grad_x, "%s: NULL pointer argument", name);
     FL_CHECK((reinterpret_cast<uintptr_t>(x) % sizeof(T)) == 0 && (reinterpret_cast<uintptr_t>(grad_x) % sizeof(T)) == 0,
              "%s: x / grad_x are not element-aligned", name);
-    FL_CHECK(B * ((N / VE + 1 + 255) / 256) < ((int64_t)1 << 32), "%s: B*N too large for the grid", name);
     launch_bwd<T>(grad, x, lse, grad_x, B, N, gr_t, reinterpret_cast<hipStream_t>(stream));
     return launch_status(name);
 }

@@ -476,15 +476,13 @@ __global__ __launch_bounds__(128) void intlse_q10_6_rows_paired(const int16_t* _
     }
 }
 
-// Calls launch(grid, x, out, acc) for consecutive chunks of at most 2^30 rows
-// (one block per row).
+// Calls launch(grid, x, out, acc) for consecutive chunks of rows (one block
+// per row), each within one dispatch for blocks of up to 256 threads.
 template <typename T, typename LAUNCH>
 static void for_row_chunks(const T* x, float* out, int32_t* acc, int64_t B, int64_t N, LAUNCH launch) {
-    constexpr int64_t kMaxGrid = (int64_t)1 << 30;
-    for (int64_t r0 = 0; r0 < B; r0 += kMaxGrid) {
-        const int64_t rows = B - r0 < kMaxGrid ? B - r0 : kMaxGrid;
+    for_grid_chunks(B, 256, [&](int64_t r0, int64_t rows) {
         launch(dim3((unsigned)rows), x + r0 * N, out + r0, acc ? acc + r0 : nullptr);
-    }
+    });
 }
 
 // Chunks per lane kept in flight ahead of the pair chain.  Every block starts

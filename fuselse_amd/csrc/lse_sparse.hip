@@ -415,14 +415,12 @@ static void launch(const LAYOUT& L, const float* child, const float* out_any, in
     const int64_t tile = 64 * P;
     const int64_t tiles = (batch + tile - 1) / tile;
     const int64_t pairs = items * tiles;
-    constexpr int64_t kChunk = (int64_t)1 << 30;  // blocks per launch
-    for (int64_t p0 = 0; p0 < pairs; p0 += kChunk) {
-        const int64_t n = pairs - p0 < kChunk ? pairs - p0 : kChunk;
+    for_grid_chunks(pairs, 64, [&](int64_t p0, int64_t n) {
         if (vec)
             sparse_kernel<Q16, true, LAYOUT><<<dim3((unsigned)n), dim3(64), 0, st>>>(L, child, batch, items, tiles, p0);
         else
             sparse_kernel<Q16, false, LAYOUT><<<dim3((unsigned)n), dim3(64), 0, st>>>(L, child, batch, items, tiles, p0);
-    }
+    });
 }
 
 // ---------------------------------------------------------------------------
@@ -529,9 +527,10 @@ __global__ __launch_bounds__(64 * WPB) void csr_bwd_kernel(const float* __restri
                                                       const int32_t* __restrict__ csc_edge,
                                                       const int32_t* __restrict__ csc_node,
                                                       float* __restrict__ gchild, float* __restrict__ glogp,
-                                                      int64_t children, int64_t batch) {
+                                                      int64_t children, int64_t batch, int64_t block0) {
     const int l = lane_id();
-    const int64_t c = (int64_t)blockIdx.x * WPB + (WPB > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0);
+    const int64_t c =
+        (block0 + (int64_t)blockIdx.x) * WPB + (WPB > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0);
     if (c >= children) return;
     const int64_t p0 = uniform64(csc_off[c]);
     const int64_t k = uniform64(csc_off[c + 1]) - p0;
@@ -584,16 +583,17 @@ extern "C" int fl_sparse_csr_bwd(const float* child, const float* out, const flo
     const bool vec = (batch % 4 == 0) && ((reinterpret_cast<uintptr_t>(child) | reinterpret_cast<uintptr_t>(out) |
                                            reinterpret_cast<uintptr_t>(grad_out) |
                                            reinterpret_cast<uintptr_t>(grad_child)) & 15) == 0;
-    const dim3 grid((unsigned)((num_children + 3) / 4));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    if (vec)
-        sparse::csr_bwd_kernel<true, 4><<<grid, dim3(256), 0, st>>>(child, out, grad_out, logparams, csc_offsets,
-                                                                  csc_edges, csc_nodes, grad_child, grad_logparams,
-                                                                  num_children, batch);
-    else
-        sparse::csr_bwd_kernel<false, 4><<<grid, dim3(256), 0, st>>>(child, out, grad_out, logparams, csc_offsets,
-                                                                   csc_edges, csc_nodes, grad_child, grad_logparams,
-                                                                   num_children, batch);
+    for_grid_chunks((num_children + 3) / 4, 256, [&](int64_t b0, int64_t nb) {
+        if (vec)
+            sparse::csr_bwd_kernel<true, 4><<<dim3((unsigned)nb), dim3(256), 0, st>>>(
+                child, out, grad_out, logparams, csc_offsets, csc_edges, csc_nodes, grad_child, grad_logparams,
+                num_children, batch, b0);
+        else
+            sparse::csr_bwd_kernel<false, 4><<<dim3((unsigned)nb), dim3(256), 0, st>>>(
+                child, out, grad_out, logparams, csc_offsets, csc_edges, csc_nodes, grad_child, grad_logparams,
+                num_children, batch, b0);
+    });
     return launch_status(name);
 }
 

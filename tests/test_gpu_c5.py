@@ -1,0 +1,92 @@
+"""The C5 sparse sum layer at the size the benchmark times (1M nodes,
+power-law fan-in with alpha = 2 on [2, 256], batch 512; bench.py's
+c5_csr_layer builds it), checked on samples against the oracle:
+
+* the fp32 forward of 2,000 sampled nodes against float64 (1e-5 relative);
+* the Q16.16 forward of the same nodes bit for bit against the oracle's
+  restatement of the reference's edge-thread tree, which for a node depends
+  only on its own edges in order, so a sub-layer of the sampled nodes over
+  the child rows they read reproduces it;
+* the fp32 backward (flows) of 300 sampled child rows and of every edge into
+  them against float64.
+
+The node sample includes the largest and smallest fan-ins.  Reference check
+of the same kind: experiment_pyjuice/run_pyjuice.py:90-119,228-239."""
+
+import importlib.util
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _bench():
+    spec = importlib.util.spec_from_file_location("bench_c5", os.path.join(ROOT, "bench.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def _sub_layer(nodes_sel, off, cids, lp, child):
+    """The CSR sub-layer of the selected nodes over the child rows they read."""
+    fan = off[nodes_sel + 1] - off[nodes_sel]
+    edges = np.concatenate([np.arange(off[n], off[n + 1]) for n in nodes_sel])
+    sub_off = np.concatenate([[0], np.cumsum(fan)]).astype(np.int64)
+    uniq, inv = np.unique(cids[edges], return_inverse=True)
+    rows = child[torch.from_numpy(uniq).to(child.device).long()].cpu().numpy()
+    return edges, sub_off, inv.astype(np.int32), lp[edges], rows
+
+
+def test_c5_layer_sampled(cuda):
+    import fuselse_amd
+
+    ext = fuselse_amd.ext
+    print("case C5 layer 1M nodes batch 512", flush=True)
+    off, _, child, d_off, d_cid, d_lp = _bench().c5_csr_layer(torch, cuda)
+    nodes, batch = child.shape
+    cids = d_cid.cpu().numpy()
+    lp = d_lp.cpu().numpy()
+    fan = np.diff(off)
+    rng = np.random.default_rng(5)
+    sel = set(rng.choice(nodes, 2000, replace=False).tolist())
+    sel.update(np.flatnonzero(fan == fan.max())[:4].tolist())
+    sel.update(np.flatnonzero(fan == 2)[:4].tolist())
+    sel = np.array(sorted(sel), np.int64)
+
+    out = ext.sparse_csr_forward(child, d_off, d_cid, d_lp)
+    outq = ext.sparse_csr_forward(child, d_off, d_cid, d_lp, q16=True)
+    _, s_off, s_cid, s_lp, s_child = _sub_layer(sel, off, cids, lp, child)
+    want = O.sparse_csr_fp64(s_child, s_off, s_cid, s_lp)
+    np.testing.assert_allclose(out[torch.from_numpy(sel).to(cuda)].cpu().numpy(), want, rtol=1e-5, atol=1e-6)
+    wq = O.sparse_q16_csr(s_child, s_off, s_cid, s_lp)
+    gq = outq[torch.from_numpy(sel).to(cuda)].cpu().numpy()
+    np.testing.assert_array_equal(gq.view(np.int32), wq.view(np.int32))
+    del outq
+
+    # backward: 300 sampled children, every edge into them and the parents of those edges
+    gen = torch.Generator(device=cuda)
+    gen.manual_seed(6)
+    gout = torch.rand(nodes, batch, device=cuda, generator=gen) + 0.05
+    gchild, glp = ext.sparse_csr_backward(child, out, gout, d_off, d_cid, d_lp)
+    kids = np.sort(rng.choice(nodes, 300, replace=False))
+    into = np.flatnonzero(np.isin(cids, kids))
+    parents = np.searchsorted(off, into, side="right") - 1
+    par_u, par_inv = np.unique(parents, return_inverse=True)
+    _, p_off, p_cid, p_lp, p_child = _sub_layer(par_u, off, cids, lp, child)
+    out64 = O.sparse_csr_fp64(p_child, p_off, p_cid, p_lp)  # the parents' outputs in float64
+    ch64 = child[torch.from_numpy(cids[into]).to(cuda).long()].cpu().numpy().astype(np.float64)
+    g64 = gout[torch.from_numpy(par_u).to(cuda)].cpu().numpy().astype(np.float64)
+    term = g64[par_inv] * np.exp(lp[into].astype(np.float64)[:, None] + ch64 - out64[par_inv])
+    want_glp = term.sum(axis=1)
+    np.testing.assert_allclose(glp[torch.from_numpy(into).to(cuda)].cpu().numpy(), want_glp, rtol=1e-5)
+    want_gc = np.zeros((len(kids), batch))
+    np.add.at(want_gc, np.searchsorted(kids, cids[into]), term)
+    got_gc = gchild[torch.from_numpy(kids).to(cuda)].cpu().numpy()
+    np.testing.assert_allclose(got_gc, want_gc, rtol=1e-5, atol=1e-30)

@@ -159,6 +159,47 @@ def test_intlse_q16_f32_past_2g_elements(big, use_lut):
     np.testing.assert_array_equal(out[rows].cpu().numpy().view(np.int32), want.view(np.int32))
 
 
+def test_intlse_q16_f32_rows_past_one_dispatch(big):
+    """IntLSE Q16.16 on (2^24 + 3, 16) fp32, 1 GiB: one 256-thread block per
+    row needs 2^32 + 768 work-items, more than one dispatch holds, so the
+    launcher splits the rows over two launches.  The first and last rows and
+    the rows on either side of the split, out and raw accumulators bit for bit
+    against the oracle's GPU tree."""
+    B, N = (1 << 24) + 3, 16
+    split = (((1 << 32) - 1) // 256) & ~7
+    print(f"case q16 f32 rows past one dispatch B={B} N={N}", flush=True)
+    x = _randn((B, N), torch.float32, 21, big, scale=2.0)
+    rows = sorted({0, 1, 2, split - 2, split - 1, split, split + 1, B - 2, B - 1})
+    xr = x[rows].cpu().numpy()
+    acc = torch.empty(B, dtype=torch.int32, device=big)
+    out = _ext().batched_logsumexp(x, acc_out=acc)
+    want, want_acc = O.q16_gpu_rows(xr, base_mod=x.data_ptr() & 15, use_lut=True, raw=True)
+    np.testing.assert_array_equal(acc[rows].cpu().numpy(), want_acc)
+    np.testing.assert_array_equal(out[rows].cpu().numpy().view(np.int32), want.view(np.int32))
+
+
+def test_bwd_f32_flat_past_one_dispatch(big):
+    """The flat fused backward over (2^21 + 1, 8192) fp32, 2^34 + 8192
+    elements (64 GiB in, 64 GiB out): 2^26 + 32 one-wave blocks, more than one
+    dispatch holds, so the launcher splits them over two launches.  The first
+    and last rows and the rows around the split against float64."""
+    B, N = (1 << 21) + 1, 8192
+    split_row = ((((1 << 32) - 1) // 64) & ~7) * 64 * 4 // N
+    print(f"case flat bwd f32 past one dispatch B={B} N={N}", flush=True)
+    torch.cuda.empty_cache()
+    x = _randn((B, N), torch.float32, 22, big, scale=3.0)
+    rows = sorted({0, 1, split_row - 1, split_row, split_row + 1, B - 1})
+    ext = _ext()
+    lse = ext.onepass_lse_float_robust(x)
+    g = torch.randn(B, device=big, generator=torch.Generator(device=big).manual_seed(23))
+    gx = ext.onepass_lse_float_backward(g, x, lse)
+    xr = x[rows].cpu().numpy()
+    want = O.lse_fp64(xr)
+    np.testing.assert_allclose(lse[rows].cpu().numpy(), want, rtol=RTOL32)
+    gw = O.lse_bwd_fp64(g[rows].cpu().numpy(), xr, want)
+    np.testing.assert_allclose(gx[rows].cpu().numpy(), gw, rtol=RTOL32, atol=1e-30)
+
+
 @pytest.mark.parametrize("N", [1000, 1001])
 def test_intlse_q10_6_past_4g_elements(big, N):
     """IntLSE Q10.6 on 4.4e9 int16 elements: N = 1000 takes the kernel with
