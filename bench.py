@@ -315,7 +315,7 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
             shapes.append((max(1, nbytes // 2048), 64, 2))
         for blocks, threads, unroll in shapes:
             def call(i, s, blocks=blocks, threads=threads, unroll=unroll):
-                _lib.call("fl_diag_read_stream", bufs[i % nb].data_ptr(), nbytes, blocks, threads, unroll,
+                _lib.diag_call("fl_diag_read_stream", bufs[i % nb].data_ptr(), nbytes, blocks, threads, unroll,
                           sink.data_ptr(), s)
             ms = loop_or_graph_ms(call, nb, graph)
             best = ms if best is None or ms < best else best
@@ -540,7 +540,7 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
                 tbuf = torch.zeros(3 * waves, dtype=torch.int64, device=dev)
                 per = []
                 for _ in range(3):
-                    _lib.call("fl_diag_chain_latency", kind, steps, waves, tbuf.data_ptr(), stream.cuda_stream)
+                    _lib.diag_call("fl_diag_chain_latency", kind, steps, waves, tbuf.data_ptr(), stream.cuda_stream)
                     torch.cuda.synchronize()
                     r = tbuf.view(waves, 3).cpu()
                     per.append(float(r[:, 0].double().median()) / steps)
@@ -860,7 +860,7 @@ def main():
     read_shapes = {}
     for blocks, threads, unroll in ((1024, 256, 4), (2048, 256, 4), (4096, 256, 2), (4096, 256, 4), (8192, 256, 2),
                                     (4 * B * N // 2048, 64, 2)):
-        rms = per_launch(lambda i: _lib.call("fl_diag_read_stream", xs[i % NBUF].data_ptr(), 4 * B * N, blocks,
+        rms = per_launch(lambda i: _lib.diag_call("fl_diag_read_stream", xs[i % NBUF].data_ptr(), 4 * B * N, blocks,
                                              threads, unroll, sink.data_ptr(), stream.cuda_stream))
         read_shapes[f"{blocks}x{threads}_u{unroll}"] = round(rms * 1e3, 2)
     read_us = min(read_shapes.values())
@@ -871,7 +871,7 @@ def main():
     copy_shapes = {}
     for blocks, threads, unroll in ((4 * B * N // 4096, 256, 1), (4 * B * N // 1024, 64, 1), (2048, 256, 4),
                                     (8192, 256, 2), (16384, 64, 4)):
-        cms = per_launch(lambda i: _lib.call("fl_diag_copy_stream", xs[i % NBUF].data_ptr(),
+        cms = per_launch(lambda i: _lib.diag_call("fl_diag_copy_stream", xs[i % NBUF].data_ptr(),
                                              ring[(i + 1) % NBUF].data_ptr(), 4 * B * N, blocks, threads, unroll,
                                              stream.cuda_stream))
         copy_shapes[f"{blocks}x{threads}_u{unroll}"] = round(cms * 1e3, 2)

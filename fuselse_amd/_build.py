@@ -1,9 +1,13 @@
-"""Builds the gfx950 C-ABI library ``fuselse_amd/libfuselse_amd.so`` in-tree.
+"""Builds the gfx950 C-ABI libraries in-tree.
 
-Every HIP source under ``fuselse_amd/csrc`` is compiled with hipcc for gfx950
-and linked into one shared library exporting the entry points declared in
-``include/fuselse_amd.h``.  The library links only the HIP runtime; it has no
-torch or Python dependency.
+* ``fuselse_amd/libfuselse_amd.so``: every HIP source directly under
+  ``fuselse_amd/csrc``, compiled with hipcc for gfx950 and linked into one
+  shared library exporting the entry points declared in
+  ``include/fuselse_amd.h``.  It links only the HIP runtime; it has no torch
+  or Python dependency.
+* ``fuselse_amd/libfuselse_amd_diag.so``: the measurement kernels under
+  ``fuselse_amd/csrc/diag`` (``include/fuselse_amd_diag.h``), linked against
+  the first library, whose status and error functions it uses.
 """
 
 from __future__ import annotations
@@ -19,6 +23,8 @@ REPO_DIR = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 OBJ_DIR = os.path.join(PKG_DIR, "_obj")
 LIB_PATH = os.path.join(PKG_DIR, "libfuselse_amd.so")
+DIAG_DIR = os.path.join(CSRC, "diag")
+DIAG_LIB_PATH = os.path.join(PKG_DIR, "libfuselse_amd_diag.so")
 ARCH = os.environ.get("FUSELSE_AMD_ARCH", "gfx950")
 
 COMMON_FLAGS = [
@@ -41,16 +47,17 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found; the gfx950 library cannot be built")
 
 
-def sources():
+def sources(directory=CSRC):
     out = []
-    for name in sorted(os.listdir(CSRC)):
+    for name in sorted(os.listdir(directory)):
         if name.endswith((".hip", ".cpp")):
-            out.append(os.path.join(CSRC, name))
+            out.append(os.path.join(directory, name))
     return out
 
 
 def _compile(src: str, verbose: bool) -> str:
-    obj = os.path.join(OBJ_DIR, os.path.basename(src) + ".o")
+    sub = "diag_" if os.path.dirname(src) == DIAG_DIR else ""
+    obj = os.path.join(OBJ_DIR, sub + os.path.basename(src) + ".o")
     cmd = [_hipcc(), *COMMON_FLAGS, "-c", src, "-o", obj]
     if src.endswith(".cpp"):
         cmd[1:1] = ["-x", "hip"]
@@ -66,20 +73,27 @@ def _compile(src: str, verbose: bool) -> str:
     return obj
 
 
-def build(verbose: bool = False, jobs: int = 8) -> str:
-    """Compile every source and link libfuselse_amd.so; returns its path."""
-    os.makedirs(OBJ_DIR, exist_ok=True)
-    srcs = sources()
-    with cf.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs)))) as ex:
-        objs = list(ex.map(lambda s: _compile(s, verbose), srcs))
-    tmp = LIB_PATH + ".tmp"
-    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+def _link(objs, out_path, extra, verbose):
+    tmp = out_path + ".tmp"
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, *extra, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, out_path)
+
+
+def build(verbose: bool = False, jobs: int = 8) -> str:
+    """Compile every source, link libfuselse_amd.so and libfuselse_amd_diag.so;
+    returns the first library's path."""
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    srcs = sources()
+    diag_srcs = sources(DIAG_DIR)
+    with cf.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs) + len(diag_srcs)))) as ex:
+        objs = list(ex.map(lambda s: _compile(s, verbose), srcs + diag_srcs))
+    _link(objs[:len(srcs)], LIB_PATH, [], verbose)
+    _link(objs[len(srcs):], DIAG_LIB_PATH, [f"-L{PKG_DIR}", "-lfuselse_amd", "-Wl,-rpath,$ORIGIN"], verbose)
     return LIB_PATH
 
 

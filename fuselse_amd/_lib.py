@@ -15,6 +15,8 @@ import re
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG_DIR, "libfuselse_amd.so")
 HEADER_PATH = os.path.join(os.path.dirname(PKG_DIR), "include", "fuselse_amd.h")
+DIAG_LIB_PATH = os.path.join(PKG_DIR, "libfuselse_amd_diag.so")
+DIAG_HEADER_PATH = os.path.join(os.path.dirname(PKG_DIR), "include", "fuselse_amd_diag.h")
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -43,9 +45,6 @@ SIGNATURES = {
     "fl_intlse_q16_f32": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _vp]),
     "fl_intlse_q16_i32": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _vp]),
     "fl_intlse_q10_6": (_int, [_vp, _vp, _vp, _i64, _i64, _vp]),
-    "fl_diag_read_stream": (_int, [_vp, _i64, _int, _int, _int, _vp, _vp]),
-    "fl_diag_copy_stream": (_int, [_vp, _vp, _i64, _int, _int, _int, _vp]),
-    "fl_diag_chain_latency": (_int, [_int, _int, _int, _vp, _vp]),
     "fl_sparse_csr_fwd": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _int, _vp]),
     "fl_sparse_csr_bwd": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp]),
     "fl_sparse_blocked_fwd": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _vp]),
@@ -53,7 +52,19 @@ SIGNATURES = {
                                      _vp, _vp, _vp, _vp]),
 }
 
+# the measurement library (include/fuselse_amd_diag.h)
+DIAG_SIGNATURES = {
+    "fl_diag_read_stream": (_int, [_vp, _i64, _int, _int, _int, _vp, _vp]),
+    "fl_diag_copy_stream": (_int, [_vp, _vp, _i64, _int, _int, _int, _vp]),
+    "fl_diag_chain_latency": (_int, [_int, _int, _int, _vp, _vp]),
+    "fl_diag_fwd_block_times": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
+    "fl_diag_read_rows_times": (_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
+    "fl_diag_read_stream_times": (_int, [_vp, _i64, _vp, _vp, _vp]),
+    "fl_diag_intlse_phases": (_int, [_int, _vp, _vp, _i64, _i64, _vp, _vp]),
+}
+
 _lib = None
+_diag = None
 
 
 class NativeLibraryMissing(RuntimeError):
@@ -88,6 +99,35 @@ def load():
         fn.argtypes = args
     _lib = lib
     return lib
+
+
+def load_diag():
+    """Load and type the measurement library once (it loads the main library
+    first, whose error state it shares)."""
+    global _diag
+    if _diag is not None:
+        return _diag
+    load()
+    if not os.path.exists(DIAG_LIB_PATH):
+        raise NativeLibraryMissing(f"fuselse_amd: measurement library {DIAG_LIB_PATH} is not built")
+    try:
+        lib = ctypes.CDLL(DIAG_LIB_PATH)
+    except OSError as e:
+        raise NativeLibraryMissing(f"fuselse_amd: cannot load {DIAG_LIB_PATH}: {e}") from e
+    for name, (res, args) in DIAG_SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _diag = lib
+    return lib
+
+
+def diag_call(name: str, *args) -> None:
+    """call() for an entry point of the measurement library."""
+    rc = getattr(load_diag(), name)(*args)
+    if rc != 0:
+        msg = load().fl_last_error().decode(errors="replace")
+        raise RuntimeError(msg or f"{name} failed with status {rc}")
 
 
 _bound = {}

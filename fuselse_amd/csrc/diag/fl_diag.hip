@@ -1,18 +1,22 @@
-// Bandwidth and latency references for the measurements.
+// The measurement library (libfuselse_amd_diag.so, include/fuselse_amd_diag.h):
+// bandwidth and latency references and per-block timestamps of the library's
+// kernels.  None of it has a counterpart in the reference.
 //
-// Read-bandwidth reference (no counterpart in the
-// reference): streams a buffer from HBM with the forward kernels' load form
-// (16-byte buffer loads with the nontemporal hint) in a flat grid-stride
-// order, and does nothing else with the data.  Its rate over the forward's own
-// input buffers, in the same run, is the read ceiling the forward is held
-// against.
+// Read-bandwidth reference: streams a buffer from HBM with the forward
+// kernels' load form (16-byte buffer loads with the nontemporal hint) in a
+// flat grid-stride order, and does nothing else with the data.  Its rate over
+// the forward's own input buffers, in the same run, is the read ceiling the
+// forward is held against.
 #include <stdint.h>
 
-#include "../../include/fuselse_amd.h"
-#include "fl_status.hpp"
-#include "lse_common.hpp"
-#include "lse_pair.hpp"
-#include "lse_tile_layout.hpp"
+#include "../../../include/fuselse_amd.h"
+#include "../../../include/fuselse_amd_diag.h"
+#include "../fl_status.hpp"
+#include "../lse_common.hpp"
+#include "../lse_fwd_kernels.hpp"
+#include "../lse_int_kernels.hpp"
+#include "../lse_pair.hpp"
+#include "../lse_tile_layout.hpp"
 
 namespace fl {
 
@@ -149,6 +153,139 @@ __global__ __launch_bounds__(1024) void chain_latency_kernel(int steps, uint64_t
     }
 }
 
+// ---------------------------------------------------------------------------
+// Per-block timestamps.  s_memrealtime reads the 100 MHz real-time counter,
+// s_memtime the shader clock; XCC_ID (hardware register 20) names the XCD a
+// wave runs on, HW_ID (register 4) its SIMD, CU, shader array and engine.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t rt_now() { return __builtin_amdgcn_s_memrealtime(); }
+__device__ __forceinline__ uint64_t clk_now() { return __builtin_amdgcn_s_memtime(); }
+__device__ __forceinline__ uint32_t xcc_id() { return (uint32_t)__builtin_amdgcn_s_getreg((3 << 11) | 20); }
+__device__ __forceinline__ uint32_t hw_id() { return (uint32_t)__builtin_amdgcn_s_getreg((31 << 11) | 4); }
+
+__device__ __forceinline__ void put_block_record(uint64_t* rec, int64_t i, uint64_t t0, uint64_t c0) {
+    const uint64_t t1 = rt_now();
+    const uint64_t c1 = clk_now();
+    uint64_t* r = rec + 6 * i;
+    r[0] = t0;
+    r[1] = t1;
+    r[2] = c1 - c0;
+    r[3] = xcc_id();
+    r[4] = hw_id();
+    r[5] = (uint64_t)i;
+}
+
+// The forward's row output with a record per row: begin() runs on the row's
+// first thread before its loads, end() once the row's LSE is known.
+struct TimedLseOut {
+    float* __restrict__ out;
+    uint64_t* __restrict__ rec;
+    struct Row {
+        uint64_t t0 = 0, c0 = 0;
+    };
+    __device__ __forceinline__ Row begin(int64_t) const { return {rt_now(), clk_now()}; }
+    __device__ __forceinline__ void end(int64_t row, Row r, float lse) const {
+        out[row] = lse;
+        put_block_record(rec, row, r.t0, r.c0);
+    }
+};
+
+// One 256-thread block per row, the forward's loads and software pipeline
+// (two register sets of U vectors per lane) with an xor in place of the fold.
+template <int U>
+__global__ __launch_bounds__(256) void read_rows_kernel(const float* __restrict__ x, int64_t N,
+                                                        uint64_t* __restrict__ rec, uint32_t* __restrict__ sink) {
+    constexpr int STRIDE = 256;
+    __shared__ uint32_t sh[4];
+    const uint64_t t0 = rt_now();
+    const uint64_t c0 = clk_now();
+    const int tid = threadIdx.x;
+    const int64_t row = blockIdx.x;
+    const int64_t nvec = N / 4;
+    const char* base = reinterpret_cast<const char*>(uniform64(reinterpret_cast<int64_t>(x + row * N)));
+    const int64_t region = uniform64(nvec * 16);
+    const int64_t trips = uniform64(batches<(int64_t)U * STRIDE>(nvec));
+    uint32_t acc = 0;
+    if (trips > 0) {
+        u32x4 a[U], c[U];
+        load_batch<STRIDE, U>(a, base, region, tid * 16, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        int64_t t = 1;
+        while (true) {
+            if (t == trips) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) acc ^= a[u][0] ^ a[u][1] ^ a[u][2] ^ a[u][3];
+                break;
+            }
+            load_batch<STRIDE, U>(c, base, region, tid * 16, t);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < U; ++u) acc ^= a[u][0] ^ a[u][1] ^ a[u][2] ^ a[u][3];
+            if (++t == trips) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) acc ^= c[u][0] ^ c[u][1] ^ c[u][2] ^ c[u][3];
+                break;
+            }
+            load_batch<STRIDE, U>(a, base, region, tid * 16, t);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < U; ++u) acc ^= c[u][0] ^ c[u][1] ^ c[u][2] ^ c[u][3];
+            ++t;
+        }
+    }
+    if ((tid & 63) == 0) sh[tid >> 6] = acc;
+    __syncthreads();
+    if (tid == 0) {
+        if ((sh[0] ^ sh[1] ^ sh[2] ^ sh[3]) == 0x9E3779B9u) sink[0] = acc;
+        put_block_record(rec, row, t0, c0);
+    }
+}
+
+// The flat read in one-wave 2 KB blocks with a record per block.
+__global__ __launch_bounds__(64) void read_stream_times_kernel(const char* __restrict__ x, uint64_t* __restrict__ rec,
+                                                               uint32_t* __restrict__ sink) {
+    const uint64_t t0 = rt_now();
+    const uint64_t c0 = clk_now();
+    const int64_t b = blockIdx.x;
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(x + b * 2048), 0, 2048, 0x00020000);
+    const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(r, threadIdx.x * 16, 0, kLoadStreamAux);
+    const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(r, (threadIdx.x + 64) * 16, 0, kLoadStreamAux);
+    const uint32_t acc = v0[0] ^ v0[1] ^ v0[2] ^ v0[3] ^ v1[0] ^ v1[1] ^ v1[2] ^ v1[3];
+    if (acc == 0x9E3779B9u) sink[0] = acc;
+    // every lane's loads have landed once its xor is done; the record waits
+    // for lane 0's, which retire in order with the wave's others
+    if (threadIdx.x == 0) put_block_record(rec, b, t0, c0);
+}
+
+// The IntLSE kernels' phase clock: times of the wave's own phases, recorded
+// by the block's first thread.
+struct RecClock {
+    uint64_t* rec;
+    uint64_t t0 = 0, c0 = 0, t1 = 0, t2 = 0, t3 = 0;
+    __device__ __forceinline__ void start() {
+        t0 = rt_now();
+        c0 = clk_now();
+    }
+    __device__ __forceinline__ void first() { t1 = rt_now(); }
+    __device__ __forceinline__ void chain_end() { t2 = rt_now(); }
+    __device__ __forceinline__ void tree_end() { t3 = rt_now(); }
+    __device__ __forceinline__ void done(int64_t row) {
+        if (threadIdx.x == 0) {
+            const uint64_t t4 = rt_now();
+            const uint64_t c1 = clk_now();
+            uint64_t* r = rec + 8 * row;
+            r[0] = t0;
+            r[1] = t1;
+            r[2] = t2;
+            r[3] = t3;
+            r[4] = t4;
+            r[5] = c1 - c0;
+            r[6] = xcc_id();
+            r[7] = (uint64_t)row;
+        }
+    }
+};
+
 }  // namespace fl
 
 using namespace fl;
@@ -237,5 +374,70 @@ extern "C" int fl_diag_copy_stream(const void* x, void* y, int64_t nbytes, int b
         default: copy_stream_kernel<256, 4><<<blocks, 256, 0, st>>>(xs, ys, nbytes); break;
         }
     }
+    return launch_status(name);
+}
+
+extern "C" int fl_diag_fwd_block_times(const float* x, float* out, int64_t B, int64_t N, uint64_t* rec, void* stream) {
+    const char* name = "fl_diag_fwd_block_times";
+    FL_CHECK(B >= 1 && B <= ((int64_t)1 << 24) && N >= 4 && N % 4 == 0, "%s: B in [1, 2^24], N a positive multiple of 4",
+             name);
+    FL_CHECK(x && out && rec, "%s: NULL pointer argument", name);
+    FL_CHECK((reinterpret_cast<uintptr_t>(x) & 15u) == 0, "%s: x is not 16-byte aligned", name);
+    lse_fwd_block_rows<float, true, 256, 2, true, TimedLseOut>
+        <<<dim3((unsigned)B), dim3(256), 0, reinterpret_cast<hipStream_t>(stream)>>>(x, TimedLseOut{out, rec}, B, N, 0);
+    return launch_status(name);
+}
+
+extern "C" int fl_diag_read_rows_times(const float* x, int64_t B, int64_t N, uint64_t* rec, uint32_t* sink,
+                                       void* stream) {
+    const char* name = "fl_diag_read_rows_times";
+    FL_CHECK(B >= 1 && B <= ((int64_t)1 << 24) && N >= 4 && N % 4 == 0, "%s: B in [1, 2^24], N a positive multiple of 4",
+             name);
+    FL_CHECK(x && rec && sink, "%s: NULL pointer argument", name);
+    FL_CHECK((reinterpret_cast<uintptr_t>(x) & 15u) == 0, "%s: x is not 16-byte aligned", name);
+    FL_CHECK(N * 4 < ((int64_t)1 << 31), "%s: rows of 2 GiB or more", name);
+    read_rows_kernel<2><<<dim3((unsigned)B), dim3(256), 0, reinterpret_cast<hipStream_t>(stream)>>>(x, N, rec, sink);
+    return launch_status(name);
+}
+
+extern "C" int fl_diag_read_stream_times(const void* x, int64_t nbytes, uint64_t* rec, uint32_t* sink, void* stream) {
+    const char* name = "fl_diag_read_stream_times";
+    FL_CHECK(nbytes > 0 && nbytes % 2048 == 0 && nbytes <= ((int64_t)1 << 31),
+             "%s: nbytes must be a positive multiple of 2048, at most 2^31", name);
+    FL_CHECK(x && rec && sink, "%s: NULL pointer argument", name);
+    FL_CHECK((reinterpret_cast<uintptr_t>(x) & 15u) == 0, "%s: x is not 16-byte aligned", name);
+    read_stream_times_kernel<<<dim3((unsigned)(nbytes / 2048)), dim3(64), 0, reinterpret_cast<hipStream_t>(stream)>>>(
+        static_cast<const char*>(x), rec, sink);
+    return launch_status(name);
+}
+
+extern "C" int fl_diag_intlse_phases(int kind, const void* x, float* out, int64_t B, int64_t N, uint64_t* rec,
+                                     void* stream) {
+    const char* name = "fl_diag_intlse_phases";
+    FL_CHECK(kind >= 0 && kind <= 2, "%s: kind must be 0, 1 or 2", name);
+    FL_CHECK(B >= 1 && B <= max_grid_blocks(256) && N >= 1, "%s: B in [1, %lld], N >= 1", name,
+             (long long)max_grid_blocks(256));
+    FL_CHECK(x && out && rec, "%s: NULL pointer argument", name);
+    const int64_t esize = kind == 2 ? 2 : 4;
+    FL_CHECK((reinterpret_cast<uintptr_t>(x) % esize) == 0, "%s: x is not element-aligned", name);
+    FL_CHECK(N * esize < ((int64_t)1 << 31), "%s: rows of 2 GiB or more", name);
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const dim3 g((unsigned)B);
+    const RecClock clk{rec};
+    if (kind == 0)
+        with_prefetch(B, 16, [&](auto d) {
+            intlse_q16_rows<SrcF32, true, d.value, RecClock><<<g, dim3(256), 0, st>>>(static_cast<const float*>(x), out,
+                                                                                      nullptr, N, clk);
+        });
+    else if (kind == 1)
+        with_prefetch(B, 16, [&](auto d) {
+            intlse_q16_rows<SrcI32, true, d.value, RecClock><<<g, dim3(256), 0, st>>>(static_cast<const int32_t*>(x),
+                                                                                      out, nullptr, N, clk);
+        });
+    else
+        with_prefetch(B, 8, [&](auto d) {
+            intlse_q10_6_rows<d.value, RecClock><<<g, dim3(256), 0, st>>>(static_cast<const int16_t*>(x), out, nullptr,
+                                                                          N, clk);
+        });
     return launch_status(name);
 }

@@ -85,12 +85,14 @@ int fl_lse_fwd_bf16(const void* x, float* out, int64_t B, int64_t N, int robust,
  * load the first three quarters of x (at most 240 MiB) without the
  * nontemporal hint, so part of x stays in the Infinity Cache (MI355X's 256 MB
  * memory-side cache) for the backward's read of the same rows.  For
- * training, where the backward (fl_lse_bwd_*) runs next on the same x: the
+ * a backward (fl_lse_bwd_*) that runs right after it on the same x: the
  * pair takes 2-4% less time at (512, 128256) fp32, (256, 128256) fp32 and
  * (2048, 128256) bf16, while this forward alone takes 2-5% more than
+ * fl_lse_fwd_*; with a few hundred MB of other traffic between the two the
+ * cache holds nothing of x any more and the pair is slower than with
  * fl_lse_fwd_*.  No counterpart in the reference (whose autograd forward
  * calls onepass_lse_float_robust, fused_fp32_kernel.cu:175); the drop-in
- * logsumexp uses it when autograd will run the backward.
+ * logsumexp uses it under autograd only when built with keep=True.
  * ------------------------------------------------------------------------- */
 int fl_lse_fwd_f32_keep(const float* x, float* out, int64_t B, int64_t N, int robust, void* stream);
 int fl_lse_fwd_f16_keep(const void* x, float* out, int64_t B, int64_t N, int robust, void* stream);
@@ -249,42 +251,6 @@ int fl_sparse_blocked_bwd(const float* node_flows, const float* node_mars, const
                           int params_are_log, const int64_t* csc_offsets, const int32_t* csc_edges,
                           int64_t num_elements, float* edge_flows, float* element_flows, float* param_flows,
                           void* stream);
-
-/* ---------------------------------------------------------------------------
- * Measurement aid (no counterpart in the reference): reads nbytes of x (a
- * multiple of 16, 16-byte aligned) from HBM with the forward kernels' load
- * form, 16-byte nontemporal buffer loads, in a flat grid-stride order over
- * `blocks` blocks of `threads` (64 or 256) threads with `unroll` (1, 2, 4 or
- * 8) loads per lane in flight, and nothing else.  The benchmark reports its
- * best rate over the forward's own input buffers as their read ceiling.
- * sink: one uint32 of device memory the kernel may write (it writes only for
- * a value no realistic input produces).
- * ------------------------------------------------------------------------- */
-int fl_diag_read_stream(const void* x, int64_t nbytes, int blocks, int threads, int unroll, uint32_t* sink,
-                        void* stream);
-
-/* Measurement aid (no counterpart in the reference): copies nbytes of x to y
- * (a multiple of 16, both 16-byte aligned, not overlapping) with the fused
- * backward's forms, 16-byte nontemporal buffer loads and 16-byte buffer
- * stores written through to memory, in a flat grid-stride order over
- * `blocks` blocks of `threads` (64 or 256) threads with `unroll` (1, 2 or 4)
- * vectors per lane.  The benchmark reports its best rate over the backward's
- * own buffers as their copy ceiling. */
-int fl_diag_copy_stream(const void* x, void* y, int64_t nbytes, int blocks, int threads, int unroll,
-                        void* stream);
-
-/* Measurement aid (no counterpart in the reference): one block of 64 * waves
- * threads (waves 1..16, on one CU) in which every wave runs `steps` (a
- * positive multiple of 16) dependent steps of one kind: 0 = v_add_u32, 1 = ds_read_u8 addressed by the
- * previous value, 2 = the Q10.6 pair step of fl_intlse_q10_6, 3 = the Q16.16
- * pair step with its LDS table, 4 = ds_read_b128 of the lane's own 16 bytes
- * (a conflict-free 16-byte LDS access), 5 = ds_write_b128 of the lane's own
- * 16 bytes followed by that read, 6 and 7 = the transposed 16-byte read and
- * the row-wise write+read of 64-column tiles in rows of 68 words, 8 and 9 =
- * the same in the layout the block-layout backward keeps its tiles in.  rec (device, 3 * waves uint64) receives per
- * wave: shader-clock cycles, 100 MHz real-time ticks, and the chain's final
- * value. */
-int fl_diag_chain_latency(int kind, int steps, int waves, uint64_t* rec, void* stream);
 
 #ifdef __cplusplus
 }

@@ -17,6 +17,22 @@ def test_header_symbols_exported():
     for name in declared:
         assert hasattr(lib, name), f"{name} declared in include/fuselse_amd.h but not exported"
     assert sorted(_lib.SIGNATURES) == declared
+    assert not [n for n in declared if n.startswith("fl_diag")], "measurement kernels belong to the diag library"
+
+
+def test_diag_header_symbols_exported():
+    """The measurement library exports what include/fuselse_amd_diag.h
+    declares, and the row-LSE library exports none of it."""
+    diag = _lib.load_diag()
+    declared = _lib.header_symbols(_lib.DIAG_HEADER_PATH)
+    assert declared and all(n.startswith("fl_diag_") for n in declared)
+    for name in declared:
+        assert hasattr(diag, name), f"{name} declared in include/fuselse_amd_diag.h but not exported"
+    assert sorted(_lib.DIAG_SIGNATURES) == declared
+    main = _lib.load()
+    for name in declared:
+        with pytest.raises(AttributeError):
+            getattr(main, name)
 
 
 def test_abi_version_and_error_string():
@@ -55,8 +71,12 @@ def test_invalid_arguments_rejected_without_launch():
     assert b"out is NULL" in lib.fl_last_error()
     # the read-ceiling kernel refuses a NULL buffer before building a resource
     # over it (the sink pointer is only checked for NULL on the host)
-    assert lib.fl_diag_read_stream(None, 256, 4, 64, 2, ctypes.c_void_p(256), None) == 1
+    diag = _lib.load_diag()
+    assert diag.fl_diag_read_stream(None, 256, 4, 64, 2, ctypes.c_void_p(256), None) == 1
     assert b"x is NULL" in lib.fl_last_error()
+    assert diag.fl_diag_fwd_block_times(None, None, 512, 4, None, None) == 1
+    assert diag.fl_diag_intlse_phases(3, None, None, 1, 1, None, None) == 1
+    assert b"kind" in lib.fl_last_error()
     # B == 0 is a no-op success
     assert lib.fl_lse_fwd_f32_noalloc(None, None, 0, 4, 1, None) == 0
     assert lib.fl_lse_fwd_f32(None, None, 0, 4, 1, None) == 0

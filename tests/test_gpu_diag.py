@@ -1,8 +1,11 @@
-"""The measurement kernels the bench's ceilings come from (fl_diag.hip).
+"""The measurement kernels the bench's ceilings and timings come from
+(libfuselse_amd_diag.so, fuselse_amd/csrc/diag/fl_diag.hip).
 
 They have no counterpart in the reference; these tests check that the copy
-ceiling really copies, that the read ceiling reads without writing, and that
-the latency probe runs every kind and rejects bad arguments."""
+ceiling really copies, that the read ceiling reads without writing, that the
+latency probe runs every kind and rejects bad arguments, and that the timed
+variants of the forward and IntLSE kernels give the library's own results
+with sane records."""
 import pytest
 import torch
 
@@ -14,7 +17,7 @@ def lib(cuda):
     """The library's entry points, returning their status codes."""
     from fuselse_amd import _lib
 
-    return _lib.load()
+    return _lib.load_diag()
 
 
 @pytest.mark.parametrize("threads,unroll", [(64, 1), (64, 2), (64, 4), (256, 1), (256, 2), (256, 4)])
@@ -71,3 +74,67 @@ def test_chain_latency_kinds(cuda, lib, kind):
     torch.cuda.synchronize()
     r = rec.view(waves, 3).cpu()
     assert (r[:, 0] > 256).all() and (r[:, 1] > 0).all()
+
+
+def test_fwd_block_times_is_the_forward(cuda, lib):
+    """(512, 20000) fp32 takes the 256-thread one-block-per-row geometry in
+    fl_lse_fwd_f32 too: the timed kernel's results are the same bits, and
+    every block's record is ordered and names its row and an XCD."""
+    import fuselse_amd
+
+    print("case diag fwd_block_times", flush=True)
+    B, N = 512, 20000
+    x = torch.randn(B, N, device=cuda) * 3
+    out = torch.empty(B, device=cuda)
+    rec = torch.zeros(6 * B, dtype=torch.int64, device=cuda)
+    st = torch.cuda.current_stream().cuda_stream
+    assert lib.fl_diag_fwd_block_times(x.data_ptr(), out.data_ptr(), B, N, rec.data_ptr(), st) == 0
+    assert torch.equal(out, fuselse_amd.ext.onepass_lse_float_robust(x))
+    r = rec.view(B, 6).cpu()
+    assert (r[:, 1] >= r[:, 0]).all() and (r[:, 2] > 0).all()
+    assert ((r[:, 3] >= 0) & (r[:, 3] < 16)).all()
+    assert torch.equal(r[:, 5], torch.arange(B))
+    sink = torch.zeros(1, dtype=torch.int32, device=cuda)
+    rec.zero_()
+    assert lib.fl_diag_read_rows_times(x.data_ptr(), B, N, rec.data_ptr(), sink.data_ptr(), st) == 0
+    r = rec.view(B, 6).cpu()
+    assert (r[:, 1] >= r[:, 0]).all() and torch.equal(r[:, 5], torch.arange(B))
+    nb = x.numel() * 4 // 2048
+    rec2 = torch.zeros(6 * nb, dtype=torch.int64, device=cuda)
+    assert lib.fl_diag_read_stream_times(x.data_ptr(), nb * 2048, rec2.data_ptr(), sink.data_ptr(), st) == 0
+    r = rec2.view(nb, 6).cpu()
+    assert (r[:, 1] >= r[:, 0]).all() and torch.equal(r[:, 5], torch.arange(nb))
+    assert int(sink.item()) == 0
+    assert lib.fl_diag_read_stream_times(x.data_ptr(), 1000, rec2.data_ptr(), sink.data_ptr(), st) != 0
+
+
+@pytest.mark.parametrize("kind", [0, 1, 2])
+def test_intlse_phases_is_the_kernel(cuda, lib, kind):
+    """The phase-timed IntLSE kernels give the library's results bit for bit
+    (shapes where it takes the same 256-thread kernel), and each block's
+    phases are in order."""
+    import fuselse_amd
+
+    print(f"case diag intlse_phases kind={kind}", flush=True)
+    ext = fuselse_amd.ext
+    B, N = 300, 12345
+    g = torch.Generator(device=cuda)
+    g.manual_seed(kind)
+    xf = torch.randn(B, N, device=cuda, generator=g) * 2
+    if kind == 0:
+        x, want = xf, ext.batched_logsumexp(xf)
+    elif kind == 1:
+        x = (xf * 94548.4609375).round().to(torch.int32)
+        want = ext.batched_logsumexp_q16_i32(x)
+    else:
+        x = (xf * 92.33248261689366).round().clamp(-32768, 32767).to(torch.int16)
+        want = ext.batched_logsumexp_q10_6(x)
+    out = torch.empty(B, device=cuda)
+    rec = torch.zeros(8 * B, dtype=torch.int64, device=cuda)
+    st = torch.cuda.current_stream().cuda_stream
+    assert lib.fl_diag_intlse_phases(kind, x.data_ptr(), out.data_ptr(), B, N, rec.data_ptr(), st) == 0
+    assert torch.equal(out.view(torch.int32), want.view(torch.int32))
+    r = rec.view(B, 8).cpu()
+    for a, b in ((0, 1), (1, 2), (2, 3), (3, 4)):
+        assert (r[:, b] >= r[:, a]).all(), (a, b)
+    assert (r[:, 5] > 0).all() and torch.equal(r[:, 7], torch.arange(B))
