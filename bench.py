@@ -266,6 +266,191 @@ def c5_csr_layer(torch, dev, nodes=1_000_000, batch=512, seed=11):
     return off, lp, child, d_off, d_cid, d_lp
 
 
+TICK_US = 0.01  # s_memrealtime counts a 100 MHz clock
+
+
+def _pct(v, q):
+    import numpy as np
+
+    return float(np.percentile(v, q))
+
+
+def _block_stats(rec, nrec, width, start_col, end_col, clk_col, xcc_col):
+    """Per-launch statistics of per-block records (int64 [nrec, width]):
+    times in us from the launch's first block start.  Returns the span, the
+    block-end and duration percentiles, the shader clock over the blocks
+    (median cycles per real-time us), and per XCD the block count and the
+    median and last block end."""
+    import numpy as np
+
+    r = rec.view(nrec, width).cpu().numpy()
+    t0 = r[:, start_col].min()
+    start = (r[:, start_col] - t0) * TICK_US
+    end = (r[:, end_col] - t0) * TICK_US
+    dur = end - start
+    ghz = r[:, clk_col] / np.maximum(dur, TICK_US) / 1e3
+    xcc = r[:, xcc_col]
+    per = {}
+    for k in sorted(set(xcc.tolist())):
+        e = end[xcc == k]
+        per[int(k)] = {"blocks": int(e.size), "end_med_us": round(float(np.median(e)), 2),
+                       "end_max_us": round(float(e.max()), 2), "dur_med_us": round(float(np.median(dur[xcc == k])), 2),
+                       "clock_ghz_med": round(float(np.median(ghz[xcc == k])), 3)}
+    meds = [v["end_med_us"] for v in per.values()]
+    return {"span_us": round(float(end.max()), 2), "start_p99_us": round(_pct(start, 99), 2),
+            "end_p1_us": round(_pct(end, 1), 2), "end_med_us": round(float(np.median(end)), 2),
+            "end_p99_us": round(_pct(end, 99), 2),
+            "tail_us": round(float(end.max() - np.median(end)), 2),
+            "dur_p1_us": round(_pct(dur, 1), 2), "dur_med_us": round(float(np.median(dur)), 2),
+            "dur_p99_us": round(_pct(dur, 99), 2), "clock_ghz_med": round(float(np.median(ghz)), 3),
+            "xcd_end_med_spread_us": round(max(meds) - min(meds), 2), "per_xcd": per}
+
+
+def _median_stats(launches):
+    """Median over launches of every scalar of _block_stats (per-XCD entries
+    keep their medians per XCD)."""
+    import numpy as np
+
+    out = {}
+    for k, v in launches[0].items():
+        if k == "per_xcd":
+            out[k] = {x: {f: (round(float(np.median([l[k][x][f] for l in launches if x in l[k]])), 3)
+                              if f != "blocks" else v[x][f]) for f in v[x]} for x in v}
+        else:
+            out[k] = round(float(np.median([l[k] for l in launches])), 3)
+    return out
+
+
+def measure_block_times(torch, dev, stream, launches=8):
+    """Per-block timestamps of the C2 forward and of two pure reads of the
+    same 263 MB inputs (libfuselse_amd_diag.so):
+      fwd: the robust forward in its C2 geometry (one 256-thread block per
+        row, two register sets of two vectors per lane), with a record per row;
+      rows_read: the same loads and loop with an xor in place of the fold;
+      flat_read: the flat read in one-wave 2 KB blocks in address order.
+    Each launch reads the next of four input buffers (every read from HBM).
+    Also the same kernels timed by HIP events (the product forward without
+    records beside them).  Reported per kernel: the median over launches of
+    the span (first block start to last block end), the block-end
+    percentiles, the tail (last end minus median end), and per XCD the median
+    and last block end."""
+    import fuselse_amd
+    from fuselse_amd import _lib
+
+    ext = fuselse_amd.ext
+    xs = [make_inputs(torch, dev, seed=1234 + i)[0] for i in range(4)]
+    out = torch.empty(B, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    nflat = 4 * B * N // 2048
+    every = 7  # the flat read records every 7th block (blocks rotate over the 8 XCDs)
+    st = stream.cuda_stream
+    calls = {
+        "fwd": (lambda i, rec: _lib.diag_call("fl_diag_fwd_block_times", xs[i % 4].data_ptr(), out.data_ptr(), B, N,
+                                              rec.data_ptr(), st), B),
+        "rows_read": (lambda i, rec: _lib.diag_call("fl_diag_read_rows_times", xs[i % 4].data_ptr(), B, N,
+                                                    rec.data_ptr(), sink.data_ptr(), st), B),
+        "flat_read": (lambda i, rec: _lib.diag_call("fl_diag_read_stream_times", xs[i % 4].data_ptr(), 4 * B * N,
+                                                    every, rec.data_ptr(), sink.data_ptr(), st),
+                      (nflat + every - 1) // every),
+    }
+    res = {"shape": [B, N], "launches": launches, "flat_read_record_every": every,
+           "order": "launches back to back on one stream, each into its own record buffer"}
+    for name, (fn, nrec) in calls.items():
+        recs = [torch.zeros(6 * nrec, dtype=torch.int64, device=dev) for _ in range(launches)]
+        for i in range(3):
+            fn(i, recs[0])
+        for i in range(launches):
+            fn(i, recs[i])
+        torch.cuda.synchronize()
+        res[name] = _median_stats([_block_stats(r, nrec, 6, 0, 1, 2, 3) for r in recs])
+        res[name]["event_us"] = round(_time_calls(torch, stream, lambda i: fn(i, recs[0]), 4, 50) * 1e3, 2)
+        log(f"blocktimes {name}: span {res[name]['span_us']} us, tail {res[name]['tail_us']} us, "
+            f"XCD spread {res[name]['xcd_end_med_spread_us']} us, events {res[name]['event_us']} us")
+        del recs
+    res["product_fwd_event_us"] = round(
+        _time_calls(torch, stream, lambda i: ext.onepass_lse_float_robust(xs[i % 4]), 4, 50) * 1e3, 2)
+    res["product_flat_read_event_us"] = round(_time_calls(
+        torch, stream, lambda i: _lib.diag_call("fl_diag_read_stream", xs[i % 4].data_ptr(), 4 * B * N, nflat, 64, 2,
+                                                sink.data_ptr(), st), 4, 50) * 1e3, 2)
+    rec = torch.zeros(6 * B, dtype=torch.int64, device=dev)
+    calls["fwd"][0](0, rec)
+    assert torch.equal(out, ext.onepass_lse_float_robust(xs[0])), "timed forward differs from the product forward"
+    del xs
+    return res
+
+
+def measure_intlse_phases(torch, dev, stream, gen, launches=6):
+    """Phase timestamps of the IntLSE row kernels (fl_diag_intlse_phases): per
+    block, from its start, the time until its first chunk is folded (the
+    first loads' latency), the chains, the tree and the store, and the shader
+    clock over the block (s_memtime cycles per s_memrealtime us).  Shapes: C4
+    Q10.6 (1024, 32000) from N(0, 2^2), the reference's published Q10.6
+    (512, 128256) from U(-100, 0), and C4 Q16.16 int32 (512, 128256).  Each
+    launch reads the next of enough buffers to exceed twice the Infinity
+    Cache."""
+    import numpy as np
+
+    import fuselse_amd
+    from fuselse_amd import _lib
+
+    ext = fuselse_amd.ext
+    cases = {
+        "q10_6_c4_1024x32000": (2, 1024, 32000,
+                                lambda: torch.clamp(torch.round(torch.randn(1024, 32000, device=dev, generator=gen)
+                                                                * 2 * 92.33248), -32768, 32767).to(torch.int16),
+                                ext.batched_logsumexp_q10_6),
+        "q10_6_published_512x128256": (2, 512, 128256,
+                                       lambda: (torch.rand(512, 128256, device=dev, generator=gen) * 100.0 - 100.0
+                                                ).mul(92.33248261689366).round().clamp(-32768, 32767)
+                                       .to(torch.int16), ext.batched_logsumexp_q10_6),
+        "q16_i32_c4_512x128256": (1, 512, 128256,
+                                  lambda: torch.clamp(torch.round(torch.randn(512, 128256, device=dev, generator=gen)
+                                                                  * 2 * 94548.4609375), -2 ** 31, 2 ** 31 - 1
+                                                      ).to(torch.int32), ext.batched_logsumexp_q16_i32),
+    }
+    st = stream.cuda_stream
+    res = {}
+    for name, (kind, b, n, mk, product) in cases.items():
+        nb = max(3, -(-2 * 256_000_000 // (b * n * (2 if kind == 2 else 4))) + 1)  # twice the Infinity Cache
+        bufs = [mk() for _ in range(nb)]
+        out = torch.empty(b, device=dev)
+        recs = [torch.zeros(8 * b, dtype=torch.int64, device=dev) for _ in range(launches)]
+        fn = (lambda i, rec: _lib.diag_call("fl_diag_intlse_phases", kind, bufs[i % nb].data_ptr(), out.data_ptr(), b,
+                                            n, rec.data_ptr(), st))
+        for i in range(3):
+            fn(i, recs[0])
+        for i in range(launches):
+            fn(i, recs[i])
+        torch.cuda.synchronize()
+        per = []
+        for rec in recs:
+            r = rec.view(b, 8).cpu().numpy()
+            t0 = r[:, 0].min()
+            t = (r[:, :5] - t0) * TICK_US
+            ph = {"first_chunk": t[:, 1] - t[:, 0], "chains": t[:, 2] - t[:, 1], "tree": t[:, 3] - t[:, 2],
+                  "store": t[:, 4] - t[:, 3], "block": t[:, 4] - t[:, 0]}
+            d = {f"{k}_med_us": float(np.median(v)) for k, v in ph.items()}
+            d.update({f"{k}_p99_us": _pct(v, 99) for k, v in ph.items()})
+            d["start_p99_us"] = _pct(t[:, 0], 99)
+            d["span_us"] = float(t[:, 4].max())
+            d["clock_ghz_med"] = float(np.median(r[:, 5] / np.maximum(ph["block"], TICK_US) / 1e3))
+            per.append(d)
+        s = {k: round(float(np.median([p[k] for p in per])), 3) for k in per[0]}
+        s["event_us"] = round(_time_calls(torch, stream, lambda i: fn(i, recs[0]), nb, 50) * 1e3, 2)
+        s["product_event_us"] = round(_time_calls(torch, stream, lambda i: product(bufs[i % nb]), nb, 50) * 1e3, 2)
+        s["shape"] = [b, n]
+        want = product(bufs[0])
+        fn(0, recs[0])
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int32), want.view(torch.int32)), f"{name}: timed kernel differs"
+        res[name] = s
+        log(f"phases {name}: span {s['span_us']} us, first {s['first_chunk_med_us']}, chains {s['chains_med_us']}, "
+            f"tree {s['tree_med_us']}, clock {s['clock_ghz_med']} GHz, events {s['event_us']} us "
+            f"(product {s['product_event_us']})")
+        del bufs, recs
+    return res
+
+
 def measure_configs(torch, ext, dev, stream, iters=50, only=None):
     """The other BASELINE configs: fp16/bf16 forward (C3), IntLSE Q16.16 fp32 /
     int32 and Q10.6 int16 (C4), sparse PC at 1M nodes (C5); beside them the
@@ -622,6 +807,10 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
         ms = _time_calls(torch, stream, lambda i: ext.batched_logsumexp_q10_6(q6[i % nb]), nb, iters)
         rec("C4_q10_6_i16in_1024x32000", ms, 2 * b * n + 4 * b, read_ceiling_us=read_ceiling_us(q6))
         del q6
+    if want("blocktimes"):
+        res["blocktimes_c2"] = measure_block_times(torch, dev, stream)
+    if want("phases"):
+        res["intlse_phases"] = measure_intlse_phases(torch, dev, stream, gen)
     if want("C5"):
         # C5: sparse PC, 1M sum nodes, power-law fan-in (alpha = 2) on [2, 256], batch 512
         nodes, batch = 1_000_000, 512
@@ -713,7 +902,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-configs", action="store_true", help="skip the other BASELINE configs")
     ap.add_argument("--only", default=None,
-                    help="comma-separated config groups (C3, split, sls, sweep, published, ramp, latency, C4, C5) to run alone, "
+                    help="comma-separated config groups (C3, split, sls, sweep, published, ramp, latency, C4, blocktimes, "
+                         "phases, C5) to run alone, "
                          "without the C2 "
                          "step; for profiling passes over one group")
     ap.add_argument("--copy-calib", action="store_true",
@@ -732,7 +922,8 @@ def main():
         import fuselse_amd
 
         groups = set(args.only.split(","))
-        unknown = groups - {"C3", "split", "sls", "sweep", "published", "ramp", "latency", "C4", "C5"}
+        unknown = groups - {"C3", "split", "sls", "sweep", "published", "ramp", "latency", "C4", "blocktimes", "phases",
+                            "C5"}
         if unknown:
             log(f"bench.py: unknown config groups {sorted(unknown)}")
             sys.exit(2)

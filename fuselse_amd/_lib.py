@@ -59,7 +59,7 @@ DIAG_SIGNATURES = {
     "fl_diag_chain_latency": (_int, [_int, _int, _int, _vp, _vp]),
     "fl_diag_fwd_block_times": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "fl_diag_read_rows_times": (_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
-    "fl_diag_read_stream_times": (_int, [_vp, _i64, _vp, _vp, _vp]),
+    "fl_diag_read_stream_times": (_int, [_vp, _i64, _int, _vp, _vp, _vp]),
     "fl_diag_intlse_phases": (_int, [_int, _vp, _vp, _i64, _i64, _vp, _vp]),
 }
 

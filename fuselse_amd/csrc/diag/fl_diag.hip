@@ -241,9 +241,11 @@ __global__ __launch_bounds__(256) void read_rows_kernel(const float* __restrict_
     }
 }
 
-// The flat read in one-wave 2 KB blocks with a record per block.
-__global__ __launch_bounds__(64) void read_stream_times_kernel(const char* __restrict__ x, uint64_t* __restrict__ rec,
-                                                               uint32_t* __restrict__ sink) {
+// The flat read in one-wave 2 KB blocks; blocks whose index is a multiple of
+// `every` leave a record (at index b / every).  A record costs a block about a
+// third of its lifetime, so sampling keeps the kernel's own timing.
+__global__ __launch_bounds__(64) void read_stream_times_kernel(const char* __restrict__ x, int every,
+                                                               uint64_t* __restrict__ rec, uint32_t* __restrict__ sink) {
     const uint64_t t0 = rt_now();
     const uint64_t c0 = clk_now();
     const int64_t b = blockIdx.x;
@@ -254,7 +256,10 @@ __global__ __launch_bounds__(64) void read_stream_times_kernel(const char* __res
     if (acc == 0x9E3779B9u) sink[0] = acc;
     // every lane's loads have landed once its xor is done; the record waits
     // for lane 0's, which retire in order with the wave's others
-    if (threadIdx.x == 0) put_block_record(rec, b, t0, c0);
+    if (threadIdx.x == 0 && b % every == 0) {
+        put_block_record(rec, b / every, t0, c0);
+        rec[6 * (b / every) + 5] = (uint64_t)b;
+    }
 }
 
 // The IntLSE kernels' phase clock: times of the wave's own phases, recorded
@@ -400,14 +405,16 @@ extern "C" int fl_diag_read_rows_times(const float* x, int64_t B, int64_t N, uin
     return launch_status(name);
 }
 
-extern "C" int fl_diag_read_stream_times(const void* x, int64_t nbytes, uint64_t* rec, uint32_t* sink, void* stream) {
+extern "C" int fl_diag_read_stream_times(const void* x, int64_t nbytes, int every, uint64_t* rec, uint32_t* sink,
+                                         void* stream) {
     const char* name = "fl_diag_read_stream_times";
     FL_CHECK(nbytes > 0 && nbytes % 2048 == 0 && nbytes <= ((int64_t)1 << 31),
              "%s: nbytes must be a positive multiple of 2048, at most 2^31", name);
+    FL_CHECK(every >= 1, "%s: every must be positive", name);
     FL_CHECK(x && rec && sink, "%s: NULL pointer argument", name);
     FL_CHECK((reinterpret_cast<uintptr_t>(x) & 15u) == 0, "%s: x is not 16-byte aligned", name);
     read_stream_times_kernel<<<dim3((unsigned)(nbytes / 2048)), dim3(64), 0, reinterpret_cast<hipStream_t>(stream)>>>(
-        static_cast<const char*>(x), rec, sink);
+        static_cast<const char*>(x), every, rec, sink);
     return launch_status(name);
 }
 

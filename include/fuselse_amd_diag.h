@@ -75,9 +75,11 @@ int fl_diag_read_rows_times(const float* x, int64_t B, int64_t N, uint64_t* rec,
 
 /* The flat read of fl_diag_read_stream in one-wave blocks of 2 KB (block b
  * reads bytes [2048 b, 2048 b + 2048) of x; nbytes a positive multiple of
- * 2048, at most 2^31 bytes), with the record of fl_diag_fwd_block_times per
- * block (rec: 6 uint64 per block, the last one the block index). */
-int fl_diag_read_stream_times(const void* x, int64_t nbytes, uint64_t* rec, uint32_t* sink, void* stream);
+ * 2048, at most 2^31 bytes).  Blocks whose index b is a multiple of `every`
+ * (>= 1) leave the record of fl_diag_fwd_block_times at index b / every (rec:
+ * 6 uint64 per record, ceil(nbytes / 2048 / every) records, the last field
+ * the block index b). */
+int fl_diag_read_stream_times(const void* x, int64_t nbytes, int every, uint64_t* rec, uint32_t* sink, void* stream);
 
 /* Phase timestamps of the IntLSE row kernels, as fl_intlse_q16_f32 (kind 0),
  * fl_intlse_q16_i32 (kind 1) and fl_intlse_q10_6 (kind 2) launch them for

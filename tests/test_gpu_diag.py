@@ -100,12 +100,15 @@ def test_fwd_block_times_is_the_forward(cuda, lib):
     r = rec.view(B, 6).cpu()
     assert (r[:, 1] >= r[:, 0]).all() and torch.equal(r[:, 5], torch.arange(B))
     nb = x.numel() * 4 // 2048
-    rec2 = torch.zeros(6 * nb, dtype=torch.int64, device=cuda)
-    assert lib.fl_diag_read_stream_times(x.data_ptr(), nb * 2048, rec2.data_ptr(), sink.data_ptr(), st) == 0
-    r = rec2.view(nb, 6).cpu()
-    assert (r[:, 1] >= r[:, 0]).all() and torch.equal(r[:, 5], torch.arange(nb))
+    for every in (1, 7):
+        nrec = (nb + every - 1) // every
+        rec2 = torch.zeros(6 * nrec, dtype=torch.int64, device=cuda)
+        assert lib.fl_diag_read_stream_times(x.data_ptr(), nb * 2048, every, rec2.data_ptr(), sink.data_ptr(), st) == 0
+        r = rec2.view(nrec, 6).cpu()
+        assert (r[:, 1] >= r[:, 0]).all() and torch.equal(r[:, 5], torch.arange(nrec) * every)
     assert int(sink.item()) == 0
-    assert lib.fl_diag_read_stream_times(x.data_ptr(), 1000, rec2.data_ptr(), sink.data_ptr(), st) != 0
+    assert lib.fl_diag_read_stream_times(x.data_ptr(), 1000, 1, rec2.data_ptr(), sink.data_ptr(), st) != 0
+    assert lib.fl_diag_read_stream_times(x.data_ptr(), 2048, 0, rec2.data_ptr(), sink.data_ptr(), st) != 0
 
 
 @pytest.mark.parametrize("kind", [0, 1, 2])
