@@ -471,8 +471,11 @@ def test_blocked_product_form_log_weights_empty_first_chunk(cuda):
 # of the kernels' own forward.  Bound: 1e-5 of the sum of |terms| of each
 # entry plus fp32 rounding of the final add.
 # ---------------------------------------------------------------------------
+# (32, 32, 512), (16, 64, 128), (8, 16, 64) and (4, 32, 192) have every parent,
+# edge and column of the single-pass kernel's tiles in range (its variant
+# without bound tests)
 PRODUCT_BWD_CASES = [(2, 5, 64), (16, 16, 130), (32, 32, 512), (24, 33, 96), (48, 70, 64), (64, 7, 260),
-                     (9, 40, 1), (32, 3, 3), (128, 20, 64)]
+                     (9, 40, 1), (32, 3, 3), (128, 20, 64), (16, 64, 128), (8, 16, 64), (4, 32, 192)]
 
 
 def _blocked_bwd_case(cuda, rng, nb, ne, bs, batch, nelem, log_params, special=False):
@@ -531,16 +534,17 @@ def test_blocked_backward_product_form_matches_fp64(cuda, bs, ne, batch, log_par
     _check_blocked_bwd(cuda, nids, cids, pids, params, em, bs, batch, log_params)
 
 
-@pytest.mark.parametrize("bs", [16, 32, 48])
-def test_blocked_backward_product_form_pairs_left_out(cuda, bs):
+@pytest.mark.parametrize("bs,ne,batch", [(16, 40, 68), (32, 40, 68), (48, 40, 68), (32, 32, 64), (16, 16, 128)])
+def test_blocked_backward_product_form_pairs_left_out(cuda, bs, ne, batch):
     """Pairs (parent, column) whose scale factor would pass 2^24 take the
     one-by-one terms: a parent whose only large weight meets a child ~200
     below the column maximum (held by a child of weight zero); a column where
     every child is -inf (parents of probability 0, no flow).  Block sizes 16
-    and 32 run the single-pass kernel (its second pass), 48 the two kernels."""
-    print(f"case blocked bwd product left-out pairs bs={bs}", flush=True)
+    and 32 run the single-pass kernel (its second pass; (32, 32, 64) and
+    (16, 16, 128) its variant without bound tests), 48 the two kernels."""
+    print(f"case blocked bwd product left-out pairs bs={bs} ne={ne} batch={batch}", flush=True)
     rng = np.random.default_rng(23)
-    nb, ne, batch, nelem = 3, 40, 68, 90
+    nb, nelem = 3, 90
     nids = (np.arange(nb) * bs).astype(np.int64)
     cids = np.stack([rng.permutation(nelem)[:ne] for _ in range(nb)]).astype(np.int64)
     pids = (np.arange(nb * ne, dtype=np.int64) * bs).reshape(nb, ne)
@@ -568,14 +572,15 @@ def test_blocked_backward_product_form_unaligned(cuda, offset):
     _check_blocked_bwd(cuda, nids, cids, pids, params, em, bs, batch, False)
 
 
-@pytest.mark.parametrize("bs", [48, 12])
-def test_blocked_backward_product_form_deterministic(cuda, bs):
+@pytest.mark.parametrize("bs,ne,batch", [(48, 33, 300), (12, 33, 300), (16, 32, 320)])
+def test_blocked_backward_product_form_deterministic(cuda, bs, ne, batch):
     """Element and parameter flows are the same bits on every call (block
     size 48: the two product kernels, which take blocks of more than 32
-    parents; 12: the single-pass kernel)."""
-    print(f"case blocked bwd product determinism bs={bs}", flush=True)
+    parents; 12: the single-pass kernel; (16, 32, 320): its variant without
+    bound tests)."""
+    print(f"case blocked bwd product determinism bs={bs} ne={ne} batch={batch}", flush=True)
     rng = np.random.default_rng(8)
-    nb, ne, batch, nelem = 40, 33, 300, 20        # few elements: many block edges per element
+    nb, nelem = 40, 20        # few elements: many block edges per element
     nids, cids, pids, params, em = _blocked_bwd_case(cuda, rng, nb, ne, bs, batch, nelem, False)
     d = _to(cuda, em, params, nids, cids, pids)
     nm = torch.zeros(nb * (bs + 1), batch, device=cuda)
