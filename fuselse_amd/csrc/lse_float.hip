@@ -174,15 +174,44 @@ static void launch_group(const T* x, OUT out, int64_t B, int64_t N, hipStream_t 
     lse_fwd_group_rows<T, ROBUST, LPR, U, PIPE, OUT><<<dim3((unsigned)grid), dim3(256), 0, st>>>(x, out, B, N);
 }
 
+// Dynamic LDS (bytes) for each block of a launch to reserve, unused, so that
+// at most `cap` of its blocks share a CU: a little more than a (cap + 1)-th of
+// the CU's LDS.  Read once per device; 0 (no reservation) where the device's
+// LDS size cannot be read.  The kernels' own LDS is a few words.
+constexpr int kLdsDevices = 64;
+static std::mutex g_lds_mu;
+static int g_lds_per_cu[kLdsDevices];  // guarded by g_lds_mu; 0 until read
+
+static unsigned lds_reserve_for(int cap) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kLdsDevices) return 0;
+    int lds;
+    {
+        std::lock_guard<std::mutex> lock(g_lds_mu);
+        if (g_lds_per_cu[dev] == 0) {
+            int v = 0;
+            if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess ||
+                v <= 0)
+                return 0;
+            g_lds_per_cu[dev] = v;
+        }
+        lds = g_lds_per_cu[dev];
+    }
+    const int r = lds / (cap + 1) + 64;
+    return r <= 65536 ? (unsigned)r : 0u;  // a launch's dynamic LDS stays within 64 KB
+}
+
+// cap > 0: at most `cap` blocks per CU (lds_reserve_for).
 template <typename T, bool ROBUST, int THREADS, int U, bool PIPE, typename OUT>
-static void launch_block(const T* x, OUT out, int64_t B, int64_t N, hipStream_t st, int64_t keep_rows) {
+static void launch_block(const T* x, OUT out, int64_t B, int64_t N, hipStream_t st, int64_t keep_rows, int cap = 0) {
     const int64_t grid = grid_stride_blocks(B, THREADS);
+    const unsigned lds = cap > 0 ? lds_reserve_for(cap) : 0u;
     if (keep_rows > 0)
         lse_fwd_block_rows<T, ROBUST, THREADS, U, PIPE, OUT, true>
-            <<<dim3((unsigned)grid), dim3(THREADS), 0, st>>>(x, out, B, N, keep_rows);
+            <<<dim3((unsigned)grid), dim3(THREADS), lds, st>>>(x, out, B, N, keep_rows);
     else
         lse_fwd_block_rows<T, ROBUST, THREADS, U, PIPE, OUT>
-            <<<dim3((unsigned)grid), dim3(THREADS), 0, st>>>(x, out, B, N, 0);
+            <<<dim3((unsigned)grid), dim3(THREADS), lds, st>>>(x, out, B, N, 0);
 }
 
 // Geometry and loop per shape ("vectors" = 16-byte vectors per row), from
@@ -231,12 +260,17 @@ static void launch_fwd(const T* x, OUT out, int64_t B, int64_t N, hipStream_t st
         // from 4096 rows of more than 2048 vectors, a 256-thread block per
         // row in batches of 4 (2-3% ahead of a wave per row at (4096, 32000)
         // and (8192, 24000), but 3% behind at (2048, 20000); 512 threads lose
-        // 19% at 3000 vectors); 32 lanes per row for 1025..2048 vectors (3%
-        // ahead at 2000); otherwise a wave per row.
+        // 19% at 3000 vectors), at most 3 blocks per CU: at 96 VGPRs (fp16)
+        // five fit, at 110 (bf16) four, and fewer rows streamed at once per
+        // CU measured faster (same process, us: fp16 (4096, 32000) 41.23 ->
+        // 40.33, (8192, 24000) 59.26 -> 56.51, (4096, 20000) 27.28 -> 26.59;
+        // bf16 40.82 -> 40.50 and 58.17 -> 56.39; 2 blocks 4-15% slower);
+        // 32 lanes per row for 1025..2048 vectors (3% ahead at 2000);
+        // otherwise a wave per row.
         if constexpr (!kHalf)
             launch_block<T, ROBUST, 256, 2, true, OUT>(x, out, B, N, st, keep_rows);
         else if (vecs > 2048 && B >= 4096)
-            launch_block<T, ROBUST, 256, 4, true, OUT>(x, out, B, N, st, keep_rows);
+            launch_block<T, ROBUST, 256, 4, true, OUT>(x, out, B, N, st, keep_rows, 3);
         else if (vecs > 1024 && vecs <= 2048)
             launch_group<T, ROBUST, 32, 4, true, OUT>(x, out, B, N, st);
         else
