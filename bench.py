@@ -807,6 +807,41 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
         ms = _time_calls(torch, stream, lambda i: ext.batched_logsumexp_q10_6(q6[i % nb]), nb, iters)
         rec("C4_q10_6_i16in_1024x32000", ms, 2 * b * n + 4 * b, read_ceiling_us=read_ceiling_us(q6))
         del q6
+    if want("cap"):
+        # The half forward for many mid-length rows at several caps on the
+        # blocks sharing a CU (fl_diag_half_rows_cap): as many as the registers
+        # allow (fp16 96 VGPRs: 5; bf16 110: 4), then 5..2.  The library
+        # launches the fp16 kernel with a cap of 3 and the bf16 one uncapped.
+        from fuselse_amd import _lib
+
+        caps = [0, 5, 4, 3, 2]
+        rows = {}
+        for b, n in ((4096, 32000), (8192, 24000), (4096, 20000)):
+            nb = nbuf_for(2 * b * n)
+            for tag, dtype, dt, prod in (("fp16", torch.float16, 0, ext.batched_logsumexp_fp16),
+                                         ("bf16", torch.bfloat16, 1, ext.batched_logsumexp_bf16)):
+                bufs = [(torch.randn(b, n, device=dev, generator=gen) * 2).to(dtype) for _ in range(nb)]
+                out = torch.empty(b, device=dev)
+                ref = prod(bufs[0])
+                calls = {}
+                for cap in caps:
+                    _lib.diag_call("fl_diag_half_rows_cap", dt, bufs[0].data_ptr(), out.data_ptr(), b, n, cap,
+                                   stream.cuda_stream)
+                    assert torch.equal(out, ref), f"cap {cap} differs"
+                    calls[f"cap{cap}_us" if cap else "uncapped_us"] = (
+                        lambda i, cap=cap: _lib.diag_call("fl_diag_half_rows_cap", dt, bufs[i % nb].data_ptr(),
+                                                          out.data_ptr(), b, n, cap, stream.cuda_stream))
+                calls["library_us"] = lambda i: prod(bufs[i % nb])
+                # three rounds over the variants, median per variant
+                times = {k: [] for k in calls}
+                for _ in range(3):
+                    for k, fn in calls.items():
+                        times[k].append(_time_calls(torch, stream, fn, nb, iters))
+                row = {k: round(float(np.median(v)) * 1e3, 2) for k, v in times.items()}
+                rows[f"{tag}_{b}x{n}"] = row
+                log(f"cap {tag} ({b}, {n}): {row}")
+                del bufs
+        res["half_rows_cap"] = rows
     if want("blocktimes"):
         res["blocktimes_c2"] = measure_block_times(torch, dev, stream)
     if want("phases"):
@@ -902,8 +937,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-configs", action="store_true", help="skip the other BASELINE configs")
     ap.add_argument("--only", default=None,
-                    help="comma-separated config groups (C3, split, sls, sweep, published, ramp, latency, C4, blocktimes, "
-                         "phases, C5) to run alone, "
+                    help="comma-separated config groups (C3, split, sls, sweep, published, ramp, latency, C4, cap, "
+                         "blocktimes, phases, C5) to run alone, "
                          "without the C2 "
                          "step; for profiling passes over one group")
     ap.add_argument("--copy-calib", action="store_true",
@@ -922,8 +957,8 @@ def main():
         import fuselse_amd
 
         groups = set(args.only.split(","))
-        unknown = groups - {"C3", "split", "sls", "sweep", "published", "ramp", "latency", "C4", "blocktimes", "phases",
-                            "C5"}
+        unknown = groups - {"C3", "split", "sls", "sweep", "published", "ramp", "latency", "C4", "cap", "blocktimes",
+                            "phases", "C5"}
         if unknown:
             log(f"bench.py: unknown config groups {sorted(unknown)}")
             sys.exit(2)

@@ -448,3 +448,33 @@ extern "C" int fl_diag_intlse_phases(int kind, const void* x, float* out, int64_
         });
     return launch_status(name);
 }
+
+extern "C" int fl_diag_half_rows_cap(int dtype, const void* x, float* out, int64_t B, int64_t N, int cap,
+                                     void* stream) {
+    const char* name = "fl_diag_half_rows_cap";
+    FL_CHECK(dtype == 0 || dtype == 1, "%s: dtype must be 0 (fp16) or 1 (bf16)", name);
+    FL_CHECK(cap >= 0 && cap <= 8, "%s: cap must be in [0, 8]", name);
+    FL_CHECK(B >= 1 && B <= max_grid_blocks(256) && N >= 1, "%s: B in [1, %lld], N >= 1", name,
+             (long long)max_grid_blocks(256));
+    FL_CHECK(x && out, "%s: NULL pointer argument", name);
+    FL_CHECK((reinterpret_cast<uintptr_t>(x) & 1u) == 0, "%s: x is not element-aligned", name);
+    unsigned lds = 0;
+    if (cap > 0) {
+        int dev = 0, per_cu = 0;
+        FL_CHECK(hipGetDevice(&dev) == hipSuccess &&
+                     hipDeviceGetAttribute(&per_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) ==
+                         hipSuccess &&
+                     per_cu > 0,
+                 "%s: cannot read the device's LDS per CU", name);
+        lds = (unsigned)(per_cu / (cap + 1) + 64);
+        FL_CHECK(lds <= 65536, "%s: cap %d needs %u bytes of LDS per block", name, cap, lds);
+    }
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (dtype == 0)
+        lse_fwd_block_rows<_Float16, false, 256, 4, true, LseOut><<<dim3((unsigned)B), dim3(256), lds, st>>>(
+            static_cast<const _Float16*>(x), LseOut{out}, B, N, 0);
+    else
+        lse_fwd_block_rows<bf16_t, false, 256, 4, true, LseOut><<<dim3((unsigned)B), dim3(256), lds, st>>>(
+            static_cast<const bf16_t*>(x), LseOut{out}, B, N, 0);
+    return launch_status(name);
+}

@@ -260,17 +260,20 @@ static void launch_fwd(const T* x, OUT out, int64_t B, int64_t N, hipStream_t st
         // from 4096 rows of more than 2048 vectors, a 256-thread block per
         // row in batches of 4 (2-3% ahead of a wave per row at (4096, 32000)
         // and (8192, 24000), but 3% behind at (2048, 20000); 512 threads lose
-        // 19% at 3000 vectors), at most 3 blocks per CU: at 96 VGPRs (fp16)
-        // five fit, at 110 (bf16) four, and fewer rows streamed at once per
-        // CU measured faster (same process, us: fp16 (4096, 32000) 41.23 ->
-        // 40.33, (8192, 24000) 59.26 -> 56.51, (4096, 20000) 27.28 -> 26.59;
-        // bf16 40.82 -> 40.50 and 58.17 -> 56.39; 2 blocks 4-15% slower);
-        // 32 lanes per row for 1025..2048 vectors (3% ahead at 2000);
-        // otherwise a wave per row.
+        // 19% at 3000 vectors); 32 lanes per row for 1025..2048 vectors (3%
+        // ahead at 2000); otherwise a wave per row.  The fp16 block kernel
+        // (96 VGPRs: five blocks fit a CU) runs at most 3 blocks per CU: fewer
+        // rows streamed at once per CU measured faster (medians of three
+        // rounds, us, 5 / 4 / 3 / 2 blocks: (4096, 32000) 41.16 / 40.64 /
+        // 40.49 / 42.30, (8192, 24000) 58.97 / 57.86 / 56.28 / 63.69,
+        // (4096, 20000) 27.09 / 26.60 / 26.48 / 31.33).  bf16 (110 VGPRs,
+        // four blocks) stays as it is: 3 blocks measured 0.8% and 2.6%
+        // faster at the first two shapes and 4.1% slower at the third.
         if constexpr (!kHalf)
             launch_block<T, ROBUST, 256, 2, true, OUT>(x, out, B, N, st, keep_rows);
         else if (vecs > 2048 && B >= 4096)
-            launch_block<T, ROBUST, 256, 4, true, OUT>(x, out, B, N, st, keep_rows, 3);
+            launch_block<T, ROBUST, 256, 4, true, OUT>(x, out, B, N, st, keep_rows,
+                                                       __is_same(T, _Float16) ? 3 : 0);
         else if (vecs > 1024 && vecs <= 2048)
             launch_group<T, ROBUST, 32, 4, true, OUT>(x, out, B, N, st);
         else

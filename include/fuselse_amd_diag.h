@@ -92,6 +92,16 @@ int fl_diag_read_stream_times(const void* x, int64_t nbytes, int every, uint64_t
  * shader-clock cycles from start to the result; the XCC id; the row. */
 int fl_diag_intlse_phases(int kind, const void* x, float* out, int64_t B, int64_t N, uint64_t* rec, void* stream);
 
+/* The plain half forward kernel that fl_lse_fwd_f16 (dtype 0) and
+ * fl_lse_fwd_bf16 (dtype 1) launch for many mid-length rows (one 256-thread
+ * block per row, four 16-byte vectors per lane per batch; 1 <= B <= 2^24),
+ * with unused dynamic LDS reserved so that at most `cap` blocks share a CU
+ * (cap 1..8; 0: no reservation, as many blocks as the registers allow).
+ * Writes out[B] as those calls do (same bits for every cap).  The library
+ * launches the fp16 kernel with cap 3 where it takes it, the bf16 one with
+ * no reservation. */
+int fl_diag_half_rows_cap(int dtype, const void* x, float* out, int64_t B, int64_t N, int cap, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -77,6 +77,8 @@ def test_invalid_arguments_rejected_without_launch():
     assert diag.fl_diag_fwd_block_times(None, None, 512, 4, None, None) == 1
     assert diag.fl_diag_intlse_phases(3, None, None, 1, 1, None, None) == 1
     assert b"kind" in lib.fl_last_error()
+    assert diag.fl_diag_half_rows_cap(0, None, None, 4, 8, 9, None) == 1
+    assert b"cap" in lib.fl_last_error()
     # B == 0 is a no-op success
     assert lib.fl_lse_fwd_f32_noalloc(None, None, 0, 4, 1, None) == 0
     assert lib.fl_lse_fwd_f32(None, None, 0, 4, 1, None) == 0

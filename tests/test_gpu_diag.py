@@ -141,3 +141,24 @@ def test_intlse_phases_is_the_kernel(cuda, lib, kind):
     for a, b in ((0, 1), (1, 2), (2, 3), (3, 4)):
         assert (r[:, b] >= r[:, a]).all(), (a, b)
     assert (r[:, 5] > 0).all() and torch.equal(r[:, 7], torch.arange(B))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_half_rows_cap_is_the_forward(cuda, lib, dtype):
+    """The half row kernel gives the library's results bit for bit at every
+    cap, at (4096, 20000), a shape where the library takes that kernel."""
+    import fuselse_amd
+
+    print(f"case diag half_rows_cap {dtype}", flush=True)
+    ext = fuselse_amd.ext
+    g = torch.Generator(device=cuda)
+    g.manual_seed(5)
+    B, N = 4096, 20000
+    x = (torch.randn(B, N, device=cuda, generator=g) * 2).to(dtype)
+    want = ext.batched_logsumexp_fp16(x) if dtype == torch.float16 else ext.batched_logsumexp_bf16(x)
+    st = torch.cuda.current_stream().cuda_stream
+    dt = 0 if dtype == torch.float16 else 1
+    for cap in (0, 2, 3, 4, 8):
+        out = torch.empty(B, device=cuda)
+        assert lib.fl_diag_half_rows_cap(dt, x.data_ptr(), out.data_ptr(), B, N, cap, st) == 0
+        assert torch.equal(out, want), cap
