@@ -1,6 +1,6 @@
 #!/usr/bin/env python3
 """Benchmark of the hot path: fp32 row log-sum-exp forward + fused backward at
-(B, N) = (512, 128256) on one MI355X (robust forward).
+(B, N) = (512, 128256) on one MI355X (benchmark config C2, robust forward).
 
 One step = one robust forward (lse = onepass_lse_float_robust(x)) and one
 fused backward (grad_x = onepass_lse_float_backward(g, x, lse)) over full
@@ -452,7 +452,7 @@ def measure_intlse_phases(torch, dev, stream, gen, launches=6):
 
 
 def measure_configs(torch, ext, dev, stream, iters=50, only=None):
-    """The other BASELINE configs: fp16/bf16 forward (C3), IntLSE Q16.16 fp32 /
+    """The other benchmark configs: fp16/bf16 forward (C3), IntLSE Q16.16 fp32 /
     int32 and Q10.6 int16 (C4), sparse PC at 1M nodes (C5); beside them the
     split-row forward, the selective log-softmax and the reference's own
     published (512, 128256) shapes.  Each input set rotates over enough buffers
@@ -935,7 +935,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-configs", action="store_true", help="skip the other BASELINE configs")
+    ap.add_argument("--no-configs", action="store_true", help="skip the other benchmark configs")
     ap.add_argument("--only", default=None,
                     help="comma-separated config groups (C3, split, sls, sweep, published, ramp, latency, C4, cap, "
                          "blocktimes, phases, C5) to run alone, "
@@ -1119,10 +1119,10 @@ def main():
         f"torch mul r+w {stream_ceilings['torch_mul_read_write_gbps']} GB/s, "
         f"fill {stream_ceilings['torch_fill_write_gbps']} GB/s")
 
-    # The robust forward on the BASELINE robust set (1% of rows with 10% -inf
-    # entries, an all -inf row, a +inf row, a NaN row, a row with +inf and
-    # -inf), against the plain forward on finite data (the reference claims
-    # about 3% extra time for its robust kernel, README.md:35).
+    # The robust forward on the C2 configuration's robust set (1% of rows with
+    # 10% -inf entries, an all -inf row, a +inf row, a NaN row, a row with +inf
+    # and -inf), against the plain forward on finite data (the reference claims
+    # about 3% extra time for its robust kernel, its README.md:35).
     def robust_set(x, seed):
         gen = torch.Generator(device=dev)
         gen.manual_seed(seed)

@@ -434,7 +434,7 @@ def set_omp_threads(n: int) -> None:
 
 
 # ----------------------------------------------------------------------------
-# workload recipes shared by tests and bench
+# workload recipes shared by tests and bench (the benchmark configs)
 # ----------------------------------------------------------------------------
 def make_c2_input(B=512, N=128256, seed=0, spike_frac=0.001, spike=15.0):
     """fp32 logits x ~ N(0, 3^2) with spike_frac of entries set to +15."""

@@ -73,7 +73,7 @@ def test_fwd_f32_unaligned_rows(cuda, B, N, elem_offset):
 
 
 def test_fwd_f32_c2_full_size(cuda):
-    """BASELINE C2 forward at (512, 128256): N(0, 3^2) with 0.1% +15 spikes."""
+    """Benchmark config C2 forward at (512, 128256): N(0, 3^2) with 0.1% +15 spikes."""
     print("case fwd_f32 C2 512x128256", flush=True)
     x = O.make_c2_input(512, 128256, seed=0)
     xd = torch.from_numpy(x).to(cuda)
@@ -84,7 +84,7 @@ def test_fwd_f32_c2_full_size(cuda):
 
 
 def test_bwd_f32_c2_full_size(cuda):
-    """BASELINE C2 fused backward at (512, 128256) with g ~ N(0, 1), the
+    """Benchmark config C2 fused backward at (512, 128256) with g ~ N(0, 1), the
     bench's workload (fused_fp32_kernel.cu:135-150): every element against
     g * exp(x - lse) in fp64, and each row's sum against g."""
     print("case bwd_f32 C2 512x128256", flush=True)
@@ -100,7 +100,7 @@ def test_bwd_f32_c2_full_size(cuda):
 
 
 def test_f32_c2_robust_set_full_size(cuda):
-    """BASELINE C2 robust set at (512, 128256), the shape and kernel the bench
+    """Benchmark config C2 robust set at (512, 128256), the shape and kernel the bench
     times: 1% of rows with 10% -inf entries, an all -inf row, a +inf row, a NaN
     row, a row with +inf and -inf.  Forward against fp64 and torch with
     torch.logsumexp's special values; fused backward against g * exp(x - lse)
@@ -272,7 +272,7 @@ def test_fwd_half_matches_fp64(cuda, dtype, B, N):
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("B,N,step", [(4096, 32000, 1), (2048, 128256, 7)])
 def test_fwd_half_c3_full_size(cuda, dtype, B, N, step):
-    """BASELINE C3 shapes at full size, x ~ N(0, 2^2) cast from fp32 (the bench's
+    """Benchmark config C3 shapes at full size, x ~ N(0, 2^2) cast from fp32 (the bench's
     recipe).  The kernel runs over the whole matrix; every step-th row is
     checked against fp64 of the rounded inputs (all rows at (4096, 32000))."""
     print(f"case fwd_half C3 {dtype} {B}x{N}", flush=True)
@@ -689,7 +689,7 @@ def test_rows_of_zero_and_one_elements(cuda):
 def test_fwd_keep_bit_identical(cuda, dtype, B, N):
     """fl_lse_fwd_*_keep (rows below the kept-row count load without the
     nontemporal hint) gives the bits of fl_lse_fwd_* on both sides of that
-    count, robust on the BASELINE robust set and plain on finite rows, at
+    count, robust on the C2 robust set and plain on finite rows, at
     C2, the bf16 C3 shape and the other one-block-per-row geometries (and a
     row-group shape, where the entries run the same kernel)."""
     from fuselse_amd import _lib

@@ -90,7 +90,7 @@ def test_q16_f32_special_values(cuda):
 
 @pytest.mark.parametrize("B,N", [(3, 5), (16, 4096), (512, 128256)])
 def test_q16_i32_bit_exact(cuda, B, N):
-    """BASELINE C4: Q16.16 int32 input quantised from N(0, 2^2) with saturation."""
+    """Benchmark config C4: Q16.16 int32 input quantised from N(0, 2^2) with saturation."""
     print(f"case q16_i32 B={B} N={N}", flush=True)
     rng = np.random.default_rng(B + N)
     x = (rng.standard_normal((B, N), dtype=np.float32) * np.float32(2.0))
@@ -118,7 +118,7 @@ def test_q16_i32_extreme_values(cuda):
 
 @pytest.mark.parametrize("B,N", [(2, 1), (3, 6), (9, 64), (5, 1001), (1024, 32000), (2, 128256)])
 def test_q10_6_bit_exact(cuda, B, N):
-    """BASELINE C4: Q10.6 int16 input from N(0, 2^2) through to_q10_6."""
+    """Benchmark config C4: Q10.6 int16 input from N(0, 2^2) through to_q10_6."""
     print(f"case q10_6 B={B} N={N}", flush=True)
     rng = np.random.default_rng(N)
     x = (rng.standard_normal((B, N), dtype=np.float32) * np.float32(2.0))
