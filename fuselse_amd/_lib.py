@@ -48,8 +48,8 @@ SIGNATURES = {
     "fl_sparse_csr_fwd": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _int, _vp]),
     "fl_sparse_csr_bwd": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp]),
     "fl_sparse_blocked_fwd": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _vp]),
-    "fl_sparse_blocked_bwd": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _vp, _i64,
-                                     _vp, _vp, _vp, _vp]),
+    "fl_sparse_blocked_bwd": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _vp, _vp,
+                                     _i64, _vp, _vp, _vp, _vp]),
 }
 
 # the measurement library (include/fuselse_amd_diag.h)

@@ -569,7 +569,8 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
                                                         const int64_t* __restrict__ nids,
                                                         const int64_t* __restrict__ cids,
                                                         const int64_t* __restrict__ pids, int64_t ne, int64_t bs,
-                                                        int64_t batch, int64_t chunks, int64_t items, int64_t id0) {
+                                                        int64_t batch, int64_t chunks, int64_t items, int64_t id0,
+                                                        int disjoint) {
     constexpr int MP = (NKP + 3) / 4;
     constexpr int LD = kTileLD;  // tile row; columns placed by tile_col
     constexpr int KC = NKP < 4 ? NKP : 4;
@@ -860,6 +861,13 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
     // param_flows[pids[j, e] + p] += (w / W) G + one-by-one terms, at
     // G[16*pt + 4*kq + r][c0 + 16*et + jc]; W, the row maximum over the chunk's
     // edges, is taken again from the same weights (lanes of a row hold all edges)
+    int64_t q[ET];
+#pragma unroll
+    for (int et = 0; et < ET; ++et) {
+        const int64_t e = c0 + 16 * et + jc;
+        q[et] = pids[ebase + (e < ne ? e : ne - 1)];
+    }
+    float pfv[MP][4][ET];
 #pragma unroll
     for (int pt = 0; pt < MP; ++pt)
 #pragma unroll
@@ -868,12 +876,10 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
             const bool pv = p < bs;
             const int64_t pcl = pv ? p : bs - 1;
             float wv[ET];
-            int64_t q[ET];
 #pragma unroll
             for (int et = 0; et < ET; ++et) {
                 const int64_t e = c0 + 16 * et + jc;
                 const bool ev = e < ne;
-                q[et] = pids[ebase + (ev ? e : ne - 1)];
                 const float w = weight_term<LOGP>(params[q[et] + pcl]);
                 wv[et] = ev && pv ? w : (LOGP ? -kInf : 0.0f);
             }
@@ -881,19 +887,51 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
 #pragma unroll
             for (int et = 1; et < ET; ++et) wm = fmaxf(wm, wv[et]);
             wm = row16_max(wm);
-            if (!pv) continue;
 #pragma unroll
             for (int et = 0; et < ET; ++et) {
                 const int64_t e = c0 + 16 * et + jc;
-                if (e >= ne) continue;
-                const float aw = LOGP ? (wm == -kInf ? 0.0f : fexp2((wv[et] - wm) * kLog2e)) : wv[et] / wm;
-                const float gsum = gacc[pt][et][r];
-                float v = gsum == 0.0f ? 0.0f : aw * gsum;
-                if (any_left) v += gx[p][16 * et + jc];
-                if (v != 0.0f)
-                    __hip_atomic_fetch_add(param_flows + q[et] + p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                float v = 0.0f;
+                if (pv && e < ne) {
+                    const float aw = LOGP ? (wm == -kInf ? 0.0f : fexp2((wv[et] - wm) * kLog2e)) : wv[et] / wm;
+                    const float gsum = gacc[pt][et][r];
+                    v = gsum == 0.0f ? 0.0f : aw * gsum;
+                    if (any_left) v += gx[p][16 * et + jc];
+                }
+                pfv[pt][r][et] = v;
             }
         }
+    if (disjoint) {
+        // No parameter is shared by two (block, parent, edge) triples of the
+        // layer, so this lane's cells are its own: a plain load, add and store,
+        // every load issued before the first store.  The wave covers each block
+        // edge's parents in one run, written back as whole lines.
+        float old[MP][4][ET];
+#pragma unroll
+        for (int pt = 0; pt < MP; ++pt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int et = 0; et < ET; ++et)
+                    old[pt][r][et] = pfv[pt][r][et] != 0.0f ? param_flows[q[et] + 16 * pt + 4 * kq + r] : 0.0f;
+#pragma unroll
+        for (int pt = 0; pt < MP; ++pt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int et = 0; et < ET; ++et)
+                    if (pfv[pt][r][et] != 0.0f)
+                        param_flows[q[et] + 16 * pt + 4 * kq + r] = old[pt][r][et] + pfv[pt][r][et];
+    } else {
+#pragma unroll
+        for (int pt = 0; pt < MP; ++pt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int et = 0; et < ET; ++et)
+                    if (pfv[pt][r][et] != 0.0f)
+                        __hip_atomic_fetch_add(param_flows + q[et] + 16 * pt + 4 * kq + r, pfv[pt][r][et],
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // element_flows[c, b] += sum of edge_flows rows csc_edges[csc_offsets[c] ..
@@ -1003,41 +1041,44 @@ void launch_et(float* edge_flows, float* param_flows, const float* gf, const flo
 template <int ET, int NKP, bool VEC, bool LOGP>
 void launch_fused(float* edge_flows, float* param_flows, const float* gf, const float* om, const float* xm,
                   const float* params, const int64_t* nids, const int64_t* cids, const int64_t* pids, int64_t nb,
-                  int64_t ne, int64_t bs, int64_t batch, hipStream_t st) {
+                  int64_t ne, int64_t bs, int64_t batch, int disjoint, hipStream_t st) {
     const int64_t chunks = (ne + CE - 1) / CE;
     const int64_t items = nb * chunks;
     for (int64_t id0 = 0; id0 < items; id0 += kMaxGroups) {
         const int64_t n = items - id0 < kMaxGroups ? items - id0 : kMaxGroups;
         blocked_bwd_fused<ET, NKP, VEC, LOGP><<<dim3((unsigned)((n + 7) / 8 * 8)), dim3(64), 0, st>>>(
-            edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, ne, bs, batch, chunks, items, id0);
+            edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, ne, bs, batch, chunks, items, id0, disjoint);
     }
 }
 
 template <int ET, bool VEC, bool LOGP>
 void launch_fused_et(float* edge_flows, float* param_flows, const float* gf, const float* om, const float* xm,
                      const float* params, const int64_t* nids, const int64_t* cids, const int64_t* pids, int64_t nb,
-                     int64_t ne, int64_t bs, int64_t batch, hipStream_t st) {
+                     int64_t ne, int64_t bs, int64_t batch, int disjoint, hipStream_t st) {
     if (bs <= 4)
-        launch_fused<ET, 1, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, st);
+        launch_fused<ET, 1, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, disjoint, st);
     else if (bs <= 8)
-        launch_fused<ET, 2, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, st);
+        launch_fused<ET, 2, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch,
+                                       disjoint, st);
     else if (bs <= 16)
-        launch_fused<ET, 4, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, st);
+        launch_fused<ET, 4, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch,
+                                       disjoint, st);
     else
-        launch_fused<ET, 8, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, st);
+        launch_fused<ET, 8, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch,
+                                       disjoint, st);
 }
 
 template <bool VEC, bool LOGP>
 void launch_all(float* edge_flows, float* param_flows, const float* gf, const float* om, const float* xm,
                 const float* params, const int64_t* nids, const int64_t* cids, const int64_t* pids, int64_t nb,
-                int64_t ne, int64_t bs, int64_t batch, hipStream_t st) {
+                int64_t ne, int64_t bs, int64_t batch, int disjoint, hipStream_t st) {
     if (bs <= kFusedMaxBs) {
         if (ne <= 16)
             launch_fused_et<1, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs,
-                                          batch, st);
+                                          batch, disjoint, st);
         else
             launch_fused_et<2, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs,
-                                          batch, st);
+                                          batch, disjoint, st);
     } else if (ne <= 16) {
         launch_et<1, VEC, LOGP>(edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, nb, ne, bs, batch, st);
     } else {
@@ -1055,7 +1096,7 @@ using namespace fl;
 extern "C" int fl_sparse_blocked_bwd(const float* node_flows, const float* node_mars, const float* element_mars,
                                      const float* params, const int64_t* nids, const int64_t* cids,
                                      const int64_t* pids, int64_t num_nblocks, int64_t num_edges, int64_t block_size,
-                                     int64_t batch, int params_are_log, const int64_t* csc_offsets,
+                                     int64_t batch, int params_are_log, int params_disjoint, const int64_t* csc_offsets,
                                      const int32_t* csc_edges, int64_t num_elements, float* edge_flows,
                                      float* element_flows, float* param_flows, void* stream) {
     const char* name = "fl_sparse_blocked_bwd";
@@ -1075,17 +1116,17 @@ extern "C" int fl_sparse_blocked_bwd(const float* node_flows, const float* node_
     if (vec) {
         if (params_are_log)
             sparse::launch_all<true, true>(edge_flows, param_flows, node_flows, node_mars, element_mars, params, nids,
-                                           cids, pids, nb, ne, bs, batch, st);
+                                           cids, pids, nb, ne, bs, batch, params_disjoint ? 1 : 0, st);
         else
             sparse::launch_all<true, false>(edge_flows, param_flows, node_flows, node_mars, element_mars, params,
-                                            nids, cids, pids, nb, ne, bs, batch, st);
+                                            nids, cids, pids, nb, ne, bs, batch, params_disjoint ? 1 : 0, st);
     } else {
         if (params_are_log)
             sparse::launch_all<false, true>(edge_flows, param_flows, node_flows, node_mars, element_mars, params,
-                                            nids, cids, pids, nb, ne, bs, batch, st);
+                                            nids, cids, pids, nb, ne, bs, batch, params_disjoint ? 1 : 0, st);
         else
             sparse::launch_all<false, false>(edge_flows, param_flows, node_flows, node_mars, element_mars, params,
-                                             nids, cids, pids, nb, ne, bs, batch, st);
+                                             nids, cids, pids, nb, ne, bs, batch, params_disjoint ? 1 : 0, st);
     }
     if (num_elements > 0) {
         for_grid_chunks((num_elements + 3) / 4, 256, [&](int64_t b0, int64_t nb) {

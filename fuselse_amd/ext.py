@@ -436,6 +436,9 @@ class BlockedPlan(NamedTuple):
     csc_edges: torch.Tensor     # int32 [nblocks * num_edges]: block edges j * num_edges + e, by child
     csc_nodes: Optional[torch.Tensor]  # int32, block_size 1 only: node_mars row of each listed edge
     param_ids: Optional[torch.Tensor]  # int64 [nblocks * num_edges], block_size 1 only: pids flattened
+    # no two (block, parent, edge) triples share a parameter: the ranges
+    # [pids[j, e], pids[j, e] + block_size) do not overlap
+    params_disjoint: bool = False
 
 
 def sparse_blocked_transpose(nids, cids, pids, block_size, num_elements):
@@ -474,7 +477,12 @@ def _blocked_plan(nids, cids, pids, block_size, num_elements):
         # the CSR flows kernel, which names each edge's node_mars row
         nodes = nids[order // ne].to(torch.int32)
         qids = pids.reshape(-1)
-    return BlockedPlan(csc_off, order.to(torch.int32), nodes, qids)
+    # parameter ranges of the block edges, sorted: disjoint when consecutive
+    # starts are at least block_size apart (then each parameter flow has one
+    # writer and takes a plain add instead of an atomic one)
+    starts = torch.sort(pids.reshape(-1)).values
+    disjoint = bool(starts.numel() < 2 or int((starts[1:] - starts[:-1]).min()) >= bs)
+    return BlockedPlan(csc_off, order.to(torch.int32), nodes, qids, disjoint)
 
 
 def sparse_blocked_backward(node_flows, element_flows, node_mars, element_mars, params, param_flows, nids, cids, pids,
@@ -524,7 +532,7 @@ def sparse_blocked_backward(node_flows, element_flows, node_mars, element_mars, 
            "edges, element rows and node rows must each be < 2^31")
     if plan is None:
         plan = sparse_blocked_transpose(nids, cids, pids, bs, num_el)
-    csc_off, csc_edge, csc_node, q = plan
+    csc_off, csc_edge, csc_node, q, disjoint = plan
     _check_device(node_mars, "node_mars", csc_offsets=csc_off, csc_edges=csc_edge, csc_nodes=csc_node, param_ids=q)
     _check(csc_off.dtype == torch.int64 and csc_off.numel() == num_el + 1 and csc_edge.dtype == torch.int32
            and csc_edge.numel() == nb * ne and (bs != 1 or (csc_node is not None and q is not None
@@ -546,7 +554,8 @@ def sparse_blocked_backward(node_flows, element_flows, node_mars, element_mars, 
     with _on_device(element_mars):
         _lib.call("fl_sparse_blocked_bwd", node_flows.data_ptr(), node_mars.data_ptr(), element_mars.data_ptr(),
                   params.data_ptr(), nids.data_ptr(), cids.data_ptr(), pids.data_ptr(), nb, ne, bs, batch,
-                  int(params_are_log), csc_off.data_ptr(), csc_edge.data_ptr(), num_el, edge_flows.data_ptr(),
+                  int(params_are_log), int(disjoint), csc_off.data_ptr(), csc_edge.data_ptr(), num_el,
+                  edge_flows.data_ptr(),
                   element_flows.data_ptr(), param_flows.data_ptr(), _stream(element_mars))
     return None
 

@@ -241,14 +241,16 @@ int fl_sparse_csr_bwd(const float* child, const float* out, const float* grad_ou
  * floats.  csc_offsets int64 [num_elements + 1] and csc_edges int32
  * [num_nblocks * num_edges] list, for each element row, the block edges
  * j * num_edges + e with cids[j, e] = c in increasing order.  Element flows
- * are summed in that order; param_flows takes one atomic add per
- * (block, parent, edge), so its order is free only where parameters are
- * shared.
+ * are summed in that order.  param_flows takes one add per (block, parent,
+ * edge): an atomic add, whose order is free only where parameters are
+ * shared, or, with params_disjoint (the caller's promise that the ranges
+ * [pids[j, e], pids[j, e] + block_size) do not overlap), for blocks of at
+ * most 32 parents, a plain read, add and write of each parameter.
  * ------------------------------------------------------------------------- */
 int fl_sparse_blocked_bwd(const float* node_flows, const float* node_mars, const float* element_mars,
                           const float* params, const int64_t* nids, const int64_t* cids, const int64_t* pids,
                           int64_t num_nblocks, int64_t num_edges, int64_t block_size, int64_t batch,
-                          int params_are_log, const int64_t* csc_offsets, const int32_t* csc_edges,
+                          int params_are_log, int params_disjoint, const int64_t* csc_offsets, const int32_t* csc_edges,
                           int64_t num_elements, float* edge_flows, float* element_flows, float* param_flows,
                           void* stream);
 

@@ -522,6 +522,27 @@ def _check_blocked_bwd(cuda, nids, cids, pids, params, em, bs, batch, log_params
     return got_e, got_p
 
 
+@pytest.mark.parametrize("bs,ne,batch", [(32, 32, 128), (16, 20, 70), (4, 33, 64), (48, 10, 64)])
+def test_blocked_backward_shared_parameters(cuda, bs, ne, batch):
+    """Parameters shared between block edges (overlapping ranges pids[j, e] +
+    [0, block_size)): the plan says so, and the single pass (at most 32
+    parents) and the two kernels (48) add each (block, parent, edge) sum
+    atomically, against fp64; with the layer's parameters disjoint, the plan
+    says that instead (and the single pass adds them with plain writes)."""
+    print(f"case blocked bwd shared params bs={bs} ne={ne} batch={batch}", flush=True)
+    rng = np.random.default_rng(bs + ne)
+    nb, nelem = 6, 40
+    nids, cids, pids, params, em = _blocked_bwd_case(cuda, rng, nb, ne, bs, batch, nelem, False)
+    ext = _ext()
+    d = {k: torch.from_numpy(v).to(cuda) for k, v in (("nids", nids), ("cids", cids), ("pids", pids))}
+    assert ext.sparse_blocked_transpose(d["nids"], d["cids"], d["pids"], bs, nelem).params_disjoint
+    shared = rng.integers(0, 3 * bs, (nb, ne)).astype(np.int64)     # ranges overlap and repeat
+    params = (rng.random(4 * bs) + 1e-3).astype(np.float32)
+    d["pids"] = torch.from_numpy(shared).to(cuda)
+    assert not ext.sparse_blocked_transpose(d["nids"], d["cids"], d["pids"], bs, nelem).params_disjoint
+    _check_blocked_bwd(cuda, nids, cids, shared, params, em, bs, batch, False)
+
+
 @pytest.mark.parametrize("bs,ne,batch", PRODUCT_BWD_CASES)
 @pytest.mark.parametrize("log_params", [False, True])
 def test_blocked_backward_product_form_matches_fp64(cuda, bs, ne, batch, log_params):
