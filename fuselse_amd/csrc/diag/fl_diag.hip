@@ -478,3 +478,22 @@ extern "C" int fl_diag_half_rows_cap(int dtype, const void* x, float* out, int64
             static_cast<const bf16_t*>(x), LseOut{out}, B, N, 0);
     return launch_status(name);
 }
+
+namespace {
+// one wave: lane l holds v[l]; out[l] = max_pair16(v)[l], out[64 + l] =
+// max_pair32(v)[l], out[128 + l] = max_pair32(max_pair16(v))[l]
+__global__ __launch_bounds__(64) void lane_pairs_kernel(const float* __restrict__ v, float* __restrict__ out) {
+    const int l = threadIdx.x;
+    const float x = v[l];
+    out[l] = max_pair16(x);
+    out[64 + l] = max_pair32(x);
+    out[128 + l] = max_pair32(max_pair16(x));
+}
+}  // namespace
+
+extern "C" int fl_diag_lane_pairs(const float* v, float* out, void* stream) {
+    const char* name = "fl_diag_lane_pairs";
+    FL_CHECK(v && out, "%s: NULL pointer argument", name);
+    lane_pairs_kernel<<<dim3(1), dim3(64), 0, reinterpret_cast<hipStream_t>(stream)>>>(v, out);
+    return launch_status(name);
+}

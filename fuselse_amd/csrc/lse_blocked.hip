@@ -47,8 +47,6 @@ namespace {
 constexpr int KSMAX = 8;        // K-steps of 4 edges per chunk, at most
 constexpr int KCMAX = 4 * KSMAX;  // edges per chunk, at most
 
-__device__ __forceinline__ float xor16(float v) { return exact_xor<16>(v); }
-__device__ __forceinline__ float xor32(float v) { return exact_xor<32>(v); }
 __device__ __forceinline__ float lane_read(float v, int src) {
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src * 4, __builtin_bit_cast(int, v)));
 }
@@ -129,8 +127,7 @@ __device__ __forceinline__ void fold_chunk(f32x4 (&acc)[MT][NT], float (&wm)[MT]
         float cw = w[mt][0];
 #pragma unroll
         for (int ks = 1; ks < NK; ++ks) cw = fmaxf(cw, w[mt][ks]);
-        cw = fmaxf(cw, xor16(cw));
-        cw = fmaxf(cw, xor32(cw));
+        cw = max_pair32(max_pair16(cw));
         const float nw = fmaxf(wm[mt], cw);
         if constexpr (LOGP) {
             beta[mt] = wm[mt] == -kInf ? 0.0f : fexp2((wm[mt] - nw) * kLog2e);
@@ -153,8 +150,7 @@ __device__ __forceinline__ void fold_chunk(f32x4 (&acc)[MT][NT], float (&wm)[MT]
         float cm = x[0][t];
 #pragma unroll
         for (int ks = 1; ks < NK; ++ks) cm = fmaxf(cm, x[ks][t]);
-        cm = fmaxf(cm, xor16(cm));
-        cm = fmaxf(cm, xor32(cm));
+        cm = max_pair32(max_pair16(cm));
         const float mn = fmaxf(m[t], cm);
         alpha[t] = m[t] == -kInf ? 0.0f : fexp2((m[t] - mn) * kLog2e);
         m[t] = mn;

@@ -45,8 +45,6 @@ namespace {
 constexpr int CE = 32;          // edges per chunk
 constexpr float kRMax = 16.6f;  // largest log W + m - o taken by the product
 
-__device__ __forceinline__ float xor16(float v) { return exact_xor<16>(v); }
-__device__ __forceinline__ float xor32(float v) { return exact_xor<32>(v); }
 __device__ __forceinline__ float lane_read(float v, int src) {
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src * 4, __builtin_bit_cast(int, v)));
 }
@@ -152,8 +150,7 @@ __device__ __forceinline__ void tile_x_finish(int64_t ne, int64_t c0, int kq, in
         for (int et = 0; et < ET; ++et)
 #pragma unroll
             for (int r = 0; r < 4; ++r) mu = fmaxf(mu, xv[et][r][u]);
-        mu = fmaxf(mu, xor16(mu));
-        m[u] = fmaxf(mu, xor32(mu));
+        m[u] = max_pair32(max_pair16(mu));
     }
 }
 template <int ET, bool VEC>
@@ -383,8 +380,7 @@ __global__ __launch_bounds__(64) void blocked_bwd_params(float* __restrict__ par
             const float w = weight_term<LOGP>(params[pids[ebase + (ev ? e : ne - 1)] + pcl]);
             wm = ev ? fmaxf(wm, w) : wm;
         }
-        wm = fmaxf(wm, xor16(wm));
-        wmx[pt] = fmaxf(wm, xor32(wm));
+        wmx[pt] = max_pair32(max_pair16(wm));
         lwm[pt] = LOGP ? wmx[pt] : logf(wmx[pt]);
     }
     const float* xrow[ET];

@@ -44,6 +44,24 @@ __device__ __forceinline__ float exact_xor(float v) {
     return __builtin_bit_cast(float, exact_xor<K>(__builtin_bit_cast(int, v)));
 }
 
+// Maxima across the rows of a wave: max_pair16(v) is fmaxf of v at lanes l and
+// l ^ 16, max_pair32(v) at l and l ^ 32.  gfx950's v_permlane16_swap_b32 and
+// v_permlane32_swap_b32 exchange the rows inside the VGPRs, with no LDS round
+// trip (ds_swizzle and ds_bpermute wait on the LDS unit).  With both operands
+// v, the 16-lane swap returns rows {0, 0, 2, 2} and {1, 1, 3, 3} of v and the
+// 32-lane swap halves {0, 0} and {1, 1}, so both lanes of a pair take fmaxf of
+// the same two operands in the same order and hold the same bits.
+__device__ __forceinline__ float max_pair16(float v) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto s = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return fmaxf(__builtin_bit_cast(float, (unsigned)s[0]), __builtin_bit_cast(float, (unsigned)s[1]));
+}
+__device__ __forceinline__ float max_pair32(float v) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto s = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return fmaxf(__builtin_bit_cast(float, (unsigned)s[0]), __builtin_bit_cast(float, (unsigned)s[1]));
+}
+
 // Partner exchange for commutative reductions whose operands are already
 // uniform within aligned groups of K lanes: DPP moves for K <= 8 (quad
 // permutes, then half-row and row mirrors, which pair the same groups as an

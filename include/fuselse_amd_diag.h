@@ -102,6 +102,13 @@ int fl_diag_intlse_phases(int kind, const void* x, float* out, int64_t B, int64_
  * no reservation. */
 int fl_diag_half_rows_cap(int dtype, const void* x, float* out, int64_t B, int64_t N, int cap, void* stream);
 
+/* The row-pair maxima of the block-layout kernels (max_pair16 / max_pair32
+ * in lse_common.hpp, gfx950's lane-swap moves) on one wave: v (device, 64
+ * floats, lane l's value v[l]); out (device, 192 floats) receives fmaxf of
+ * v over lanes {l, l ^ 16} at out[l], over {l, l ^ 32} at out[64 + l] and over
+ * {l, l ^ 16, l ^ 32, l ^ 48} at out[128 + l]. */
+int fl_diag_lane_pairs(const float* v, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -79,6 +79,8 @@ def test_invalid_arguments_rejected_without_launch():
     assert b"kind" in lib.fl_last_error()
     assert diag.fl_diag_half_rows_cap(0, None, None, 4, 8, 9, None) == 1
     assert b"cap" in lib.fl_last_error()
+    assert diag.fl_diag_lane_pairs(None, None, None) == 1
+    assert b"NULL" in lib.fl_last_error()
     # B == 0 is a no-op success
     assert lib.fl_lse_fwd_f32_noalloc(None, None, 0, 4, 1, None) == 0
     assert lib.fl_lse_fwd_f32(None, None, 0, 4, 1, None) == 0

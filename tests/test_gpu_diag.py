@@ -162,3 +162,36 @@ def test_half_rows_cap_is_the_forward(cuda, lib, dtype):
         out = torch.empty(B, device=cuda)
         assert lib.fl_diag_half_rows_cap(dt, x.data_ptr(), out.data_ptr(), B, N, cap, st) == 0
         assert torch.equal(out, want), cap
+
+
+def test_lane_pairs_are_row_maxima(cuda, lib):
+    """max_pair16 / max_pair32, the lane-swap maxima the block-layout kernels
+    take their column and row maxima with, pair lane l with l ^ 16 and l ^ 32.
+    The products are unchanged by the reference they are shifted by, so their
+    own tests would not notice other pairs: this checks the pairs directly,
+    on distinct values per lane (each 16-lane row's maximum at a different
+    position) and on -inf and NaN lanes, against the maxima on the host."""
+    print("case diag lane_pairs", flush=True)
+    g = torch.Generator().manual_seed(3)
+    cases = [torch.randperm(64, generator=g).float() - 20.0, torch.randn(64, generator=g)]
+    special = torch.randn(64, generator=g)
+    special[[0, 17, 33, 34, 50]] = float("-inf")
+    special[[16, 48, 49]] = float("nan")
+    special[[1, 2, 18, 35]] = torch.tensor([float("inf"), 0.0, -0.0, 7.0])
+    cases.append(special)
+    st = torch.cuda.current_stream().cuda_stream
+    lanes = torch.arange(64)
+    for v in cases:
+        out = torch.full((192,), 123.0, device=cuda)
+        assert lib.fl_diag_lane_pairs(v.to(cuda).data_ptr(), out.data_ptr(), st) == 0
+        got = out.cpu()
+
+        def fmax(a, b):  # fmaxf: a NaN operand gives the other one
+            return torch.where(a.isnan(), b, torch.where(b.isnan(), a, torch.maximum(a, b)))
+
+        p16 = fmax(v, v[lanes ^ 16])
+        p32 = fmax(v, v[lanes ^ 32])
+        p4 = fmax(p16, p16[lanes ^ 32])
+        for name, want, have in (("16", p16, got[:64]), ("32", p32, got[64:128]), ("16+32", p4, got[128:])):
+            same = (want == have) | (want.isnan() & have.isnan())
+            assert bool(same.all()), (name, v, have)
