@@ -497,3 +497,101 @@ extern "C" int fl_diag_lane_pairs(const float* v, float* out, void* stream) {
     lane_pairs_kernel<<<dim3(1), dim3(64), 0, reinterpret_cast<hipStream_t>(stream)>>>(v, out);
     return launch_status(name);
 }
+
+namespace {
+// One wave per (group of 8 * 64 / L destination rows, 4 * L-column tile), ids
+// dealt to the XCDs in contiguous ranges: lane l copies columns
+// 4 * L * ct + 4 * (l % L) .. + 3 of rows (8 * 64 / L) * g + (64 / L) * ks + l / L,
+// ks < 8, the loads of a tile issued before its first store.  With L = 16 this
+// is the block-layout forward's access pattern (child rows gathered by id,
+// 16 bytes per lane, four rows of 256 bytes per load, one block's 32 outputs
+// per wave) with no arithmetic; L = 32 and 64 read the same bytes as two rows
+// of 512 or one row of 1024 bytes per load.
+template <int L, int POL>
+__global__ __launch_bounds__(64) void gather_rows_kernel(const float* __restrict__ src,
+                                                         const int64_t* __restrict__ idx, float* __restrict__ dst,
+                                                         int64_t nrows, int64_t batch, int64_t ctiles, int64_t items,
+                                                         int64_t id0) {
+    constexpr int RI = 64 / L;  // rows per load
+    const int64_t per_xcd = gridDim.x / 8;
+    const int64_t id = id0 + (int64_t)(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (id >= items) return;
+    const int64_t ct = id % ctiles;
+    const int64_t g = id / ctiles;
+    const int l = lane_id();
+    const int64_t col = ct * 4 * L + 4 * (l % L);
+    const bool cv = col < batch;
+    f32x4 v[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+        const int64_t i = g * 8 * RI + RI * ks + l / L;
+        const int64_t row = idx[i < nrows ? i : nrows - 1];
+        const float* p = src + row * batch + (cv ? col : 0);
+        v[ks] = (POL & 1) ? load_stream<f32x4>(p) : *reinterpret_cast<const f32x4*>(p);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // the wave's destination rows as one buffer resource (stores written
+    // through to memory, sc1 nt: POL & 4)
+    const int64_t r0 = g * 8 * RI;
+    const int64_t rn = nrows - r0 < 8 * RI ? nrows - r0 : 8 * RI;
+    const __amdgpu_buffer_rsrc_t rd =
+        __builtin_amdgcn_make_buffer_rsrc(dst + r0 * batch, 0, (int)(rn * batch * 4), 0x00020000);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+        const int64_t i = g * 8 * RI + RI * ks + l / L;
+        if (i < nrows && cv) {
+            if constexpr (POL & 4)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[ks]), rd,
+                                                       (int)(((i - r0) * batch + col) * 4), 0, kStoreStreamAux);
+            else if constexpr (POL & 2)
+                store_stream(v[ks], dst + i * batch + col);
+            else
+                *reinterpret_cast<f32x4*>(dst + i * batch + col) = v[ks];
+        }
+    }
+}
+
+template <int L, int POL>
+void launch_gather_rows(const float* src, const int64_t* idx, float* dst, int64_t nrows, int64_t batch,
+                        hipStream_t st) {
+    const int64_t ctiles = (batch + 4 * L - 1) / (4 * L);
+    const int64_t items = (nrows + 8 * 64 / L - 1) / (8 * 64 / L) * ctiles;
+    constexpr int64_t kMax = max_grid_blocks(64);
+    for (int64_t id0 = 0; id0 < items; id0 += kMax) {
+        const int64_t n = items - id0 < kMax ? items - id0 : kMax;
+        gather_rows_kernel<L, POL><<<dim3((unsigned)((n + 7) / 8 * 8)), dim3(64), 0, st>>>(src, idx, dst, nrows, batch,
+                                                                                      ctiles, items, id0);
+    }
+}
+
+template <int POL>
+void launch_gather_pol(const float* src, const int64_t* idx, float* dst, int64_t nrows, int64_t batch, int lanes,
+                       hipStream_t st) {
+    if (lanes == 16) launch_gather_rows<16, POL>(src, idx, dst, nrows, batch, st);
+    else if (lanes == 32) launch_gather_rows<32, POL>(src, idx, dst, nrows, batch, st);
+    else launch_gather_rows<64, POL>(src, idx, dst, nrows, batch, st);
+}
+}  // namespace
+
+extern "C" int fl_diag_gather_rows(const float* src, const int64_t* idx, float* dst, int64_t nrows, int64_t batch,
+                                   int lanes_per_row, int policy, void* stream) {
+    const char* name = "fl_diag_gather_rows";
+    FL_CHECK(nrows >= 0 && batch >= 0, "%s: negative size", name);
+    FL_CHECK(lanes_per_row == 16 || lanes_per_row == 32 || lanes_per_row == 64, "%s: lanes_per_row must be 16, 32 or 64",
+             name);
+    if (nrows == 0 || batch == 0) return ok();
+    FL_CHECK(src && idx && dst, "%s: NULL pointer argument", name);
+    FL_CHECK(batch % 4 == 0 && ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0,
+             "%s: rows must be 16-byte vectors (batch %% 4 == 0, 16-byte aligned buffers)", name);
+    FL_CHECK(policy >= 0 && policy <= 5 && policy != 3, "%s: policy must be 0, 1, 2, 4 or 5", name);
+    FL_CHECK(batch <= ((int64_t)1 << 31) / (4 * 8 * 64), "%s: batch too large for the destination resource", name);
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    switch (policy) {
+        case 0: launch_gather_pol<0>(src, idx, dst, nrows, batch, lanes_per_row, st); break;
+        case 1: launch_gather_pol<1>(src, idx, dst, nrows, batch, lanes_per_row, st); break;
+        case 2: launch_gather_pol<2>(src, idx, dst, nrows, batch, lanes_per_row, st); break;
+        case 4: launch_gather_pol<4>(src, idx, dst, nrows, batch, lanes_per_row, st); break;
+        default: launch_gather_pol<5>(src, idx, dst, nrows, batch, lanes_per_row, st); break;
+    }
+    return launch_status(name);
+}

@@ -35,6 +35,7 @@
 // values of the robust fold (NaN wins, +inf wins, -inf is the identity).
 #include <math.h>
 #include <stdint.h>
+#include <type_traits>
 
 #include "lse_blocked.hpp"
 #include "lse_common.hpp"
@@ -190,28 +191,106 @@ __device__ __forceinline__ void load_fold(f32x4 (&acc)[MT][NT], float (&wm)[MT],
     fold_chunk<MT, NK, NT, LOGP, FIRST>(acc, wm, m, x, w, kq);
 }
 
+// True where the product cannot resolve the entry: S outside [thr, 2^100],
+// NaN and +inf included (S is a sum of products of non-negative factors, so
+// never below +0).  The floats of [thr, 2^100] are one interval of unsigned
+// bit patterns: one subtraction and one unsigned compare.
+__device__ __forceinline__ bool unresolved(float s, uint32_t lo, uint32_t span) {
+    return __builtin_bit_cast(uint32_t, s) - lo > span;
+}
+
+// Writes a tile's results, node_mars[nrow0 + p, c] = log W_p + m_c + log S, for
+// the parents and columns in range (D layout: lane l holds rows
+// p0 + 16*mt + 4*kq + r; lwm: log W in the A layout, row 16*mt + jc at lane
+// jc, so D row 16*mt + 4*kq + r reads lane 4*kq + r).  Entries the product
+// cannot resolve (rare: see the accuracy note above) are only flagged in the
+// store loop; a lane with any recomputes them by the exact online log-sum-exp
+// over the block's edges and stores them over the product's value.
+template <int MT, int NT, bool VEC, bool LOGP>
+__device__ __forceinline__ void store_tile(float* __restrict__ node_mars, const float* __restrict__ child,
+                                           const float* __restrict__ params, const int64_t* __restrict__ cids,
+                                           const int64_t* __restrict__ pids, int64_t ebase, int64_t ne, int64_t bs,
+                                           int64_t batch, int64_t nrow0, int64_t p0, int kq, int64_t col,
+                                           const f32x4 (&acc)[MT][NT], const float (&lwm)[MT],
+                                           const float (&m)[NT]) {
+    const float thr = (float)ne * 0x1p-102f;
+    const uint32_t lo = __builtin_bit_cast(uint32_t, thr);
+    const uint32_t span = __builtin_bit_cast(uint32_t, 0x1p100f) - lo;
+    static_assert(MT * 4 * NT <= 64, "one bit per held entry");
+    using Mask = typename std::conditional<MT * 4 * NT <= 32, uint32_t, uint64_t>::type;
+    Mask redo = 0;  // bit (4*mt + r)*NT + t: entry left to the exact fold
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float lwr = lane_read(lwm[mt], 4 * kq + r);
+            const int64_t p = p0 + 16 * mt + 4 * kq + r;
+            if (p >= bs) continue;
+            float* orow = node_mars + (nrow0 + p) * batch;
+#pragma unroll
+            for (int q = 0; q < NT / 4; ++q) {
+                const int64_t cq = col + 64 * q;
+                float res[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const float s = acc[mt][4 * q + u][r];
+                    res[u] = lwr + m[4 * q + u] + flog2(s) * kLn2;
+                    const bool bad = unresolved(s, lo, span) && (VEC ? cq : cq + u) < batch;
+                    redo |= bad ? (Mask)1 << ((4 * mt + r) * NT + 4 * q + u) : (Mask)0;
+                }
+                if constexpr (VEC) {
+                    if (cq < batch) store_stream(f32x4{res[0], res[1], res[2], res[3]}, orow + cq);
+                } else {
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        if (cq + u < batch) orow[cq + u] = res[u];
+                }
+            }
+        }
+    while (redo) {
+        const int bit = __builtin_ctzll((uint64_t)redo);
+        redo &= redo - 1;
+        const int mr = bit / NT, t = bit % NT;
+        const int64_t p = p0 + 16 * (mr >> 2) + 4 * kq + (mr & 3);
+        const int64_t c = col + 64 * (t >> 2) + (t & 3);
+        float mm = -kInf, ss = 0.0f;
+        for (int64_t e = 0; e < ne; ++e) {
+            const float w = params[pids[ebase + e] + p];
+            const float lw = LOGP ? w : logf(fmaxf(w, 1e-45f));
+            const float v[1] = {lw + child[cids[ebase + e] * batch + c]};
+            lse_fold<true, 1>(mm, ss, v);
+        }
+        node_mars[(nrow0 + p) * batch + c] = lse_finish<true>(mm, ss);
+    }
+}
+
 }  // namespace
 
-// One wave per (node block j, parent group g, column tile ct); logical ids
-// run ct fastest, then g, then j, and are dealt to the XCDs in contiguous
-// ranges (physical workgroup w runs on XCD w % 8), so the column tiles and
-// parent groups of one node block share an L2 for the block's weights and
-// child rows.  NK: K-steps of the single chunk when ne <= 4*NK; MULTI: any
+// Waves per SIMD the register allocation must allow: four for a single chunk
+// (the accumulators then live in VGPRs, not AGPRs: 101 registers instead of
+// 86 + 44 for 32 parents, four waves instead of three), except 64 parents
+// with 32 edges, and several chunks, whose register sets would spill at four.
+constexpr int fwd_min_waves(int mt, int nk, bool multi) { return multi || (mt == 4 && nk == 8) ? 1 : 4; }
+
+// One wave per (node block j, parent group g, column tile ct), W consecutive
+// column tiles per workgroup (wave w of workgroup cg takes ct = W*cg + w);
+// logical workgroup ids run cg fastest, then g, then j, and are dealt to the
+// XCDs in contiguous ranges (physical workgroup w runs on XCD w % 8), so the
+// column tiles and parent groups of one node block share an L2 for the
+// block's weights and child rows.  NK: K-steps of the single chunk when ne <= 4*NK; MULTI: any
 // ne, in chunks of 32 edges and a tail of 8, 16 or 32.
-template <int MT, int NK, int NT, bool MULTI, bool VEC, bool LOGP>
-__global__ __launch_bounds__(64) void blocked_mfma_kernel(float* __restrict__ node_mars,
-                                                          const float* __restrict__ child,
-                                                          const float* __restrict__ params,
-                                                          const int64_t* __restrict__ nids,
-                                                          const int64_t* __restrict__ cids,
-                                                          const int64_t* __restrict__ pids, int64_t ne, int64_t bs,
-                                                          int64_t batch, int64_t ctiles, int64_t pgroups,
-                                                          int64_t items, int64_t id0) {
+template <int MT, int NK, int NT, bool MULTI, bool VEC, bool LOGP, int W>
+__global__ __launch_bounds__(64 * W, fwd_min_waves(MT, NK, MULTI)) void blocked_mfma_kernel(
+    float* __restrict__ node_mars, const float* __restrict__ child, const float* __restrict__ params,
+    const int64_t* __restrict__ nids, const int64_t* __restrict__ cids, const int64_t* __restrict__ pids, int64_t ne,
+    int64_t bs, int64_t batch, int64_t ctiles, int64_t pgroups, int64_t items, int64_t id0) {
     const int64_t per_xcd = gridDim.x / 8;
     const int64_t id = id0 + (int64_t)(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
     if (id >= items) return;
-    const int64_t ct = id % ctiles;
-    const int64_t jg = id / ctiles;
+    const int64_t cgroups = (ctiles + W - 1) / W;
+    const int64_t ct = id % cgroups * W + (int64_t)(threadIdx.x >> 6);
+    if (ct >= ctiles) return;
+    const int64_t jg = id / cgroups;
     const int64_t g = jg % pgroups;
     const int64_t j = jg / pgroups;
     const int l = lane_id();
@@ -257,60 +336,11 @@ __global__ __launch_bounds__(64) void blocked_mfma_kernel(float* __restrict__ no
                                                    jc, col, batch);
     }
 
-    // D layout: lane l holds rows p0 + 16*mt + 4*kq + r.  Their weight maxima
-    // live in A-layout lane 4*kq + r.
-    const float thr = (float)ne * 0x1p-102f;
-    const int64_t nrow0 = nids[j];
-    static_assert(MT * 4 * NT <= 64, "one bit per held entry");
-    uint64_t redo = 0;  // bit (4*mt + r)*NT + t: entry left to the exact fold
+    float lwm[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        const float lwm = LOGP ? wm[mt] : logf(wm[mt]);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float lwr = lane_read(lwm, 4 * kq + r);
-            const int64_t p = p0 + 16 * mt + 4 * kq + r;
-            if (p >= bs) continue;
-            float* orow = node_mars + (nrow0 + p) * batch;
-#pragma unroll
-            for (int q = 0; q < NT / 4; ++q) {
-                const int64_t cq = col + 64 * q;
-                float res[4];
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const float s = acc[mt][4 * q + u][r];
-                    res[u] = lwr + m[4 * q + u] + flog2(s) * kLn2;
-                    if (!(s >= thr && s <= 0x1p100f) && cq + u < batch)
-                        redo |= (uint64_t)1 << ((4 * mt + r) * NT + 4 * q + u);
-                }
-                if constexpr (VEC) {
-                    if (cq < batch) *reinterpret_cast<f32x4*>(orow + cq) = f32x4{res[0], res[1], res[2], res[3]};
-                } else {
-#pragma unroll
-                    for (int u = 0; u < 4; ++u)
-                        if (cq + u < batch) orow[cq + u] = res[u];
-                }
-            }
-        }
-    }
-    // Entries the product cannot resolve (rare: see the accuracy note above),
-    // recomputed by the exact online log-sum-exp over the block's edges and
-    // stored over the product's value by the same lane.
-    while (redo) {
-        const int bit = __builtin_ctzll(redo);
-        redo &= redo - 1;
-        const int mr = bit / NT, t = bit % NT;
-        const int64_t p = p0 + 16 * (mr >> 2) + 4 * kq + (mr & 3);
-        const int64_t c = col + 64 * (t >> 2) + (t & 3);
-        float mm = -kInf, ss = 0.0f;
-        for (int64_t e = 0; e < ne; ++e) {
-            const float w = params[pids[ebase + e] + p];
-            const float lw = LOGP ? w : logf(fmaxf(w, 1e-45f));
-            const float v[1] = {lw + child[cids[ebase + e] * batch + c]};
-            lse_fold<true, 1>(mm, ss, v);
-        }
-        node_mars[(nrow0 + p) * batch + c] = lse_finish<true>(mm, ss);
-    }
+    for (int mt = 0; mt < MT; ++mt) lwm[mt] = LOGP ? wm[mt] : logf(wm[mt]);
+    store_tile<MT, NT, VEC, LOGP>(node_mars, child, params, cids, pids, ebase, ne, bs, batch, nids[j], p0, kq, col,
+                                  acc, lwm, m);
 }
 
 // Parents per product row group: 16, 32 or 64.  Groups of 64 suit one chunk
@@ -319,20 +349,39 @@ __global__ __launch_bounds__(64) void blocked_mfma_kernel(float* __restrict__ no
 // 475 us against 401), so those take groups of 32.
 static int blocked_mt(int64_t bs, int64_t ne) { return bs <= 16 ? 1 : bs <= 32 || ne > KCMAX ? 2 : 4; }
 
+template <int MT, int NK, int NT, bool MULTI, bool VEC, bool LOGP, int W>
+static void launch_kw(float* node_mars, const float* child, const float* params, const int64_t* nids,
+                      const int64_t* cids, const int64_t* pids, int64_t nblocks, int64_t ne, int64_t bs,
+                      int64_t batch, int64_t ctiles, hipStream_t st) {
+    const int64_t pgroups = (bs + 16 * MT - 1) / (16 * MT);
+    const int64_t items = nblocks * pgroups * ((ctiles + W - 1) / W);
+    constexpr int64_t kMax = max_grid_blocks(64 * W);  // workgroups per launch, a multiple of 8
+    for (int64_t id0 = 0; id0 < items; id0 += kMax) {
+        const int64_t n = items - id0 < kMax ? items - id0 : kMax;
+        const unsigned grid = (unsigned)((n + 7) / 8 * 8);
+        blocked_mfma_kernel<MT, NK, NT, MULTI, VEC, LOGP, W><<<dim3(grid), dim3(64 * W), 0, st>>>(
+            node_mars, child, params, nids, cids, pids, ne, bs, batch, ctiles, pgroups, items, id0);
+    }
+}
+
+// Column tiles of one (node block, parent group) go to the waves of one
+// workgroup, four at a time, so one CU reads 4 * 16 * NT consecutive columns
+// of each child row and writes them of each parent row.  The rows are
+// gathered, and a CU taking a kilobyte of a row at once instead of a quarter
+// of it reads and writes the layer's bytes 13% faster: a copy with this
+// kernel's loads and stores over the bench layer's child ids takes 159 us in
+// four-wave workgroups against 183 us in one-wave ones.
 template <int MT, int NK, int NT, bool MULTI, bool VEC, bool LOGP>
 static void launch_k(float* node_mars, const float* child, const float* params, const int64_t* nids,
                      const int64_t* cids, const int64_t* pids, int64_t nblocks, int64_t ne, int64_t bs,
                      int64_t batch, hipStream_t st) {
     const int64_t ctiles = (batch + 16 * NT - 1) / (16 * NT);
-    const int64_t pgroups = (bs + 16 * MT - 1) / (16 * MT);
-    const int64_t items = nblocks * pgroups * ctiles;
-    constexpr int64_t kMax = max_grid_blocks(64);  // workgroups per launch, a multiple of 8
-    for (int64_t id0 = 0; id0 < items; id0 += kMax) {
-        const int64_t n = items - id0 < kMax ? items - id0 : kMax;
-        const unsigned grid = (unsigned)((n + 7) / 8 * 8);
-        blocked_mfma_kernel<MT, NK, NT, MULTI, VEC, LOGP><<<dim3(grid), dim3(64), 0, st>>>(
-            node_mars, child, params, nids, cids, pids, ne, bs, batch, ctiles, pgroups, items, id0);
-    }
+    if (ctiles >= 4)
+        launch_kw<MT, NK, NT, MULTI, VEC, LOGP, 4>(node_mars, child, params, nids, cids, pids, nblocks, ne, bs, batch,
+                                                   ctiles, st);
+    else
+        launch_kw<MT, NK, NT, MULTI, VEC, LOGP, 1>(node_mars, child, params, nids, cids, pids, nblocks, ne, bs, batch,
+                                                   ctiles, st);
 }
 
 template <int MT, bool VEC, bool LOGP>

@@ -195,3 +195,23 @@ def test_lane_pairs_are_row_maxima(cuda, lib):
         for name, want, have in (("16", p16, got[:64]), ("32", p32, got[64:128]), ("16+32", p4, got[128:])):
             same = (want == have) | (want.isnan() & have.isnan())
             assert bool(same.all()), (name, v, have)
+
+
+@pytest.mark.parametrize("lanes,policy", [(16, 0), (32, 0), (64, 0), (16, 1), (16, 2), (16, 4), (64, 5)])
+@pytest.mark.parametrize("nrows,batch", [(100, 100), (64, 512), (33, 4)])
+def test_gather_rows_copies(cuda, lib, nrows, batch, lanes, policy):
+    """The gather copy writes dst[i] = src[idx[i]] for every row and column
+    (ragged row groups and column tiles) and nothing past them, at every
+    lane geometry and cache policy."""
+    print(f"case diag gather_rows {nrows}x{batch} lanes {lanes} policy {policy}", flush=True)
+    g = torch.Generator(device=cuda)
+    g.manual_seed(9)
+    src = torch.randn(300, batch, device=cuda, generator=g)
+    idx = torch.randint(0, 300, (nrows,), device=cuda, generator=g)
+    dst = torch.full((nrows + 1, batch), 5.0, device=cuda)
+    st = torch.cuda.current_stream().cuda_stream
+    assert lib.fl_diag_gather_rows(src.data_ptr(), idx.data_ptr(), dst.data_ptr(), nrows, batch, lanes, policy,
+                                   st) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(dst[:nrows], src[idx])
+    assert bool((dst[nrows] == 5.0).all())
