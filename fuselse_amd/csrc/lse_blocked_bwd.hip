@@ -746,7 +746,7 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
                 if (e >= ne) continue;
                 float* orow = edge_flows + (ebase + e) * batch;
                 if constexpr (VEC) {
-                    if (col < batch) *reinterpret_cast<f32x4*>(orow + col) = f32x4{res[0], res[1], res[2], res[3]};
+                    if (col < batch) store_stream(f32x4{res[0], res[1], res[2], res[3]}, orow + col);
                 } else {
 #pragma unroll
                     for (int u = 0; u < 4; ++u)
@@ -931,8 +931,9 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
 }
 
 // element_flows[c, b] += sum of edge_flows rows csc_edges[csc_offsets[c] ..
-// csc_offsets[c + 1]) in that order: one wave per element row, 256 columns
-// per pass.
+// csc_offsets[c + 1]) in that order: one wave per element row, 512 columns
+// per pass (two 16-byte vectors per lane, both issued before either is
+// used), the sums stored with the nontemporal hint.
 template <bool VEC>
 __global__ __launch_bounds__(256) void blocked_bwd_elements(float* __restrict__ element_flows,
                                                             const float* __restrict__ edge_flows,
@@ -946,23 +947,37 @@ __global__ __launch_bounds__(256) void blocked_bwd_elements(float* __restrict__ 
     if (k0 >= k1) return;
     const int l = lane_id();
     float* er = element_flows + c * batch;
-    for (int64_t b0 = 0; b0 < batch; b0 += 256) {
-        const int64_t col = b0 + 4 * l;
-        float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int64_t b0 = 0; b0 < batch; b0 += 512) {
+        const int64_t col[2] = {b0 + 4 * l, b0 + 256 + 4 * l};
+        float s[2][4] = {};
         for (int64_t k = k0; k < k1; ++k) {
-            float v[4];
-            ld4<VEC>(edge_flows + (int64_t)csc_edges[k] * batch, col, batch, 0.0f, v);
+            const float* row = edge_flows + (int64_t)csc_edges[k] * batch;
+            float v[2][4];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) s[u] += v[u];
+            for (int h = 0; h < 2; ++h) ld4_raw<VEC>(row, col[h], batch, v[h]);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                ld4_fill<VEC>(col[h], batch, 0.0f, v[h]);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) s[h][u] += v[h][u];
+            }
         }
-        float cur[4];
-        ld4<VEC>(er, col, batch, 0.0f, cur);
-        if constexpr (VEC) {
-            if (col < batch) *reinterpret_cast<f32x4*>(er + col) = f32x4{cur[0] + s[0], cur[1] + s[1], cur[2] + s[2], cur[3] + s[3]};
-        } else {
+        float cur[2][4];
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
-                if (col + u < batch) er[col + u] = cur[u] + s[u];
+        for (int h = 0; h < 2; ++h) ld4_raw<VEC>(er, col[h], batch, cur[h]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            ld4_fill<VEC>(col[h], batch, 0.0f, cur[h]);
+            if constexpr (VEC) {
+                if (col[h] < batch)
+                    store_stream(f32x4{cur[h][0] + s[h][0], cur[h][1] + s[h][1], cur[h][2] + s[h][2],
+                                       cur[h][3] + s[h][3]},
+                                 er + col[h]);
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (col[h] + u < batch) er[col[h] + u] = cur[h][u] + s[h][u];
+            }
         }
     }
 }
