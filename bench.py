@@ -459,6 +459,8 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
     to exceed twice the 256 MB Infinity Cache."""
     import numpy as np
 
+    from fuselse_amd import _lib
+
     res = {}
 
     def rec(name, ms, nbytes, **extra):
@@ -893,10 +895,27 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
         x_out = torch.empty(nbk * bs, batch, device=dev)
         ms_pp = _time_calls(torch, stream, lambda i: ext.sparse_csr_forward(em, x_off, x_cid, x_lp, out=x_out), 1,
                             max(5, iters // 5))
+        # ceilings of the fp32 forward's traffic, fl_diag_gather_rows over the
+        # same child ids into the same [262144, 512] rows: its own pattern
+        # (four rows of 256 bytes per load, four column-tile waves of a block
+        # per workgroup, nontemporal stores), the same in one-wave workgroups,
+        # and whole 1 KB row pieces per load
+        gidx = cids.reshape(-1).contiguous()
+        sts = stream.cuda_stream
+
+        def gather_us(lanes, waves):
+            call = lambda i: _lib.diag_call("fl_diag_gather_rows", em.data_ptr(), gidx.data_ptr(), x_out.data_ptr(),
+                                            gidx.numel(), batch, lanes, waves, 2, sts)
+            return round(_time_calls(torch, stream, call, 1, max(5, iters // 5)) * 1e3, 1)
+
+        ceil = {"gather_ceiling_us": gather_us(16, 4), "gather_1wave_us": gather_us(16, 1),
+                "gather_rows_1kb_us": gather_us(64, 1)}
+        assert torch.equal(x_out, em[gidx]), "gather copy mismatch"
         for fn, tag in [(ext.sparse_forward_float, "fp32"), (ext.sparse_forward_q16, "q16")]:
             ms = _time_calls(torch, stream, lambda i: fn(nm, em, params, nids, cids, pids, bs), 1, max(5, iters // 5))
-            extra = {"per_parent_us": round(ms_pp * 1e3, 1)} if tag == "fp32" else {}
+            extra = {"per_parent_us": round(ms_pp * 1e3, 1), **ceil} if tag == "fp32" else {}
             rec(f"C5_blocked_{tag}_8192x32_e32_b512", ms, fbytes, nnz=nbk * bs * ne, **extra)
+        ext.sparse_csr_forward(em, x_off, x_cid, x_lp, out=x_out)
         ext.sparse_forward_float(nm, em, params, nids, cids, pids, bs)
         assert torch.allclose(nm, x_out, rtol=1e-5, atol=1e-5), "block-layout product form mismatch"
         del x_cid, x_lp, x_out

@@ -499,25 +499,29 @@ extern "C" int fl_diag_lane_pairs(const float* v, float* out, void* stream) {
 }
 
 namespace {
-// One wave per (group of 8 * 64 / L destination rows, 4 * L-column tile), ids
-// dealt to the XCDs in contiguous ranges: lane l copies columns
-// 4 * L * ct + 4 * (l % L) .. + 3 of rows (8 * 64 / L) * g + (64 / L) * ks + l / L,
-// ks < 8, the loads of a tile issued before its first store.  With L = 16 this
-// is the block-layout forward's access pattern (child rows gathered by id,
-// 16 bytes per lane, four rows of 256 bytes per load, one block's 32 outputs
-// per wave) with no arithmetic; L = 32 and 64 read the same bytes as two rows
-// of 512 or one row of 1024 bytes per load.
-template <int L, int POL>
-__global__ __launch_bounds__(64) void gather_rows_kernel(const float* __restrict__ src,
-                                                         const int64_t* __restrict__ idx, float* __restrict__ dst,
-                                                         int64_t nrows, int64_t batch, int64_t ctiles, int64_t items,
-                                                         int64_t id0) {
+// One wave per (group of 8 * 64 / L destination rows, 4 * L-column tile), W
+// consecutive tiles of one row group per workgroup (wave w of workgroup cg
+// takes tile W * cg + w), workgroup ids dealt to the XCDs in contiguous
+// ranges: lane l copies columns 4 * L * ct + 4 * (l % L) .. + 3 of rows
+// (8 * 64 / L) * g + (64 / L) * ks + l / L, ks < 8, the loads of a tile issued
+// before its first store.  With L = 16 this is the block-layout forward's
+// access pattern (child rows gathered by id, 16 bytes per lane, four rows of
+// 256 bytes per load, one block's 32 outputs per wave; W = 4 as the library
+// launches it) with no arithmetic; L = 32 and 64 read the same bytes as two
+// rows of 512 or one row of 1024 bytes per load.
+template <int L, int W, int POL>
+__global__ __launch_bounds__(64 * W) void gather_rows_kernel(const float* __restrict__ src,
+                                                             const int64_t* __restrict__ idx, float* __restrict__ dst,
+                                                             int64_t nrows, int64_t batch, int64_t ctiles,
+                                                             int64_t items, int64_t id0) {
     constexpr int RI = 64 / L;  // rows per load
     const int64_t per_xcd = gridDim.x / 8;
     const int64_t id = id0 + (int64_t)(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
     if (id >= items) return;
-    const int64_t ct = id % ctiles;
-    const int64_t g = id / ctiles;
+    const int64_t cgroups = (ctiles + W - 1) / W;
+    const int64_t ct = id % cgroups * W + (int64_t)(threadIdx.x >> 6);
+    if (ct >= ctiles) return;
+    const int64_t g = id / cgroups;
     const int l = lane_id();
     const int64_t col = ct * 4 * L + 4 * (l % L);
     const bool cv = col < batch;
@@ -551,30 +555,37 @@ __global__ __launch_bounds__(64) void gather_rows_kernel(const float* __restrict
     }
 }
 
-template <int L, int POL>
+template <int L, int W, int POL>
 void launch_gather_rows(const float* src, const int64_t* idx, float* dst, int64_t nrows, int64_t batch,
                         hipStream_t st) {
     const int64_t ctiles = (batch + 4 * L - 1) / (4 * L);
-    const int64_t items = (nrows + 8 * 64 / L - 1) / (8 * 64 / L) * ctiles;
-    constexpr int64_t kMax = max_grid_blocks(64);
+    const int64_t items = (nrows + 8 * 64 / L - 1) / (8 * 64 / L) * ((ctiles + W - 1) / W);
+    constexpr int64_t kMax = max_grid_blocks(64 * W);
     for (int64_t id0 = 0; id0 < items; id0 += kMax) {
         const int64_t n = items - id0 < kMax ? items - id0 : kMax;
-        gather_rows_kernel<L, POL><<<dim3((unsigned)((n + 7) / 8 * 8)), dim3(64), 0, st>>>(src, idx, dst, nrows, batch,
-                                                                                      ctiles, items, id0);
+        gather_rows_kernel<L, W, POL><<<dim3((unsigned)((n + 7) / 8 * 8)), dim3(64 * W), 0, st>>>(
+            src, idx, dst, nrows, batch, ctiles, items, id0);
     }
+}
+
+template <int W, int POL>
+void launch_gather_lanes(const float* src, const int64_t* idx, float* dst, int64_t nrows, int64_t batch, int lanes,
+                         hipStream_t st) {
+    if (lanes == 16) launch_gather_rows<16, W, POL>(src, idx, dst, nrows, batch, st);
+    else if (lanes == 32) launch_gather_rows<32, W, POL>(src, idx, dst, nrows, batch, st);
+    else launch_gather_rows<64, W, POL>(src, idx, dst, nrows, batch, st);
 }
 
 template <int POL>
 void launch_gather_pol(const float* src, const int64_t* idx, float* dst, int64_t nrows, int64_t batch, int lanes,
-                       hipStream_t st) {
-    if (lanes == 16) launch_gather_rows<16, POL>(src, idx, dst, nrows, batch, st);
-    else if (lanes == 32) launch_gather_rows<32, POL>(src, idx, dst, nrows, batch, st);
-    else launch_gather_rows<64, POL>(src, idx, dst, nrows, batch, st);
+                       int waves, hipStream_t st) {
+    if (waves == 4) launch_gather_lanes<4, POL>(src, idx, dst, nrows, batch, lanes, st);
+    else launch_gather_lanes<1, POL>(src, idx, dst, nrows, batch, lanes, st);
 }
 }  // namespace
 
 extern "C" int fl_diag_gather_rows(const float* src, const int64_t* idx, float* dst, int64_t nrows, int64_t batch,
-                                   int lanes_per_row, int policy, void* stream) {
+                                   int lanes_per_row, int waves, int policy, void* stream) {
     const char* name = "fl_diag_gather_rows";
     FL_CHECK(nrows >= 0 && batch >= 0, "%s: negative size", name);
     FL_CHECK(lanes_per_row == 16 || lanes_per_row == 32 || lanes_per_row == 64, "%s: lanes_per_row must be 16, 32 or 64",
@@ -583,15 +594,16 @@ extern "C" int fl_diag_gather_rows(const float* src, const int64_t* idx, float* 
     FL_CHECK(src && idx && dst, "%s: NULL pointer argument", name);
     FL_CHECK(batch % 4 == 0 && ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0,
              "%s: rows must be 16-byte vectors (batch %% 4 == 0, 16-byte aligned buffers)", name);
+    FL_CHECK(waves == 1 || waves == 4, "%s: waves must be 1 or 4", name);
     FL_CHECK(policy >= 0 && policy <= 5 && policy != 3, "%s: policy must be 0, 1, 2, 4 or 5", name);
     FL_CHECK(batch <= ((int64_t)1 << 31) / (4 * 8 * 64), "%s: batch too large for the destination resource", name);
     const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     switch (policy) {
-        case 0: launch_gather_pol<0>(src, idx, dst, nrows, batch, lanes_per_row, st); break;
-        case 1: launch_gather_pol<1>(src, idx, dst, nrows, batch, lanes_per_row, st); break;
-        case 2: launch_gather_pol<2>(src, idx, dst, nrows, batch, lanes_per_row, st); break;
-        case 4: launch_gather_pol<4>(src, idx, dst, nrows, batch, lanes_per_row, st); break;
-        default: launch_gather_pol<5>(src, idx, dst, nrows, batch, lanes_per_row, st); break;
+        case 0: launch_gather_pol<0>(src, idx, dst, nrows, batch, lanes_per_row, waves, st); break;
+        case 1: launch_gather_pol<1>(src, idx, dst, nrows, batch, lanes_per_row, waves, st); break;
+        case 2: launch_gather_pol<2>(src, idx, dst, nrows, batch, lanes_per_row, waves, st); break;
+        case 4: launch_gather_pol<4>(src, idx, dst, nrows, batch, lanes_per_row, waves, st); break;
+        default: launch_gather_pol<5>(src, idx, dst, nrows, batch, lanes_per_row, waves, st); break;
     }
     return launch_status(name);
 }

@@ -155,8 +155,13 @@ __device__ __forceinline__ void fold_chunk(f32x4 (&acc)[MT][NT], float (&wm)[MT]
         const float mn = fmaxf(m[t], cm);
         alpha[t] = m[t] == -kInf ? 0.0f : fexp2((m[t] - mn) * kLog2e);
         m[t] = mn;
+        // a column of -inf (and NaN) children so far is taken relative to 0:
+        // its -inf terms are exp(-inf) = 0 and a NaN stays NaN, to reach the
+        // exact fold (a select of 0 for every term of such a column would drop
+        // a NaN that later chunks' finite children then hide)
+        const float mz = mn == -kInf ? 0.0f : mn;
 #pragma unroll
-        for (int ks = 0; ks < NK; ++ks) x[ks][t] = mn == -kInf ? 0.0f : fexp2((x[ks][t] - mn) * kLog2e);
+        for (int ks = 0; ks < NK; ++ks) x[ks][t] = fexp2((x[ks][t] - mz) * kLog2e);
     }
     if constexpr (!FIRST) {
         // D-layout row 16*mt + 4*kq + r takes the row factor of A-layout lane 4*kq + r

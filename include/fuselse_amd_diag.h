@@ -112,18 +112,18 @@ int fl_diag_lane_pairs(const float* v, float* out, void* stream);
 /* A gather copy: dst[i, :] = src[idx[i], :] for i < nrows (src, dst: fp32 rows
  * of batch columns, batch % 4 == 0, 16-byte aligned; idx: int64 [nrows],
  * valid rows of src).  Each 64-lane wave moves 16 bytes per lane of 8 * 64 / L
- * rows, L = lanes_per_row lanes on each row (16, 32 or 64): with L = 16 (four
- * rows of 256 bytes per load, 32 rows per wave) it is the access pattern of
- * the block-layout forward's single-chunk kernel without its arithmetic, so
- * its time at a layer's child ids is the ceiling of that layer's forward
- * traffic (the gathered child rows read once, the parent rows written once);
- * L = 32 and 64 read the same rows as two of 512 or one of 1024 bytes per
- * load.  policy: 0 plain loads and stores; 1 nontemporal loads (nt); 2
- * nontemporal stores; 4 stores written through to memory (sc1 nt, through a
- * buffer resource over the wave's destination rows); 5 both 1 and 4
- * (batch <= 2^20). */
+ * rows, L = lanes_per_row lanes on each row (16, 32 or 64), and `waves`
+ * (1 or 4) waves of a workgroup take neighbouring column tiles of the same
+ * rows.  With L = 16 and 4 waves (four rows of 256 bytes per load, 32 rows per
+ * wave) it is the access pattern of the block-layout forward's single-chunk
+ * kernel without its arithmetic, so its time at a layer's child ids is the
+ * ceiling of that layer's forward traffic (the gathered child rows read once,
+ * the parent rows written once).  policy: 0 plain loads and stores; 1
+ * nontemporal loads (nt); 2 nontemporal stores (the forward's); 4 stores
+ * written through to memory (sc1 nt, through a buffer resource over the
+ * wave's destination rows); 5 both 1 and 4 (batch <= 2^20). */
 int fl_diag_gather_rows(const float* src, const int64_t* idx, float* dst, int64_t nrows, int64_t batch,
-                        int lanes_per_row, int policy, void* stream);
+                        int lanes_per_row, int waves, int policy, void* stream);
 
 #ifdef __cplusplus
 }

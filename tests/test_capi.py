@@ -81,15 +81,16 @@ def test_invalid_arguments_rejected_without_launch():
     assert b"cap" in lib.fl_last_error()
     assert diag.fl_diag_lane_pairs(None, None, None) == 1
     assert b"NULL" in lib.fl_last_error()
-    assert diag.fl_diag_gather_rows(None, None, None, 4, 8, 16, 0, None) == 1
+    assert diag.fl_diag_gather_rows(None, None, None, 4, 8, 16, 1, 0, None) == 1
     assert b"NULL" in lib.fl_last_error()
-    assert diag.fl_diag_gather_rows(ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 4, 6, 16, 0,
-                                    None) == 1
-    assert b"16-byte" in lib.fl_last_error()
-    assert diag.fl_diag_gather_rows(None, None, None, 4, 8, 8, 0, None) == 1
-    assert b"lanes_per_row" in lib.fl_last_error()
     vp = ctypes.c_void_p(256)
-    assert diag.fl_diag_gather_rows(vp, vp, vp, 4, 8, 16, 3, None) == 1
+    assert diag.fl_diag_gather_rows(vp, vp, vp, 4, 6, 16, 1, 0, None) == 1
+    assert b"16-byte" in lib.fl_last_error()
+    assert diag.fl_diag_gather_rows(None, None, None, 4, 8, 8, 1, 0, None) == 1
+    assert b"lanes_per_row" in lib.fl_last_error()
+    assert diag.fl_diag_gather_rows(vp, vp, vp, 4, 8, 16, 2, 0, None) == 1
+    assert b"waves" in lib.fl_last_error()
+    assert diag.fl_diag_gather_rows(vp, vp, vp, 4, 8, 16, 1, 3, None) == 1
     assert b"policy" in lib.fl_last_error()
     # B == 0 is a no-op success
     assert lib.fl_lse_fwd_f32_noalloc(None, None, 0, 4, 1, None) == 0

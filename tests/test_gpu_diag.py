@@ -197,21 +197,24 @@ def test_lane_pairs_are_row_maxima(cuda, lib):
             assert bool(same.all()), (name, v, have)
 
 
-@pytest.mark.parametrize("lanes,policy", [(16, 0), (32, 0), (64, 0), (16, 1), (16, 2), (16, 4), (64, 5)])
-@pytest.mark.parametrize("nrows,batch", [(100, 100), (64, 512), (33, 4)])
-def test_gather_rows_copies(cuda, lib, nrows, batch, lanes, policy):
+@pytest.mark.parametrize("lanes,waves,policy",
+                         [(16, 1, 0), (32, 1, 0), (64, 1, 0), (16, 1, 1), (16, 1, 2), (16, 1, 4), (64, 1, 5),
+                          (16, 4, 2), (64, 4, 0)])
+@pytest.mark.parametrize("nrows,batch", [(100, 100), (64, 512), (33, 4), (40, 1000)])
+def test_gather_rows_copies(cuda, lib, nrows, batch, lanes, waves, policy):
     """The gather copy writes dst[i] = src[idx[i]] for every row and column
-    (ragged row groups and column tiles) and nothing past them, at every
-    lane geometry and cache policy."""
-    print(f"case diag gather_rows {nrows}x{batch} lanes {lanes} policy {policy}", flush=True)
+    (ragged row groups and column tiles, workgroups with idle waves) and
+    nothing past them, at every lane geometry, workgroup size and cache
+    policy."""
+    print(f"case diag gather_rows {nrows}x{batch} lanes {lanes} waves {waves} policy {policy}", flush=True)
     g = torch.Generator(device=cuda)
     g.manual_seed(9)
     src = torch.randn(300, batch, device=cuda, generator=g)
     idx = torch.randint(0, 300, (nrows,), device=cuda, generator=g)
     dst = torch.full((nrows + 1, batch), 5.0, device=cuda)
     st = torch.cuda.current_stream().cuda_stream
-    assert lib.fl_diag_gather_rows(src.data_ptr(), idx.data_ptr(), dst.data_ptr(), nrows, batch, lanes, policy,
-                                   st) == 0
+    assert lib.fl_diag_gather_rows(src.data_ptr(), idx.data_ptr(), dst.data_ptr(), nrows, batch, lanes, waves,
+                                   policy, st) == 0
     torch.cuda.synchronize()
     assert torch.equal(dst[:nrows], src[idx])
     assert bool((dst[nrows] == 5.0).all())

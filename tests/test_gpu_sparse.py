@@ -384,8 +384,9 @@ def test_blocked_product_form_matches_fp64(cuda, bs, ne, batch, log_params):
 
 def test_blocked_product_form_special_values_and_fallback(cuda):
     """Entries the product cannot resolve take the exact fold: -inf children,
-    columns of -inf, +inf and NaN children, zero weights, a parent whose only
-    large weights meet children ~200 nats below the column maximum."""
+    columns of -inf, +inf and NaN children (a NaN among -inf children of the
+    first 32-edge chunk included), zero weights, a parent whose only large
+    weights meet children ~200 nats below the column maximum."""
     print("case blocked product special values", flush=True)
     rng = np.random.default_rng(5)
     nb, ne, bs, batch, nelem = 3, 40, 16, 68, 60
@@ -398,6 +399,10 @@ def test_blocked_product_form_special_values_and_fallback(cuda):
     em[:, 5] = -np.inf                           # a column where every child is -inf
     em[cids[1, 0], 7] = np.inf                   # +inf wins
     em[cids[2, 1], 9] = np.nan                   # NaN wins
+    # block 0, column 11: the first 32-edge chunk all -inf but one NaN, the
+    # last 8 edges finite: the NaN still wins
+    em[cids[0, :32], 11] = -np.inf
+    em[cids[0, 4], 11] = np.nan
     params[pids[0, :] + 2] = 0.0                 # parent 2 of block 0: every weight zero
     params[pids[1, 5] + 4] = 0.0                 # one zero weight
     # block 2, parent 6: weight ~1 only on edge 0, whose child sits 200 below
@@ -416,6 +421,7 @@ def test_blocked_product_form_special_values_and_fallback(cuda):
     want[rows] = vals
     assert np.isneginf(got[:, 5]).all()
     assert np.isnan(got[bs * 2:, 9]).all() and np.isposinf(got[bs:2 * bs, 7]).all()
+    assert np.isnan(got[:bs, 11]).all()
     np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6, equal_nan=True)
     assert (np.abs(got[2 * bs + 6, 20:30] - want[2 * bs + 6, 20:30]) < 1e-3).all()
 
