@@ -90,3 +90,64 @@ def test_c5_layer_sampled(cuda):
     np.add.at(want_gc, np.searchsorted(kids, cids[into]), term)
     got_gc = gchild[torch.from_numpy(kids).to(cuda)].cpu().numpy()
     np.testing.assert_allclose(got_gc, want_gc, rtol=1e-5, atol=1e-30)
+
+
+def test_c5_blocked_layer_sampled(cuda):
+    """The block-layout layer the benchmark times (8192 blocks of 32 nodes,
+    32 edges per block over 262144 element rows, batch 512, bench.py's C5
+    block layer), checked on samples against the float64 oracle: the forward
+    of 64 sampled blocks (the first and last included) over the child rows
+    they read; the backward's element flows of 200 sampled element rows,
+    whose every block edge comes from the blocks that reach them, and the
+    parameter flows of those blocks."""
+    import fuselse_amd
+
+    ext = fuselse_amd.ext
+    print("case C5 block layer 8192 blocks x 32 nodes, 32 edges, batch 512", flush=True)
+    nbk, bs, ne, nel, batch = 8192, 32, 32, 262144, 512
+    floor = float(np.float32(1e-45))
+    gen = torch.Generator(device=cuda)
+    gen.manual_seed(7)
+    em = torch.log(torch.rand(nel, batch, device=cuda, generator=gen).clamp_min_(1e-30))
+    nids = torch.arange(nbk, device=cuda, dtype=torch.int64) * bs
+    cids = torch.randint(0, nel, (nbk, ne), device=cuda, generator=gen, dtype=torch.int64)
+    pids = (torch.arange(nbk * ne, device=cuda, dtype=torch.int64) * bs).reshape(nbk, ne)
+    params = torch.rand(nbk * ne * bs, device=cuda, generator=gen) + 1e-3
+    nm = torch.empty(nbk * bs, batch, device=cuda)
+    ext.sparse_forward_float(nm, em, params, nids, cids, pids, bs)
+    c_np, p_np, par_np = cids.cpu().numpy(), pids.cpu().numpy(), params.cpu().numpy()
+    rng = np.random.default_rng(8)
+
+    def sub_blocks(blocks):
+        """The blocks' child rows (compact), their child ids into them, their
+        parent rows of `rows_of` tensors and compact node ids."""
+        uniq, inv = np.unique(c_np[blocks], return_inverse=True)
+        em_sub = em[torch.from_numpy(uniq).to(cuda)].cpu().numpy()
+        node_rows = (blocks[:, None] * bs + np.arange(bs)[None, :]).reshape(-1)
+        nids_sub = (np.arange(len(blocks)) * bs).astype(np.int64)
+        return uniq, em_sub, inv.reshape(len(blocks), ne).astype(np.int64), node_rows, nids_sub
+
+    blocks = np.unique(np.concatenate([[0, nbk - 1], rng.choice(nbk, 62, replace=False)]))
+    _, em_sub, c_sub, node_rows, nids_sub = sub_blocks(blocks)
+    rows, vals = O.sparse_blocked_fp64(em_sub, par_np, nids_sub, c_sub, p_np[blocks], bs, clamp=floor)
+    got = nm[torch.from_numpy(node_rows[rows]).to(cuda)].cpu().numpy()
+    np.testing.assert_allclose(got, vals, rtol=1e-5, atol=1e-6)
+
+    nf = torch.rand(nbk * bs, batch, device=cuda, generator=gen)
+    ef = torch.zeros(nel, batch, device=cuda)
+    pf = torch.zeros(params.numel(), device=cuda)
+    ext.sparse_blocked_backward(nf, ef, nm, em, params, pf, nids, cids, pids, bs)
+    kids = np.sort(rng.choice(np.unique(c_np), 200, replace=False))
+    reach = np.unique(np.flatnonzero(np.isin(c_np, kids).any(axis=1)))
+    uniq, em_sub, c_sub, node_rows, nids_sub = sub_blocks(reach)
+    nrows = torch.from_numpy(node_rows).to(cuda)
+    nf_sub = nf[nrows].cpu().numpy()
+    nm_sub = nm[nrows].cpu().numpy()
+    de, dp = O.sparse_blocked_bwd_fp64(nf_sub, nm_sub, em_sub, par_np, nids_sub, c_sub, p_np[reach], bs, clamp=floor)
+    # every term is positive (node_flows in [0, 1)), so 1e-5 of the sum bounds fp32 accumulation
+    at = np.searchsorted(uniq, kids)
+    got_e = ef[torch.from_numpy(kids).to(cuda)].cpu().numpy()
+    np.testing.assert_allclose(got_e, de[at], rtol=1e-5, atol=1e-30)
+    q = (p_np[reach][:, :, None] + np.arange(bs)[None, None, :]).reshape(-1)
+    got_p = pf[torch.from_numpy(q).to(cuda)].cpu().numpy()
+    np.testing.assert_allclose(got_p, dp[q], rtol=1e-5, atol=1e-30)
