@@ -83,6 +83,20 @@ __device__ __forceinline__ void ld4_raw(const float* __restrict__ row, int64_t c
         for (int u = 0; u < 4; ++u) v[u] = row[col + u < batch ? col + u : 0];
     }
 }
+// ld4_raw with the nontemporal hint when NT (rows of 16-byte vectors): for
+// rows read once, which leave nothing in the caches that a later read finds.
+template <bool VEC, bool NT>
+__device__ __forceinline__ void ld4_raw_nt(const float* __restrict__ row, int64_t col, int64_t batch, float (&v)[4]) {
+    if constexpr (VEC && NT) {
+        const f32x4 t = load_stream<f32x4>(row + (col < batch ? col : 0));
+        v[0] = t.x;
+        v[1] = t.y;
+        v[2] = t.z;
+        v[3] = t.w;
+    } else {
+        ld4_raw<VEC>(row, col, batch, v);
+    }
+}
 template <bool VEC>
 __device__ __forceinline__ void ld4_fill(int64_t col, int64_t batch, float fill, float (&v)[4]) {
 #pragma unroll
@@ -556,8 +570,12 @@ __global__ __launch_bounds__(64) void blocked_bwd_params(float* __restrict__ par
 // again with the same arithmetic and adds their one-by-one terms (the code
 // for them inside the loop cost 55 registers and half the occupancy).
 // NKP: parent K-steps (4 parents each), MP = NKP / 4 rounded up: 16-parent
-// tiles of the product over the batch.
-template <int ET, int NKP, bool VEC, bool LOGP>
+// tiles of the product over the batch.  NTP: the block's parent rows (o, g)
+// take nontemporal loads, for layers of one edge chunk, where no other wave
+// reads them again (one chunk at the bench layer: 473 -> 445 us; with two
+// chunks the hint cost 4%, the other chunk's wave missing what the caches
+// would have kept).
+template <int ET, int NKP, bool VEC, bool LOGP, bool NTP>
 __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge_flows,
                                                         float* __restrict__ param_flows,
                                                         const float* __restrict__ gf, const float* __restrict__ om,
@@ -650,8 +668,8 @@ __global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge
             for (int ks = 0; ks < NKP; ++ks) {
                 const int64_t p = 4 * ks + kq;
                 const int64_t n = nrow0 + (p < bs ? p : bs - 1);
-                ld4_raw<VEC>(om + n * batch, col, batch, ov[ks]);
-                ld4_raw<VEC>(gf + n * batch, col, batch, gv[ks]);
+                ld4_raw_nt<VEC, NTP>(om + n * batch, col, batch, ov[ks]);
+                ld4_raw_nt<VEC, NTP>(gf + n * batch, col, batch, gv[ks]);
             }
             __builtin_amdgcn_sched_barrier(0);
             tile_x_finish<ET, VEC>(ne, c0, kq, col, batch, xv, m);
@@ -1057,8 +1075,15 @@ void launch_fused(float* edge_flows, float* param_flows, const float* gf, const 
     const int64_t items = nb * chunks;
     for (int64_t id0 = 0; id0 < items; id0 += kMaxGroups) {
         const int64_t n = items - id0 < kMaxGroups ? items - id0 : kMaxGroups;
-        blocked_bwd_fused<ET, NKP, VEC, LOGP><<<dim3((unsigned)((n + 7) / 8 * 8)), dim3(64), 0, st>>>(
-            edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, ne, bs, batch, chunks, items, id0, disjoint);
+        const dim3 grid((unsigned)((n + 7) / 8 * 8));
+        if (chunks == 1)
+            blocked_bwd_fused<ET, NKP, VEC, LOGP, true><<<grid, dim3(64), 0, st>>>(
+                edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, ne, bs, batch, chunks, items, id0,
+                disjoint);
+        else
+            blocked_bwd_fused<ET, NKP, VEC, LOGP, false><<<grid, dim3(64), 0, st>>>(
+                edge_flows, param_flows, gf, om, xm, params, nids, cids, pids, ne, bs, batch, chunks, items, id0,
+                disjoint);
     }
 }
 
