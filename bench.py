@@ -204,6 +204,25 @@ def _time_calls(torch, stream, fn, nbuf, iters):
 MAX_GRAPH_CALLS = 1024
 
 
+def _time_calls_flushed(torch, stream, fn, iters, flush):
+    """Average duration (ms) of fn() with flush() (other traffic, not timed)
+    before each call: HIP events on the kernels' stream around each call
+    alone, so repeated calls on the same inputs find none of them left in
+    the Infinity Cache by the call before."""
+    for _ in range(2):
+        flush()
+        fn()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+    torch.cuda.synchronize()
+    for a, b in evs:
+        flush()
+        a.record(stream)
+        fn()
+        b.record(stream)
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in evs) / iters
+
+
 def _time_graph(torch, fn, iters, result):
     """Average per-call duration (ms) of fn(i, stream), i < iters, captured in
     one HIP graph and replayed three times; and result() after the replays."""
@@ -902,18 +921,31 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
         # and whole 1 KB row pieces per load
         gidx = cids.reshape(-1).contiguous()
         sts = stream.cuda_stream
+        # the inputs (512 MB of child rows) are twice the Infinity Cache, and
+        # calls repeated on them find up to half left there by the call
+        # before; the *flushed_us figures time each call after a read of
+        # 512 MB of other data (a read, so the cache holds clean lines that
+        # the timed call evicts without writing them back)
+        fl_src = torch.ones(128 << 20, dtype=torch.float32, device=dev)
+        flush = lambda: fl_src.sum()
 
-        def gather_us(lanes, waves):
-            call = lambda i: _lib.diag_call("fl_diag_gather_rows", em.data_ptr(), gidx.data_ptr(), x_out.data_ptr(),
-                                            gidx.numel(), batch, lanes, waves, 2, sts)
+        def gather_us(lanes, waves, flushed=False):
+            call = lambda i=0: _lib.diag_call("fl_diag_gather_rows", em.data_ptr(), gidx.data_ptr(), x_out.data_ptr(),
+                                              gidx.numel(), batch, lanes, waves, 2, sts)
+            if flushed:
+                return round(_time_calls_flushed(torch, stream, call, max(5, iters // 5), flush) * 1e3, 1)
             return round(_time_calls(torch, stream, call, 1, max(5, iters // 5)) * 1e3, 1)
 
-        ceil = {"gather_ceiling_us": gather_us(16, 4), "gather_1wave_us": gather_us(16, 1),
-                "gather_rows_1kb_us": gather_us(64, 1)}
+        ceil = {"gather_ceiling_us": gather_us(16, 4), "gather_ceiling_flushed_us": gather_us(16, 4, True),
+                "gather_1wave_us": gather_us(16, 1), "gather_rows_1kb_us": gather_us(64, 1)}
         assert torch.equal(x_out, em[gidx]), "gather copy mismatch"
         for fn, tag in [(ext.sparse_forward_float, "fp32"), (ext.sparse_forward_q16, "q16")]:
             ms = _time_calls(torch, stream, lambda i: fn(nm, em, params, nids, cids, pids, bs), 1, max(5, iters // 5))
-            extra = {"per_parent_us": round(ms_pp * 1e3, 1), **ceil} if tag == "fp32" else {}
+            extra = {}
+            if tag == "fp32":
+                fms = _time_calls_flushed(torch, stream, lambda: fn(nm, em, params, nids, cids, pids, bs),
+                                          max(5, iters // 5), flush)
+                extra = {"flushed_us": round(fms * 1e3, 1), "per_parent_us": round(ms_pp * 1e3, 1), **ceil}
             rec(f"C5_blocked_{tag}_8192x32_e32_b512", ms, fbytes, nnz=nbk * bs * ne, **extra)
         ext.sparse_csr_forward(em, x_off, x_cid, x_lp, out=x_out)
         ext.sparse_forward_float(nm, em, params, nids, cids, pids, bs)
@@ -942,9 +974,11 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
         touched = int(torch.unique(cids).numel())
         bbytes = (2 * nbk * bs * batch * 4 + nbk * ne * batch * 4 + 2 * touched * batch * 4 + 3 * nbk * ne * bs * 4
                   + nbk * ne * 16)
-        rec("C5_blocked_bwd_fp32_8192x32_e32_b512", ms, bbytes, nnz=nbk * bs * ne,
+        fms = _time_calls_flushed(torch, stream, lambda: ext.sparse_blocked_backward(
+            nf, ef, nm, em, params, pf, nids, cids, pids, bs, plan=plan), max(5, iters // 5), flush)
+        rec("C5_blocked_bwd_fp32_8192x32_e32_b512", ms, bbytes, nnz=nbk * bs * ne, flushed_us=round(fms * 1e3, 1),
             without_plan_us=round(ms_np * 1e3, 1), plan_build_ms=round(plan_ms, 2), element_rows_touched=touched)
-        del em, nm, nf, ef, pf, plan
+        del em, nm, nf, ef, pf, plan, fl_src
     return res
 
 
