@@ -341,7 +341,7 @@ __global__ __launch_bounds__(64) void blocked_bwd_edges(float* __restrict__ edge
             }
             float* orow = edge_flows + (ebase + e) * batch;
             if constexpr (VEC) {
-                if (col < batch) *reinterpret_cast<f32x4*>(orow + col) = f32x4{res[0], res[1], res[2], res[3]};
+                if (col < batch) store_stream(f32x4{res[0], res[1], res[2], res[3]}, orow + col);
             } else {
 #pragma unroll
                 for (int u = 0; u < 4; ++u)
