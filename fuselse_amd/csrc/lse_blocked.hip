@@ -61,21 +61,23 @@ __device__ __forceinline__ float weight_term(float w) {
 
 // Child values of chunk edges c0 + 4*ks + kq at the lane's four columns;
 // edges past ne read -inf (their addresses clamped to edge ne - 1), columns
-// past the batch read 0 (never stored).
-template <int NK, int NT, bool VEC>
+// past the batch read 0 (never stored).  FULL: every edge of the chunk and
+// every column of the tile is in range (a wave-uniform fact), so the values
+// are taken as loaded.
+template <int NK, int NT, bool VEC, bool FULL>
 __device__ __forceinline__ void load_chunk(float (&x)[NK][NT], const float* __restrict__ child,
                                            const int64_t* __restrict__ cids, int64_t ebase, int64_t ne, int64_t c0,
                                            int kq, int64_t col, int64_t batch) {
 #pragma unroll
     for (int ks = 0; ks < NK; ++ks) {
         const int64_t e = c0 + 4 * ks + kq;
-        const bool ev = e < ne;
+        const bool ev = FULL || e < ne;
         const float* row = child + cids[ebase + (ev ? e : ne - 1)] * batch;
 #pragma unroll
         for (int q = 0; q < NT / 4; ++q) {
             const int64_t cq = col + 64 * q;
             if constexpr (VEC) {
-                const bool cv = cq < batch;
+                const bool cv = FULL || cq < batch;
                 const f32x4 v = *reinterpret_cast<const f32x4*>(row + (cv ? cq : 0));
                 x[ks][4 * q] = ev ? (cv ? v.x : 0.0f) : -kInf;
                 x[ks][4 * q + 1] = ev ? (cv ? v.y : 0.0f) : -kInf;
@@ -84,7 +86,7 @@ __device__ __forceinline__ void load_chunk(float (&x)[NK][NT], const float* __re
             } else {
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    const bool cv = cq + t < batch;
+                    const bool cv = FULL || cq + t < batch;
                     const float v = row[cv ? cq + t : 0];
                     x[ks][4 * q + t] = ev ? (cv ? v : 0.0f) : -kInf;
                 }
@@ -95,20 +97,21 @@ __device__ __forceinline__ void load_chunk(float (&x)[NK][NT], const float* __re
 
 // Raw weights of chunk edges c0 + 4*ks + kq for parents p0 + 16*mt + jc
 // (the lane's A-layout entries); invalid entries read as -inf (log weights)
-// or 0 (linear weights), the identity of the row maximum.
-template <int MT, int NK, bool LOGP>
+// or 0 (linear weights), the identity of the row maximum.  FULL: every edge
+// and parent is in range.
+template <int MT, int NK, bool LOGP, bool FULL>
 __device__ __forceinline__ void load_weights(float (&w)[MT][NK], const float* __restrict__ params,
                                              const int64_t* __restrict__ pids, int64_t ebase, int64_t ne, int64_t bs,
                                              int64_t c0, int64_t p0, int kq, int jc) {
 #pragma unroll
     for (int ks = 0; ks < NK; ++ks) {
         const int64_t e = c0 + 4 * ks + kq;
-        const bool ev = e < ne;
+        const bool ev = FULL || e < ne;
         const int64_t q = pids[ebase + (ev ? e : ne - 1)];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
             const int64_t p = p0 + 16 * mt + jc;
-            const bool pv = p < bs;
+            const bool pv = FULL || p < bs;
             const float v = weight_term<LOGP>(params[q + (pv ? p : bs - 1)]);
             w[mt][ks] = ev && pv ? v : (LOGP ? -kInf : 0.0f);
         }
@@ -184,15 +187,15 @@ __device__ __forceinline__ void fold_chunk(f32x4 (&acc)[MT][NT], float (&wm)[MT]
 }
 
 // Loads and folds the NK K-steps of edges from c0.
-template <int MT, int NK, int NT, bool VEC, bool LOGP, bool FIRST>
+template <int MT, int NK, int NT, bool VEC, bool LOGP, bool FIRST, bool FULL = false>
 __device__ __forceinline__ void load_fold(f32x4 (&acc)[MT][NT], float (&wm)[MT], float (&m)[NT],
                                           const float* __restrict__ child, const float* __restrict__ params,
                                           const int64_t* __restrict__ cids, const int64_t* __restrict__ pids,
                                           int64_t ebase, int64_t ne, int64_t bs, int64_t c0, int64_t p0, int kq,
                                           int jc, int64_t col, int64_t batch) {
     float x[NK][NT], w[MT][NK];
-    load_chunk<NK, NT, VEC>(x, child, cids, ebase, ne, c0, kq, col, batch);
-    load_weights<MT, NK, LOGP>(w, params, pids, ebase, ne, bs, c0, p0, kq, jc);
+    load_chunk<NK, NT, VEC, FULL>(x, child, cids, ebase, ne, c0, kq, col, batch);
+    load_weights<MT, NK, LOGP, FULL>(w, params, pids, ebase, ne, bs, c0, p0, kq, jc);
     fold_chunk<MT, NK, NT, LOGP, FIRST>(acc, wm, m, x, w, kq);
 }
 
@@ -317,8 +320,15 @@ __global__ __launch_bounds__(64 * W, fwd_min_waves(MT, NK, MULTI)) void blocked_
     for (int mt = 0; mt < MT; ++mt) wm[mt] = LOGP ? -kInf : 0.0f;
 
     if constexpr (!MULTI) {
-        load_fold<MT, NK, NT, VEC, LOGP, true>(acc, wm, m, child, params, cids, pids, ebase, ne, bs, 0, p0, kq, jc,
-                                               col, batch);
+        // the masks of edges, parents and columns past their ends are all
+        // true for a whole chunk of a whole tile: that case takes a copy of
+        // the fold without them
+        if (ne == 4 * NK && p0 + 16 * MT <= bs && (ct + 1) * 16 * NT <= batch)
+            load_fold<MT, NK, NT, VEC, LOGP, true, true>(acc, wm, m, child, params, cids, pids, ebase, ne, bs, 0, p0,
+                                                         kq, jc, col, batch);
+        else
+            load_fold<MT, NK, NT, VEC, LOGP, true, false>(acc, wm, m, child, params, cids, pids, ebase, ne, bs, 0, p0,
+                                                          kq, jc, col, batch);
     } else {
         // full chunks of KCMAX edges, one at a time (a second buffer in flight
         // cost more in occupancy than it hid), then the rest in the smallest
