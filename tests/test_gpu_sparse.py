@@ -351,8 +351,11 @@ def test_blocked_backward_with_a_reused_plan(cuda):
 # ---------------------------------------------------------------------------
 F32_FLOOR = float(np.float32(1e-45))
 
+# (32, 32, 100) and (64, 32, 200): whole tiles of whole chunks (the unmasked
+# fold) and a last partial tile (the masked one) in the same launch
 PRODUCT_CASES = [(8, 5, 64), (16, 32, 130), (24, 33, 512), (32, 32, 512), (48, 7, 96), (64, 100, 260),
-                 (128, 16, 64), (32, 1, 3), (9, 70, 600), (16, 64, 1), (2, 40, 200), (5, 16, 129), (3, 9, 8)]
+                 (128, 16, 64), (32, 1, 3), (9, 70, 600), (16, 64, 1), (2, 40, 200), (5, 16, 129), (3, 9, 8),
+                 (32, 32, 100), (64, 32, 200)]
 
 
 @pytest.mark.parametrize("bs,ne,batch", PRODUCT_CASES)
