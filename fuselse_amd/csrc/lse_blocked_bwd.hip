@@ -574,9 +574,13 @@ __global__ __launch_bounds__(64) void blocked_bwd_params(float* __restrict__ par
 // take nontemporal loads, for layers of one edge chunk, where no other wave
 // reads them again (one chunk at the bench layer: 473 -> 445 us; with two
 // chunks the hint cost 4%, the other chunk's wave missing what the caches
-// would have kept).
+// would have kept).  Compiled for at least two waves per SIMD: the
+// accumulators then live in VGPRs (241 registers at 32 parents, where the
+// default allocation took 197 + 48 AGPRs; 448 -> 443 us), 16 parents run
+// three waves per SIMD instead of two, and rows that are not 16-byte vectors
+// two instead of one.
 template <int ET, int NKP, bool VEC, bool LOGP, bool NTP>
-__global__ __launch_bounds__(64) void blocked_bwd_fused(float* __restrict__ edge_flows,
+__global__ __launch_bounds__(64, 2) void blocked_bwd_fused(float* __restrict__ edge_flows,
                                                         float* __restrict__ param_flows,
                                                         const float* __restrict__ gf, const float* __restrict__ om,
                                                         const float* __restrict__ xm, const float* __restrict__ params,
