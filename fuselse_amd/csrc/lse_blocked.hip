@@ -276,9 +276,14 @@ __device__ __forceinline__ void store_tile(float* __restrict__ node_mars, const 
 
 // Waves per SIMD the register allocation must allow: four for a single chunk
 // (the accumulators then live in VGPRs, not AGPRs: 101 registers instead of
-// 86 + 44 for 32 parents, four waves instead of three), except 64 parents
-// with 32 edges, and several chunks, whose register sets would spill at four.
-constexpr int fwd_min_waves(int mt, int nk, bool multi) { return multi || (mt == 4 && nk == 8) ? 1 : 4; }
+// 86 + 44 for 32 parents, four waves instead of three) and for several chunks
+// of 32 parents (128 registers instead of 132 + 52: four waves instead of
+// two), three for several chunks of 16 parents; 64 parents with 32 edges keep
+// the default allocation (three waves; four would spill), and several chunks
+// never take 64 parents.
+constexpr int fwd_min_waves(int mt, int nk, bool multi) {
+    return mt == 4 ? (nk == 8 || multi ? 1 : 4) : multi ? (mt == 2 ? 4 : 3) : 4;
+}
 
 // One wave per (node block j, parent group g, column tile ct), W consecutive
 // column tiles per workgroup (wave w of workgroup cg takes ct = W*cg + w);
