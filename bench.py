@@ -688,9 +688,26 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
             ms = _time_calls(torch, stream, lambda i: fn(bufs[i % nb]), nb, iters)
             ms_res = _time_calls(torch, stream, lambda i: fn(bufs[0]), 1, iters)
             ref_ms = v100[tag][0]
+            extra = {}
+            if tag == "fp16":
+                # the same rows in batches of 256 and 1024: time = fixed cost +
+                # bytes / row rate, fitted through the three batch sizes
+                pts = [(b, ms)]
+                for bb in (256, 1024):
+                    nbb = nbuf_for(2 * bb * n)
+                    bb_bufs = [mk(torch.rand(bb, n, device=dev, generator=gen) * 100.0 - 100.0).contiguous()
+                               for _ in range(nbb)]
+                    pts.append((bb, _time_calls(torch, stream, lambda i: fn(bb_bufs[i % nbb]), nbb, iters)))
+                    del bb_bufs
+                xs_ = [2.0 * bb * n for bb, _ in pts]
+                ys_ = [t for _, t in pts]
+                mx, my = sum(xs_) / 3, sum(ys_) / 3
+                slope = sum((x_ - mx) * (y_ - my) for x_, y_ in zip(xs_, ys_)) / sum((x_ - mx) ** 2 for x_ in xs_)
+                extra = {"rows_us": {str(bb): round(t * 1e3, 2) for bb, t in sorted(pts)},
+                         "fixed_us": round((my - slope * mx) * 1e3, 2), "row_rate_gbps": round(1e-6 / slope, 1)}
             rec(f"published_{tag}_fwd_512x128256", ms, nbytes, resident_us=round(ms_res * 1e3, 2),
                 read_ceiling_us=read_ceiling_us(bufs),
-                v100_ms=ref_ms, v100_pct_peak=round(100 * nbytes / (ref_ms * 1e-3) / 900e9, 1))
+                v100_ms=ref_ms, v100_pct_peak=round(100 * nbytes / (ref_ms * 1e-3) / 900e9, 1), **extra)
             del bufs
     if want("ramp"):
         # Fixed cost against streaming rate: the read ceiling kernel and the
