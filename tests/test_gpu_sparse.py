@@ -385,14 +385,17 @@ def test_blocked_product_form_matches_fp64(cuda, bs, ne, batch, log_params):
     assert (got[untouched] == 7.0).all()
 
 
-def test_blocked_product_form_special_values_and_fallback(cuda):
+@pytest.mark.parametrize("ne,bs,batch", [(40, 16, 68), (32, 32, 128)])
+def test_blocked_product_form_special_values_and_fallback(cuda, ne, bs, batch):
     """Entries the product cannot resolve take the exact fold: -inf children,
     columns of -inf, +inf and NaN children (a NaN among -inf children of the
     first 32-edge chunk included), zero weights, a parent whose only large
-    weights meet children ~200 nats below the column maximum."""
-    print("case blocked product special values", flush=True)
+    weights meet children ~200 nats below the column maximum.  40 edges run
+    the multi-chunk kernel; 32 edges of 32 parents over whole tiles the
+    unmasked fold, whose stores flag the fallback through a running maximum."""
+    print(f"case blocked product special values ne={ne} bs={bs} batch={batch}", flush=True)
     rng = np.random.default_rng(5)
-    nb, ne, bs, batch, nelem = 3, 40, 16, 68, 60
+    nb, nelem = 3, 60
     nids = (np.arange(nb) * bs).astype(np.int64)
     cids = np.stack([rng.permutation(nelem)[:ne] for _ in range(nb)]).astype(np.int64)
     pids = (np.arange(nb * ne, dtype=np.int64) * bs).reshape(nb, ne)
