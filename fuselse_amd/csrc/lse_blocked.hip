@@ -214,7 +214,7 @@ __device__ __forceinline__ bool unresolved(float s, uint32_t lo, uint32_t span) 
 // cannot resolve (rare: see the accuracy note above) are only flagged in the
 // store loop; a lane with any recomputes them by the exact online log-sum-exp
 // over the block's edges and stores them over the product's value.
-template <int MT, int NT, bool VEC, bool LOGP, bool FULL = false>
+template <int MT, int NT, bool VEC, bool LOGP>
 __device__ __forceinline__ void store_tile(float* __restrict__ node_mars, const float* __restrict__ child,
                                            const float* __restrict__ params, const int64_t* __restrict__ cids,
                                            const int64_t* __restrict__ pids, int64_t ebase, int64_t ne, int64_t bs,
@@ -227,44 +227,6 @@ __device__ __forceinline__ void store_tile(float* __restrict__ node_mars, const 
     static_assert(MT * 4 * NT <= 64, "one bit per held entry");
     using Mask = typename std::conditional<MT * 4 * NT <= 32, uint32_t, uint64_t>::type;
     Mask redo = 0;  // bit (4*mt + r)*NT + t: entry left to the exact fold
-    if constexpr (FULL) {
-        // every parent and column of the tile is in range: the loop keeps only
-        // the largest distance of an entry's bits from [thr, 2^100]'s lower
-        // end, and the rare tile with one past the span sets its bits after
-        uint32_t dmax = 0;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float lwr = lane_read(lwm[mt], 4 * kq + r);
-                float* orow = node_mars + (nrow0 + p0 + 16 * mt + 4 * kq + r) * batch;
-#pragma unroll
-                for (int q = 0; q < NT / 4; ++q) {
-                    float res[4];
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        const float s = acc[mt][4 * q + u][r];
-                        res[u] = lwr + m[4 * q + u] + flog2(s) * kLn2;
-                        const uint32_t d = __builtin_bit_cast(uint32_t, s) - lo;
-                        dmax = d > dmax ? d : dmax;
-                    }
-                    if constexpr (VEC)
-                        store_stream(f32x4{res[0], res[1], res[2], res[3]}, orow + col + 64 * q);
-                    else
-#pragma unroll
-                        for (int u = 0; u < 4; ++u) orow[col + 64 * q + u] = res[u];
-                }
-            }
-        if (dmax > span) {
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-#pragma unroll
-                    for (int t = 0; t < NT; ++t)
-                        redo |= unresolved(acc[mt][t][r], lo, span) ? (Mask)1 << ((4 * mt + r) * NT + t) : (Mask)0;
-        }
-    } else {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -293,7 +255,6 @@ __device__ __forceinline__ void store_tile(float* __restrict__ node_mars, const 
                 }
             }
         }
-    }
     while (redo) {
         const int bit = __builtin_ctzll((uint64_t)redo);
         redo &= redo - 1;
@@ -367,18 +328,12 @@ __global__ __launch_bounds__(64 * W, fwd_min_waves(MT, NK, MULTI)) void blocked_
         // the masks of edges, parents and columns past their ends are all
         // true for a whole chunk of a whole tile: that case takes a copy of
         // the fold without them
-        if (ne == 4 * NK && p0 + 16 * MT <= bs && (ct + 1) * 16 * NT <= batch) {
+        if (ne == 4 * NK && p0 + 16 * MT <= bs && (ct + 1) * 16 * NT <= batch)
             load_fold<MT, NK, NT, VEC, LOGP, true, true>(acc, wm, m, child, params, cids, pids, ebase, ne, bs, 0, p0,
                                                          kq, jc, col, batch);
-            float lwm[MT];
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) lwm[mt] = LOGP ? wm[mt] : logf(wm[mt]);
-            store_tile<MT, NT, VEC, LOGP, true>(node_mars, child, params, cids, pids, ebase, ne, bs, batch, nids[j],
-                                                p0, kq, col, acc, lwm, m);
-            return;
-        }
-        load_fold<MT, NK, NT, VEC, LOGP, true, false>(acc, wm, m, child, params, cids, pids, ebase, ne, bs, 0, p0, kq,
-                                                      jc, col, batch);
+        else
+            load_fold<MT, NK, NT, VEC, LOGP, true, false>(acc, wm, m, child, params, cids, pids, ebase, ne, bs, 0, p0,
+                                                          kq, jc, col, batch);
     } else {
         // full chunks of KCMAX edges, one at a time (a second buffer in flight
         // cost more in occupancy than it hid), then the rest in the smallest

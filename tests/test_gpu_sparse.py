@@ -392,7 +392,7 @@ def test_blocked_product_form_special_values_and_fallback(cuda, ne, bs, batch):
     first 32-edge chunk included), zero weights, a parent whose only large
     weights meet children ~200 nats below the column maximum.  40 edges run
     the multi-chunk kernel; 32 edges of 32 parents over whole tiles the
-    unmasked fold, whose stores flag the fallback through a running maximum."""
+    unmasked fold."""
     print(f"case blocked product special values ne={ne} bs={bs} batch={batch}", flush=True)
     rng = np.random.default_rng(5)
     nb, nelem = 3, 60
