@@ -993,8 +993,23 @@ def measure_configs(torch, ext, dev, stream, iters=50, only=None):
                   + nbk * ne * 16)
         fms = _time_calls_flushed(torch, stream, lambda: ext.sparse_blocked_backward(
             nf, ef, nm, em, params, pf, nids, cids, pids, bs, plan=plan), max(5, iters // 5), flush)
+        # the single pass's memory traffic alone (fl_diag_blocked_bwd_pattern:
+        # its loads and edge-flow stores with one product and sum per column),
+        # at its geometry (one wave per block, 18 KB of LDS per wave) and with
+        # four waves of a block taking interleaved column tiles
+        pat_out = torch.empty(nbk * ne, batch, device=dev)
+
+        def pattern_us(waves):
+            call = lambda i=0: _lib.diag_call("fl_diag_blocked_bwd_pattern", pat_out.data_ptr(), nf.data_ptr(),
+                                              nm.data_ptr(), em.data_ptr(), nids.data_ptr(), cids.data_ptr(), nbk,
+                                              batch, waves, 18432, sts)
+            return round(_time_calls(torch, stream, call, 1, max(5, iters // 5)) * 1e3, 1)
+
+        pattern = {"single_pass_pattern_us": pattern_us(1), "single_pass_pattern_w4_us": pattern_us(4)}
+        del pat_out
         rec("C5_blocked_bwd_fp32_8192x32_e32_b512", ms, bbytes, nnz=nbk * bs * ne, flushed_us=round(fms * 1e3, 1),
-            without_plan_us=round(ms_np * 1e3, 1), plan_build_ms=round(plan_ms, 2), element_rows_touched=touched)
+            without_plan_us=round(ms_np * 1e3, 1), plan_build_ms=round(plan_ms, 2), element_rows_touched=touched,
+            **pattern)
         del em, nm, nf, ef, pf, plan, fl_src
     return res
 

@@ -64,6 +64,7 @@ DIAG_SIGNATURES = {
     "fl_diag_half_rows_cap": (_int, [_int, _vp, _vp, _i64, _i64, _int, _vp]),
     "fl_diag_lane_pairs": (_int, [_vp, _vp, _vp]),
     "fl_diag_gather_rows": (_int, [_vp, _vp, _vp, _i64, _i64, _int, _int, _int, _vp]),
+    "fl_diag_blocked_bwd_pattern": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _int, _int, _vp]),
 }
 
 _lib = None

@@ -607,3 +607,79 @@ extern "C" int fl_diag_gather_rows(const float* src, const int64_t* idx, float* 
     }
     return launch_status(name);
 }
+
+namespace {
+// The memory pattern of the block-layout backward's single pass at 32
+// parents and 32 edges (one edge chunk), with its arithmetic reduced to one
+// product and sum per column: wave w of a workgroup (one workgroup per node
+// block j) takes the 64-column tiles w, w + W, ...; per tile, lane
+// (kq = l / 16, jc = l % 16) loads columns b0 + 4 jc .. + 3 of the gathered
+// child rows cids[j, 16 et + 4 kq + r] (et < 2, r < 4) with plain loads and
+// of the parent rows nids[j] + 4 ks + kq (ks < 8) of o and g with the
+// nontemporal hint, all issued before the first use, and stores with the
+// nontemporal hint
+//   F[32 j + e, b] = x[cids[j, e], b] + sum_ks o[n, b] g[n, b],
+//   n = nids[j] + 4 ks + (e / 4) % 4,
+// the single pass's loads and edge-flow stores in the same order.  Dynamic
+// LDS (lds_per_wave bytes per wave) sets the occupancy the single pass has.
+template <int W>
+__global__ __launch_bounds__(64 * W) void bwd_pattern_kernel(float* __restrict__ F, const float* __restrict__ g,
+                                                             const float* __restrict__ o, const float* __restrict__ x,
+                                                             const int64_t* __restrict__ nids,
+                                                             const int64_t* __restrict__ cids, int64_t batch,
+                                                             int64_t block0) {
+    const int64_t j = block0 + blockIdx.x;
+    const int w = threadIdx.x >> 6;
+    const int l = lane_id(), kq = l >> 4, jc = l & 15;
+    const int64_t nrow0 = nids[j];
+    int64_t xr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xr[i] = cids[j * 32 + 16 * (i >> 2) + 4 * kq + (i & 3)];
+    for (int64_t b0 = 64 * w; b0 < batch; b0 += 64 * W) {
+        const int64_t col = b0 + 4 * jc;
+        f32x4 xv[8], ov[8], gv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xv[i] = *reinterpret_cast<const f32x4*>(x + xr[i] * batch + col);
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            const int64_t n = nrow0 + 4 * ks + kq;
+            ov[ks] = load_stream<f32x4>(o + n * batch + col);
+            gv[ks] = load_stream<f32x4>(g + n * batch + col);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        f32x4 sum = ov[0] * gv[0];
+#pragma unroll
+        for (int ks = 1; ks < 8; ++ks) sum += ov[ks] * gv[ks];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            store_stream(xv[i] + sum, F + (j * 32 + 16 * (i >> 2) + 4 * kq + (i & 3)) * batch + col);
+    }
+}
+}  // namespace
+
+extern "C" int fl_diag_blocked_bwd_pattern(float* F, const float* g, const float* o, const float* x,
+                                           const int64_t* nids, const int64_t* cids, int64_t nblocks,
+                                           int64_t batch, int waves, int lds_per_wave, void* stream) {
+    const char* name = "fl_diag_blocked_bwd_pattern";
+    FL_CHECK(nblocks >= 0 && batch >= 0, "%s: negative size", name);
+    if (nblocks == 0 || batch == 0) return ok();
+    FL_CHECK(F && g && o && x && nids && cids, "%s: NULL pointer argument", name);
+    FL_CHECK(batch % 64 == 0 && ((reinterpret_cast<uintptr_t>(F) | reinterpret_cast<uintptr_t>(g) |
+                                  reinterpret_cast<uintptr_t>(o) | reinterpret_cast<uintptr_t>(x)) & 15) == 0,
+             "%s: batch must be a multiple of 64 and the buffers 16-byte aligned", name);
+    FL_CHECK(waves == 1 || waves == 2 || waves == 4, "%s: waves must be 1, 2 or 4", name);
+    FL_CHECK(lds_per_wave >= 0 && lds_per_wave <= 40960, "%s: lds_per_wave must be in [0, 40960]", name);
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const size_t lds = (size_t)lds_per_wave * waves;
+    constexpr int64_t kMax = max_grid_blocks(256);
+    for (int64_t b0 = 0; b0 < nblocks; b0 += kMax) {
+        const unsigned n = (unsigned)(nblocks - b0 < kMax ? nblocks - b0 : kMax);
+        if (waves == 1)
+            bwd_pattern_kernel<1><<<dim3(n), dim3(64), lds, st>>>(F, g, o, x, nids, cids, batch, b0);
+        else if (waves == 2)
+            bwd_pattern_kernel<2><<<dim3(n), dim3(128), lds, st>>>(F, g, o, x, nids, cids, batch, b0);
+        else
+            bwd_pattern_kernel<4><<<dim3(n), dim3(256), lds, st>>>(F, g, o, x, nids, cids, batch, b0);
+    }
+    return launch_status(name);
+}

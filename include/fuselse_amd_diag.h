@@ -125,6 +125,24 @@ int fl_diag_lane_pairs(const float* v, float* out, void* stream);
 int fl_diag_gather_rows(const float* src, const int64_t* idx, float* dst, int64_t nrows, int64_t batch,
                         int lanes_per_row, int waves, int policy, void* stream);
 
+/* The memory pattern of fl_sparse_blocked_bwd's single pass for blocks of 32
+ * parents and 32 edges, with one product and sum per column in place of its
+ * arithmetic: F [nblocks * 32, batch] gets
+ *   F[32 j + e, b] = x[cids[j, e], b] + sum_{ks < 8} o[n, b] * g[n, b],
+ *   n = nids[j] + 4 ks + (e / 4) % 4,
+ * from the same loads (child rows gathered by id, 256 bytes of each per
+ * 64-column tile; the block's o and g rows with the nontemporal hint) and the
+ * same edge-flow stores as the single pass, in its order.  One workgroup per
+ * node block, `waves` (1, 2 or 4) waves taking interleaved column tiles;
+ * lds_per_wave bytes of dynamic LDS per wave (the single pass holds 18432)
+ * give it the single pass's occupancy.  batch % 64 == 0, 16-byte aligned
+ * buffers; cids int64 [nblocks, 32], valid rows of x; nids valid row starts
+ * of 32 rows in o and g.  Its time at a layer is the cost of the single
+ * pass's memory traffic alone. */
+int fl_diag_blocked_bwd_pattern(float* F, const float* g, const float* o, const float* x, const int64_t* nids,
+                                const int64_t* cids, int64_t nblocks, int64_t batch, int waves, int lds_per_wave,
+                                void* stream);
+
 #ifdef __cplusplus
 }
 #endif

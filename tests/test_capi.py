@@ -92,6 +92,15 @@ def test_invalid_arguments_rejected_without_launch():
     assert b"waves" in lib.fl_last_error()
     assert diag.fl_diag_gather_rows(vp, vp, vp, 4, 8, 16, 1, 3, None) == 1
     assert b"policy" in lib.fl_last_error()
+    assert diag.fl_diag_blocked_bwd_pattern(None, None, None, None, None, None, 2, 64, 1, 0, None) == 1
+    assert b"NULL" in lib.fl_last_error()
+    assert diag.fl_diag_blocked_bwd_pattern(vp, vp, vp, vp, vp, vp, 2, 100, 1, 0, None) == 1
+    assert b"multiple of 64" in lib.fl_last_error()
+    assert diag.fl_diag_blocked_bwd_pattern(vp, vp, vp, vp, vp, vp, 2, 64, 3, 0, None) == 1
+    assert b"waves" in lib.fl_last_error()
+    assert diag.fl_diag_blocked_bwd_pattern(vp, vp, vp, vp, vp, vp, 2, 64, 4, 40961, None) == 1
+    assert b"lds_per_wave" in lib.fl_last_error()
+    assert diag.fl_diag_blocked_bwd_pattern(None, None, None, None, None, None, 0, 64, 1, 0, None) == 0
     # B == 0 is a no-op success
     assert lib.fl_lse_fwd_f32_noalloc(None, None, 0, 4, 1, None) == 0
     assert lib.fl_lse_fwd_f32(None, None, 0, 4, 1, None) == 0

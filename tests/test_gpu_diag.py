@@ -218,3 +218,34 @@ def test_gather_rows_copies(cuda, lib, nrows, batch, lanes, waves, policy):
     torch.cuda.synchronize()
     assert torch.equal(dst[:nrows], src[idx])
     assert bool((dst[nrows] == 5.0).all())
+
+
+@pytest.mark.parametrize("waves,lds", [(1, 18432), (2, 0), (4, 18432)])
+@pytest.mark.parametrize("nblocks,batch", [(5, 64), (12, 512), (3, 192)])
+def test_blocked_bwd_pattern(cuda, lib, nblocks, batch, waves, lds):
+    """The single pass's memory pattern writes, for every block edge and
+    column, its child row plus the sum over the lane's eight parents of o * g
+    (parents 4 ks + (e / 4) % 4), and nothing past the block's rows, at every
+    workgroup size and with idle waves (batch 64 at four waves)."""
+    print(f"case diag blocked_bwd_pattern {nblocks}x{batch} waves {waves} lds {lds}", flush=True)
+    g = torch.Generator(device=cuda)
+    g.manual_seed(11)
+    nel = 70
+    x = torch.randn(nel, batch, device=cuda, generator=g)
+    o = torch.randn(nblocks * 32 + 8, batch, device=cuda, generator=g)
+    gg = torch.randn(nblocks * 32 + 8, batch, device=cuda, generator=g)
+    nids = torch.arange(nblocks, device=cuda, dtype=torch.int64) * 32 + 3
+    cids = torch.randint(0, nel, (nblocks, 32), device=cuda, generator=g, dtype=torch.int64)
+    F = torch.full((nblocks * 32 + 1, batch), 7.0, device=cuda)
+    st = torch.cuda.current_stream().cuda_stream
+    assert lib.fl_diag_blocked_bwd_pattern(F.data_ptr(), gg.data_ptr(), o.data_ptr(), x.data_ptr(), nids.data_ptr(),
+                                           cids.data_ptr(), nblocks, batch, waves, lds, st) == 0
+    torch.cuda.synchronize()
+    want = torch.empty(nblocks * 32, batch, device=cuda)
+    for j in range(nblocks):
+        for e in range(32):
+            rows = int(nids[j]) + 4 * torch.arange(8, device=cuda) + (e // 4) % 4
+            want[32 * j + e] = x[cids[j, e]] + (o[rows] * gg[rows]).sum(0)
+    torch.testing.assert_close(F[:-1], want, rtol=1e-5, atol=1e-5)
+    assert bool((F[-1] == 7.0).all())
+
