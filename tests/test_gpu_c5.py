@@ -151,3 +151,46 @@ def test_c5_blocked_layer_sampled(cuda):
     q = (p_np[reach][:, :, None] + np.arange(bs)[None, None, :]).reshape(-1)
     got_p = pf[torch.from_numpy(q).to(cuda)].cpu().numpy()
     np.testing.assert_allclose(got_p, dp[q], rtol=1e-5, atol=1e-30)
+
+
+def test_c5_blocked_layer_whole_against_expansion(cuda):
+    """Every output of the block-layout layer the benchmark times against an
+    independent GPU computation of the same layer: the layer expanded to one
+    CSR node per parent (node j*32 + p with the block's 32 edges and the
+    log-weights log(params[pids[j, e] + p])), run through the per-parent CSR
+    forward and flows kernels, which the oracle pins on their own.  The
+    product form's forward, element flows and parameter flows must agree
+    with them on all 262144 nodes, 262144 element rows and 8.4M edges at
+    1e-5 relative (every term of the flows is positive: node_flows in
+    [0, 1))."""
+    import fuselse_amd
+
+    ext = fuselse_amd.ext
+    print("case C5 block layer whole against its CSR expansion", flush=True)
+    nbk, bs, ne, nel, batch = 8192, 32, 32, 262144, 512
+    gen = torch.Generator(device=cuda)
+    gen.manual_seed(9)
+    em = torch.log(torch.rand(nel, batch, device=cuda, generator=gen).clamp_min_(1e-30))
+    nids = torch.arange(nbk, device=cuda, dtype=torch.int64) * bs
+    cids = torch.randint(0, nel, (nbk, ne), device=cuda, generator=gen, dtype=torch.int64)
+    pids = (torch.arange(nbk * ne, device=cuda, dtype=torch.int64) * bs).reshape(nbk, ne)
+    params = torch.rand(nbk * ne * bs, device=cuda, generator=gen) + 1e-3
+    pos = torch.arange(bs, device=cuda)
+    qidx = (pids[:, None, :] + pos[None, :, None]).reshape(-1)  # CSR edge (j*bs + p)*ne + e
+    x_cid = cids[:, None, :].expand(nbk, bs, ne).reshape(-1).to(torch.int32).contiguous()
+    x_lp = torch.log(params[qidx]).contiguous()
+    x_off = torch.arange(0, nbk * bs * ne + 1, ne, device=cuda, dtype=torch.int64)
+
+    nm = torch.empty(nbk * bs, batch, device=cuda)
+    ext.sparse_forward_float(nm, em, params, nids, cids, pids, bs)
+    want = ext.sparse_csr_forward(em, x_off, x_cid, x_lp)
+    torch.testing.assert_close(nm, want, rtol=1e-5, atol=1e-5)
+    del want
+
+    nf = torch.rand(nbk * bs, batch, device=cuda, generator=gen)
+    ef = torch.zeros(nel, batch, device=cuda)
+    pf = torch.zeros(params.numel(), device=cuda)
+    ext.sparse_blocked_backward(nf, ef, nm, em, params, pf, nids, cids, pids, bs)
+    g_child, g_lp = ext.sparse_csr_backward(em, nm, nf, x_off, x_cid, x_lp)
+    torch.testing.assert_close(ef, g_child, rtol=1e-5, atol=1e-30)
+    torch.testing.assert_close(pf[qidx], g_lp, rtol=1e-5, atol=1e-30)
